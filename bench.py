@@ -1,0 +1,333 @@
+"""Benchmark of the MI355X depthwise Conv1D hot path (one JSON line).
+
+Metric: "FWD+dX+dK ms & HBM GB/s (% peak), B16384 H128 L48
+K48 fp32, 1 GPU". A step is one pass of the hot path over one batch:
+FWD, dX and dK (atomic, zero-init outside the dK event as in the reference's
+protocol, README.md:136-140). Inputs are synthetic, drawn on a CPU
+torch.Generator in the order x, w, dY (x, dY ~ N(0,1), w ~ N(0,1/K)) and
+copied to HBM before timing.
+
+    python bench.py [--gpus 1] [--steps 100] [--warmup 20] [--no-cpu-baseline]
+
+``value`` = mean FWD + mean dX + mean dK kernel ms over the K timed steps
+(HIP events on the launch stream; the reference sums separately timed path
+means, kernels/warp_tiled_ampere.py:1059-1096). ``ms_per_step`` is the wall
+time of the K steps / K between two device synchronisations.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "FWD+dX+dK ms & HBM GB/s (% peak), B16384 H128 L48 K48 fp32, 1 GPU"
+WORKLOADS = {
+    # the metric's workload.
+    "primary": (16384, 128, 48, 48),
+    # parity cases, benchmarked only on request.
+    "short": (32768, 256, 48, 4),
+    "odd_k": (16384, 128, 48, 47),
+    "edge": (1000, 96, 37, 48),
+}
+PEAK_HBM_GBPS = 8000.0
+# Published aggregate of the reference for this metric (README.md:96,
+# A100 PCIe 40 GB): 11.283 ms.
+REFERENCE_AGGREGATE_MS = 11.283
+POLICY = ROOT / "pathtile_amd" / "tune" / "frozen_policy.json"
+PROFILES = ROOT / "profiles"
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--workload", choices=sorted(WORKLOADS), default="primary")
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-runs", type=int, default=5)
+    return p.parse_args(argv)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def frozen_config() -> dict:
+    from pathtile_amd import runtime
+
+    cfg = {
+        "fwd_waves_per_block": runtime.DEFAULT_WAVES_PER_BLOCK,
+        "dx_waves_per_block": runtime.DEFAULT_DX_WAVES_PER_BLOCK,
+        "dk_threads_per_block": runtime.DEFAULT_BWDK_BLOCK,
+        "source": "runtime defaults",
+    }
+    if POLICY.exists():
+        pol = json.loads(POLICY.read_text())
+        sel = pol.get("selected", {})
+        cfg.update({k: int(sel[k]) for k in ("fwd_waves_per_block", "dx_waves_per_block",
+                                              "dk_threads_per_block") if k in sel})
+        cfg["source"] = str(POLICY.relative_to(ROOT))
+    return cfg
+
+
+def make_inputs(B, H, L, K, seed):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, H, L, generator=g, dtype=torch.float32)
+    w = torch.randn(H, K, generator=g, dtype=torch.float32) / math.sqrt(K)
+    dy = torch.randn(B, H, L, generator=g, dtype=torch.float32)
+    return x, w, dy
+
+
+def correctness_gate(rt, x, w, dy, rows: int = 512) -> dict:
+    """Refuse to time a wrong kernel (benchmark/benchmark_dk_fairness.py:149-170):
+    compare the HIP paths with PyTorch's own conv1d/autograd on the GPU for the
+    first `rows` batch entries."""
+    import torch
+    import torch.nn.functional as F
+
+    B, H, L = x.shape
+    K = w.shape[1]
+    xs, dys = x[:rows].contiguous(), dy[:rows].contiguous()
+    y = torch.empty_like(xs)
+    dx = torch.empty_like(xs)
+    gk = torch.empty(H, K, device=x.device)
+    rt.launch_fwd(xs, w, y)
+    rt.launch_bwd_input(dys, w, dx)
+    rt.launch_bwd_weight(dys, xs, gk, K, zero_first=True)
+    xr = xs.double().requires_grad_(True)
+    wr = w.double().requires_grad_(True)
+    left = K // 2
+    yr = F.conv1d(F.pad(xr, (left, K - 1 - left)), wr.unsqueeze(1), groups=H)
+    gx_r, gk_r = torch.autograd.grad(yr, (xr, wr), dys.double())
+
+    def err(a, b):
+        return float((a.double() - b).abs().max() / b.abs().max().clamp_min(1e-12))
+
+    e = {"fwd": err(y, yr.detach()), "dx": err(dx, gx_r), "dk": err(gk, gk_r)}
+    ok = e["fwd"] < 1e-5 and e["dx"] < 1e-5 and e["dk"] < 1e-4
+    if not ok:
+        raise SystemExit(f"correctness gate failed: {e}")
+    return e
+
+
+def mean(v):
+    return sum(v) / len(v) if v else float("nan")
+
+
+def read_traffic(kernel_tag: str) -> dict | None:
+    """HBM bytes per launch of `kernel_tag` from the committed rocprofv3 PMC
+    summary (profiles/pmc_traffic_<kernel_tag>.md, lines
+    'FETCH_BYTES_PER_LAUNCH: <n>' and 'WRITE_BYTES_PER_LAUNCH: <n>')."""
+    f = PROFILES / f"pmc_traffic_{kernel_tag}.md"
+    if not f.exists():
+        return None
+    text = f.read_text()
+    m1 = re.search(r"FETCH_BYTES_PER_LAUNCH:\s*([0-9.eE+]+)", text)
+    m2 = re.search(r"WRITE_BYTES_PER_LAUNCH:\s*([0-9.eE+]+)", text)
+    if not (m1 and m2):
+        return None
+    return {"fetch": float(m1.group(1)), "write": float(m2.group(1))}
+
+
+def cpu_baseline(x, w, dy, runs: int) -> dict:
+    """PyTorch CPU with the reference's PyTorch timing boundaries
+    (benchmark/benchmark_shape_sweep_ampere.py:349-407): FWD = F.pad +
+    F.conv1d(groups=H); dX = autograd.grad(y, x); dK = autograd.grad(y, w);
+    graph construction outside the timer."""
+    import torch
+
+    import oracle  # CPU restatement of the reference's PyTorch boundary
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        cores = os.cpu_count() or 1
+    threads = max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
+    torch.set_num_threads(threads)
+    f = oracle.pytorch_depthwise_same
+    out = {}
+    t_all = time.perf_counter()
+    for phase in ("fwd", "dx", "dk"):
+        ts = []
+        for r in range(runs + 1):
+            if phase == "fwd":
+                t0 = time.perf_counter()
+                f(x, w)
+                t1 = time.perf_counter()
+            elif phase == "dx":
+                xr = x.detach().requires_grad_(True)
+                y = f(xr, w)
+                t0 = time.perf_counter()
+                torch.autograd.grad(y, xr, dy)
+                t1 = time.perf_counter()
+            else:
+                wr = w.detach().requires_grad_(True)
+                y = f(x, wr)
+                t0 = time.perf_counter()
+                torch.autograd.grad(y, wr, dy)
+                t1 = time.perf_counter()
+            if r > 0:  # first run is the warm-up
+                ts.append((t1 - t0) * 1e3)
+        out[phase] = mean(ts)
+        log(f"cpu {phase}: {out[phase]:.1f} ms")
+    total = out["fwd"] + out["dx"] + out["dk"]
+    try:
+        cpu_model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo")
+                         if l.startswith("model name"))
+    except Exception:
+        cpu_model = "unknown"
+    B, H, L = x.shape
+    return {
+        "value": round(total, 3),
+        "unit": "ms",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"full workload B={B} H={H} L={L} K={w.shape[1]}, PyTorch {torch.__version__} "
+                   f"CPU F.pad+F.conv1d(groups=H) / autograd.grad (reference PyTorch boundary), "
+                   f"1 warm-up + {runs} timed runs per path, {threads} threads on {cpu_model}"),
+        "paths_ms": {k: round(v, 3) for k, v in out.items()},
+        "wall_s": round(time.perf_counter() - t_all, 1),
+    }
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (--gpus {args.gpus} requested): the "
+              "path is a single-GPU kernel; see DESIGN.md for how it would shard.",
+              file=sys.stderr, flush=True)
+        return 2
+    import torch
+
+    from pathtile_amd import runtime
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    B, H, L, K = WORKLOADS[args.workload]
+    cfg = frozen_config()
+    rt = runtime.HipWarpRuntime(waves_per_block=cfg["fwd_waves_per_block"],
+                                dx_waves_per_block=cfg["dx_waves_per_block"],
+                                bwdk_block=cfg["dk_threads_per_block"])
+    log(f"workload B={B} H={H} L={L} K={K} config={cfg}")
+    x_cpu, w_cpu, dy_cpu = make_inputs(B, H, L, K, args.seed)
+    x, w, dy = x_cpu.to(dev), w_cpu.to(dev), dy_cpu.to(dev)
+    y = torch.empty_like(x)
+    dx = torch.empty_like(x)
+    gk = torch.zeros(H, K, device=dev)
+    gate = correctness_gate(rt, x, w, dy)
+    log(f"correctness gate vs torch (first 512 rows): {gate}")
+
+    def step(coll=None):
+        rt.launch_fwd(x, w, y, coll)
+        rt.launch_bwd_input(dy, w, dx, coll)
+        gk.zero_()
+        rt.launch_bwd_weight(dy, x, gk, K, coll)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    coll = runtime.KernelEventCollector()
+    coll.enabled = True
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(coll)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    rows = coll.rows(synchronize=True)
+    per = {ph: [r["runtime_ms"] for r in rows if r["phase"] == ph]
+           for ph in ("fwd", "bwd_input", "bwd_weight")}
+    assert all(len(v) == args.steps for v in per.values())
+
+    # dK including the zero-init (one call: fill kernel + atomic kernel) and
+    # the deterministic two-pass dK, timed the same way after the steps.
+    extra = runtime.KernelEventCollector()
+    extra.enabled = True
+    for _ in range(args.warmup):
+        rt.launch_bwd_weight(dy, x, gk, K, zero_first=True)
+        rt.launch_bwd_weight_deterministic(dy, x, gk, K)
+    torch.cuda.synchronize()
+    for _ in range(args.steps):
+        rt.launch_bwd_weight(dy, x, gk, K, extra, zero_first=True)
+    for _ in range(args.steps):
+        rt.launch_bwd_weight_deterministic(dy, x, gk, K, extra)
+    erows = extra.rows(synchronize=True)
+    per["bwd_weight_zero"] = [r["runtime_ms"] for r in erows if r["phase"] == "bwd_weight_zero"]
+    per["bwd_weight_det"] = [r["runtime_ms"] for r in erows if r["phase"] == "bwd_weight_det"]
+
+    nbytes = runtime.minimum_algorithmic_bytes(B, H, L, K)
+    paths = {}
+    for ph, v in per.items():
+        ms = mean(v)
+        gbps = runtime.algorithmic_bandwidth_gbps(nbytes, ms)
+        paths[ph] = {"ms": round(ms, 5), "min_ms": round(min(v), 5),
+                     "gbps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_HBM_GBPS, 2)}
+    agg = paths["fwd"]["ms"] + paths["bwd_input"]["ms"] + paths["bwd_weight"]["ms"]
+    dominant = max(("fwd", "bwd_input", "bwd_weight"), key=lambda k: paths[k]["ms"])
+    tag = {"fwd": "fwd", "bwd_input": "dx", "bwd_weight": "dk"}[dominant]
+    ach = paths[dominant]["gbps"]
+    traffic = read_traffic(f"{tag}_{args.workload}")
+    line = {
+        "metric": METRIC,
+        "value": round(agg, 5),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms / args.steps, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": round(agg / REFERENCE_AGGREGATE_MS, 5),
+        "vs_baseline_ref": "reference aggregate 11.283 ms on A100 PCIe (README.md:96); value/ref, lower is better",
+        "dtype": "f32",
+        "data": "synthetic (CPU torch.Generator: x, w, dY; x,dY~N(0,1), w~N(0,1/K))",
+        "config": {
+            "workload": f"B{B} H{H} L{L} K{K} fp32 ({args.workload}; BASELINE.json configs[1])"
+            if args.workload == "primary" else f"B{B} H{H} L{L} K{K} fp32 ({args.workload})",
+            "B": B, "H": H, "L": L, "K": K,
+            "fwd_waves_per_block": cfg["fwd_waves_per_block"],
+            "dx_waves_per_block": cfg["dx_waves_per_block"],
+            "dk_threads_per_block": cfg["dk_threads_per_block"],
+            "launch_config_source": cfg["source"],
+        },
+        "aggregate_gbps": round(3 * nbytes / (agg / 1e3) / 1e9, 1),
+        "aggregate_pct_peak": round(100 * 3 * nbytes / (agg / 1e3) / 1e9 / PEAK_HBM_GBPS, 2),
+        "algorithmic_bytes_per_path": nbytes,
+        "paths": paths,
+        "correctness_gate": {k: float(f"{v:.3e}") for k, v in gate.items()},
+        "roofline": {
+            "kernel": {"fwd": "dwconv_rows_kernel<FWD>", "bwd_input": "dwconv_rows_kernel<DX>",
+                       "bwd_weight": "dwconv_dk_kernel"}[dominant],
+            "bound": "hbm",
+            "achieved": ach,
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(ach / PEAK_HBM_GBPS, 4),
+            "traffic": (traffic["fetch"] + traffic["write"]) if traffic else None,
+            "algorithmic_bytes": nbytes,
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        line["cpu_baseline"] = cpu_baseline(x_cpu, w_cpu, dy_cpu, args.cpu_runs)
+    rt.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

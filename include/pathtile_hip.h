@@ -1,0 +1,132 @@
+/*
+ * pathtile_hip.h — C ABI of the MI355X (gfx950) depthwise Conv1D library.
+ *
+ * Semantics shared by every entry point (FP32, contiguous row-major tensors):
+ *   x, y, dy, dx : [B, H, L]      w, dk : [H, K]      p = K / 2 (floor)
+ *   y [b,h,t] = sum_{j<K} w[h,j] * x [b,h,t+j-p]      (zero outside [0, L))
+ *   dx[b,h,s] = sum_{j<K} w[h,j] * dy[b,h,s-j+p]
+ *   dk[h,j]   = sum_b sum_t dy[b,h,t] * x[b,h,t+j-p]
+ * i.e. cross-correlation, "same" length with asymmetric padding (left p,
+ * right K-1-p), as in the reference kernels
+ * kernels/warp_tiled_ampere.py:372-434 (fwd), :440-502 (dx), :509-619 (dk)
+ * and the PyTorch boundary benchmark/benchmark_shape_sweep_ampere.py:220-239.
+ *
+ * Limits: 1 <= L <= 48, 1 <= K <= 48 (the reference rejects L>48 or K>48 at
+ * kernels/warp_tiled_ampere.py:715-716), B >= 0, H >= 0, B*H*L < 2^31.
+ *
+ * Every entry point:
+ *   - never allocates device memory and never throws across the boundary;
+ *   - enqueues work on `stream` (a hipStream_t, NULL = default stream) of the
+ *     device that is current on the calling thread, and returns without
+ *     synchronising;
+ *   - returns PT_OK or a negative PT_ERR_* code (the reference's only C ABI,
+ *     benchmark/flashdwc_fp32_bridge.cu:14-19, returns -2 for bad arguments;
+ *     PT_ERR_SHAPE keeps that value).
+ */
+#ifndef PATHTILE_HIP_H
+#define PATHTILE_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PT_ABI_VERSION 1
+
+#define PT_OK 0
+#define PT_ERR_NULL (-1)       /* a required pointer is NULL                 */
+#define PT_ERR_SHAPE (-2)      /* B,H,L,K outside the supported range        */
+#define PT_ERR_CONFIG (-3)     /* launch configuration not supported         */
+#define PT_ERR_WORKSPACE (-4)  /* workspace missing or too small             */
+#define PT_ERR_HIP (-5)        /* the HIP runtime reported a launch error    */
+#define PT_ERR_ALIGN (-6)      /* pointer not 4-byte aligned                 */
+
+#define PT_MAX_L 48
+#define PT_MAX_K 48
+
+/* Kernel identifiers for pt_kernel_attributes. */
+#define PT_KERNEL_FWD 0
+#define PT_KERNEL_DX 1
+#define PT_KERNEL_DK 2
+#define PT_KERNEL_DK_REDUCE 3
+
+/* Version of this ABI (PT_ABI_VERSION). */
+int pt_abi_version(void);
+
+/* Static text for a status code ("ok", "invalid shape", ...). */
+const char* pt_status_string(int status);
+
+/*
+ * Forward pass y = conv(x, w).
+ * Replaces the launch of dwconv1d_warptile_fwd in
+ * AmpereWarpRuntime.launch_fwd (kernels/warp_tiled_ampere.py:723-747).
+ * waves_per_block: 64-lane wavefronts per workgroup, one of 1,2,4,8,16 (the
+ * MI355X counterpart of WARPS_PER_BLOCK, kernels/warp_tiled_ampere.py:643-644).
+ */
+int pt_dwconv1d_fwd_f32(const float* x, const float* w, float* y, int B, int H,
+                        int L, int K, int waves_per_block, void* stream);
+
+/*
+ * Input gradient dx = conv^T(dy, w).
+ * Replaces dwconv1d_warptile_bwd_input in AmpereWarpRuntime.launch_bwd_input
+ * (kernels/warp_tiled_ampere.py:749-770).
+ */
+int pt_dwconv1d_dx_f32(const float* dy, const float* w, float* dx, int B,
+                       int H, int L, int K, int waves_per_block, void* stream);
+
+/*
+ * Weight gradient, atomic variant: dk += sum over batch tiles.
+ * Replaces dwconv1d_warptile_bwd_weight in AmpereWarpRuntime.launch_bwd_weight
+ * (kernels/warp_tiled_ampere.py:772-812). The reference requires the caller
+ * to zero dk first (:890-893); zero_first != 0 clears dk on `stream` with a
+ * fill kernel before the accumulation, so "dK including zero-init" is one
+ * call. threads_per_block: a multiple of 64 in [64, 1024] (the counterpart of
+ * BWDK_BLOCK, :645-649). Summation order across workgroups is not fixed.
+ */
+int pt_dwconv1d_dk_atomic_f32(const float* dy, const float* x, float* dk,
+                              int B, int H, int L, int K,
+                              int threads_per_block, int zero_first,
+                              void* stream);
+
+/*
+ * Bytes of workspace pt_dwconv1d_dk_det_f32 needs for this shape/config
+ * (the [H, K, num_btiles] partials of
+ * kernels/warp_tiled_noatomic_optimized.py:1448-1471).
+ */
+int pt_dwconv1d_dk_det_workspace_bytes(int B, int H, int L, int K,
+                                       int threads_per_block, size_t* bytes);
+
+/*
+ * Weight gradient, deterministic two-pass variant: per-batch-tile partials
+ * into `workspace`, then a fixed-order reduction that overwrites dk (no
+ * zero-init needed). Bitwise reproducible for a fixed shape and
+ * threads_per_block. Replaces dwconv1d_warptile_bwd_weight_partials +
+ * dwconv1d_warptile_reduce_partials
+ * (kernels/warp_tiled_noatomic_optimized.py:881,1116; launch :1473-1554).
+ */
+int pt_dwconv1d_dk_det_f32(const float* dy, const float* x, float* dk,
+                           void* workspace, size_t workspace_bytes, int B,
+                           int H, int L, int K, int threads_per_block,
+                           void* stream);
+
+/*
+ * Compiled resources of the kernel that serves (L, K) for `kernel_id`
+ * (PT_KERNEL_*), as hipFuncGetAttributes reports them on the current device:
+ * registers per lane, static LDS bytes, scratch (private) bytes per lane and
+ * max threads per block. Any output pointer may be NULL. Counterpart of the
+ * PyCUDA attributes read by AmpereWarpRuntime.resource_report
+ * (kernels/warp_tiled_ampere.py:814-833). Needs a device.
+ */
+int pt_kernel_attributes(int kernel_id, int L, int K, int* regs,
+                         int* lds_bytes, int* scratch_bytes, int* max_threads);
+
+/* Dynamic LDS bytes one workgroup of `kernel_id` uses at this launch config. */
+int pt_dynamic_lds_bytes(int kernel_id, int L, int K, int block_config,
+                         int* lds_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PATHTILE_HIP_H */

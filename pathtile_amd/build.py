@@ -1,0 +1,71 @@
+"""Build ``libpathtile_hip.so`` (gfx950) in-tree with hipcc.
+
+Usage: ``python -m pathtile_amd.build`` (or ``__graft_entry__.build()``).
+
+The library is a plain C-ABI shared object (``include/pathtile_hip.h``); it
+links against libamdhip64 by its soname, so inside a process that already
+imported torch it binds to torch's HIP runtime and shares its streams.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+SRC = PKG / "csrc" / "dwconv1d.hip"
+INCLUDE = ROOT / "include"
+LIB = PKG / "libpathtile_hip.so"
+ARCH = os.environ.get("PATHTILE_OFFLOAD_ARCH", "gfx950")
+
+HIPCC_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    f"--offload-arch={ARCH}",
+    # Packed FP32 (v_pk_fma_f32 and friends) stays off on this pool.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # float atomicAdd lowers to the hardware global_atomic_add_f32.
+    "-munsafe-fp-atomics",
+    "-Wall",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def build(verbose: bool = False, output: Path | None = None) -> Path:
+    """Compile the HIP sources into ``pathtile_amd/libpathtile_hip.so``."""
+    out = Path(output) if output else LIB
+    tmp = out.with_name(out.name + f".tmp{os.getpid()}")
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-o", str(tmp), str(SRC)]
+    t0 = time.time()
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        try:
+            tmp.unlink()
+        except FileNotFoundError:
+            pass
+        raise RuntimeError(
+            "hipcc failed:\n" + " ".join(cmd) + "\n" + proc.stdout + proc.stderr
+        )
+    os.replace(tmp, out)
+    if verbose:
+        print(f"[pathtile_amd.build] {out} in {time.time() - t0:.1f}s", flush=True)
+    return out
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    sys.exit(0)

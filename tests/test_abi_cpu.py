@@ -1,0 +1,143 @@
+"""C-ABI and host-logic tests that need no GPU.
+
+The library is loaded and every symbol ``include/pathtile_hip.h`` declares
+must be exported; argument validation is exercised only on paths that
+return before any HIP call (invalid shapes/configs/NULL pointers).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "pathtile_hip.h"
+
+
+def _declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pt_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from pathtile_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libpathtile_hip.so not built (python -m pathtile_amd.build)")
+    return _lib.load()
+
+
+def test_header_declares_the_expected_entry_points():
+    syms = _declared_symbols()
+    for name in (
+        "pt_dwconv1d_fwd_f32",
+        "pt_dwconv1d_dx_f32",
+        "pt_dwconv1d_dk_atomic_f32",
+        "pt_dwconv1d_dk_det_f32",
+        "pt_dwconv1d_dk_det_workspace_bytes",
+        "pt_kernel_attributes",
+        "pt_status_string",
+        "pt_abi_version",
+    ):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from pathtile_amd import _lib
+
+    syms = _declared_symbols()
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (pt_[a-z0-9_]+)", out))
+    assert set(syms) <= exported, set(syms) - exported
+    assert set(syms) == set(_lib.SIGNATURES), set(syms) ^ set(_lib.SIGNATURES)
+    for name in syms:
+        assert getattr(lib, name) is not None
+
+
+def test_status_codes(lib):
+    from pathtile_amd import _lib
+
+    assert lib.pt_abi_version() == 1
+    assert _lib.status_string(0) == "ok"
+    assert "shape" in _lib.status_string(_lib.PT_ERR_SHAPE)
+    assert _lib.status_string(-99) == "unknown status"
+    with pytest.raises(ValueError):
+        _lib.check(_lib.PT_ERR_SHAPE, "x")
+    with pytest.raises(_lib.PathTileLibraryError):
+        _lib.check(_lib.PT_ERR_HIP, "x")
+
+
+def _fake(n=64):
+    # Host buffers stand in for device pointers: every call below must be
+    # rejected before any pointer is dereferenced or any HIP call is made.
+    return (ctypes.c_float * n)()
+
+
+def test_argument_validation_before_launch(lib):
+    from pathtile_amd import _lib
+
+    a, b, c = _fake(), _fake(), _fake()
+    P = ctypes.cast
+    vp = ctypes.c_void_p
+    pa, pb, pc = (vp(ctypes.addressof(t)) for t in (a, b, c))
+    S = None
+    # NULL pointers
+    assert lib.pt_dwconv1d_fwd_f32(None, pb, pc, 1, 1, 8, 3, 4, S) == _lib.PT_ERR_NULL
+    assert lib.pt_dwconv1d_dx_f32(pa, None, pc, 1, 1, 8, 3, 4, S) == _lib.PT_ERR_NULL
+    assert lib.pt_dwconv1d_dk_atomic_f32(pa, pb, None, 1, 1, 8, 3, 256, 0, S) == _lib.PT_ERR_NULL
+    # shapes: L, K in [1, 48]
+    for L, K in ((49, 3), (0, 3), (8, 49), (8, 0)):
+        assert lib.pt_dwconv1d_fwd_f32(pa, pb, pc, 1, 1, L, K, 4, S) == _lib.PT_ERR_SHAPE
+        assert lib.pt_dwconv1d_dk_atomic_f32(pa, pb, pc, 1, 1, L, K, 256, 0, S) == _lib.PT_ERR_SHAPE
+    assert lib.pt_dwconv1d_fwd_f32(pa, pb, pc, -1, 1, 8, 3, 4, S) == _lib.PT_ERR_SHAPE
+    assert lib.pt_dwconv1d_fwd_f32(pa, pb, pc, 1 << 20, 1 << 10, 48, 3, 4, S) == _lib.PT_ERR_SHAPE
+    # launch configs
+    for w in (0, 3, 5, 32):
+        assert lib.pt_dwconv1d_fwd_f32(pa, pb, pc, 1, 1, 8, 3, w, S) == _lib.PT_ERR_CONFIG
+    for t in (0, 32, 96, 800, 1024):
+        assert lib.pt_dwconv1d_dk_atomic_f32(pa, pb, pc, 1, 1, 8, 3, t, 0, S) == _lib.PT_ERR_CONFIG
+    # alignment
+    mis = vp(ctypes.addressof(a) + 2)
+    assert lib.pt_dwconv1d_fwd_f32(mis, pb, pc, 1, 1, 8, 3, 4, S) == _lib.PT_ERR_ALIGN
+    # empty batch / channels: nothing to launch
+    assert lib.pt_dwconv1d_fwd_f32(pa, pb, pc, 0, 4, 8, 3, 4, S) == _lib.PT_OK
+    assert lib.pt_dwconv1d_dx_f32(pa, pb, pc, 5, 0, 8, 3, 4, S) == _lib.PT_OK
+    # workspace too small for the deterministic dK
+    assert lib.pt_dwconv1d_dk_det_f32(pa, pb, pc, None, 0, 64, 2, 8, 3, 256, S) == _lib.PT_ERR_WORKSPACE
+    del P
+
+
+def test_workspace_bytes(lib):
+    from pathtile_amd import _lib
+
+    out = ctypes.c_size_t(0)
+    st = lib.pt_dwconv1d_dk_det_workspace_bytes(16384, 128, 48, 48, 256, ctypes.byref(out))
+    assert st == _lib.PT_OK
+    # [H, K, num_btiles] floats; num_btiles * tile covers B
+    nbt = out.value // (128 * 48 * 4)
+    assert out.value == 128 * 48 * 4 * nbt and nbt >= 1
+    assert nbt * (256 // 64) * 64 >= 16384 / 16  # tiles cover the batch
+    st = lib.pt_dwconv1d_dk_det_workspace_bytes(0, 4, 8, 3, 256, ctypes.byref(out))
+    assert st == _lib.PT_OK and out.value == 0
+    lds = ctypes.c_int(0)
+    assert lib.pt_dynamic_lds_bytes(_lib.PT_KERNEL_FWD, 48, 48, 8, ctypes.byref(lds)) == 0
+    assert lds.value == 8 * 5120
+    assert lib.pt_dynamic_lds_bytes(_lib.PT_KERNEL_FWD, 48, 48, 3, ctypes.byref(lds)) == _lib.PT_ERR_CONFIG
+
+
+def test_library_is_not_linked_to_the_oracle():
+    from pathtile_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("library not built")
+    needed = subprocess.run(["readelf", "-d", str(_lib.LIB_PATH)], capture_output=True,
+                            text=True, check=True).stdout
+    assert "oracle" not in needed
+    assert "libamdhip64.so" in needed

@@ -1,0 +1,287 @@
+"""GPU parity of the HIP kernels against the CPU oracle (marked ``gpu``).
+
+Bars (stated per test):
+* FWD / dX: bit-exact against the oracle's restatement of the reference's
+  FP32 fmaf chain (oracle.fwd_f32_refchain / dx_f32_refchain) and within
+  1e-5 max-abs-scaled of FP64;
+* dK (atomic and deterministic): within 1e-4 max-abs-scaled of FP64
+  (atomic order is not fixed); the deterministic variant is also bitwise
+  reproducible run to run; taps that meet no element are exactly 0.
+Large shapes are checked on sampled batch rows (FWD/dX) and in full (dK).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+FWD_TOL = 1e-5
+DK_TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def rt():
+    from pathtile_amd import runtime
+
+    r = runtime.HipWarpRuntime()
+    yield r
+    r.close()
+
+
+def _dev(*ts):
+    return [t.to("cuda:0") for t in ts]
+
+
+def _inputs(B, H, L, K, seed):
+    print(f"[case] B={B} H={H} L={L} K={K} seed={seed}", flush=True)
+    return oracle.make_inputs(B, H, L, K, seed)
+
+
+def _fwd(rt, x, w):
+    y = torch.empty_like(x)
+    rt.launch_fwd(x, w, y)
+    return y
+
+
+def _dx(rt, dy, w):
+    dx = torch.empty_like(dy)
+    rt.launch_bwd_input(dy, w, dx)
+    return dx
+
+
+def _dk_atomic(rt, dy, x, K, zero_first=True):
+    gk = torch.full((x.shape[1], K), float("nan"), device=x.device) if zero_first \
+        else torch.zeros((x.shape[1], K), device=x.device)
+    rt.launch_bwd_weight(dy, x, gk, K, zero_first=zero_first)
+    return gk
+
+
+def _dk_det(rt, dy, x, K):
+    gk = torch.full((x.shape[1], K), float("nan"), device=x.device)
+    rt.launch_bwd_weight_deterministic(dy, x, gk, K)
+    return gk
+
+
+SHAPES = [
+    (64, 16, 48, 48),     # C1
+    (1000, 96, 37, 48),   # E1: B not a multiple of 64, K > L, L % 4 != 0
+    (300, 16, 48, 47),    # odd K (E2 family)
+    (257, 8, 48, 4),      # short filter (S family)
+    (70, 5, 16, 48),      # K > L, zero-overlap taps
+    (3, 7, 1, 5),         # L = 1
+    (65, 3, 17, 13),      # reference dK edge case (benchmark_dk_packing.py:276-289)
+    (1, 1, 1, 1),         # reference dK edge case
+    (33, 9, 24, 8),
+    (128, 64, 32, 32),
+    (40, 4, 40, 24),
+    (17, 2, 8, 3),
+    (5, 3, 48, 1),
+    (129, 2, 45, 40),
+    (64, 128, 48, 48),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "B{}H{}L{}K{}".format(*s))
+def test_fwd_dx_bit_exact_and_fp64(rt, shape):
+    B, H, L, K = shape
+    x, w, dy = _inputs(B, H, L, K, seed=1000 + B + H + L + K)
+    xd, wd, dyd = _dev(x, w, dy)
+    y = _fwd(rt, xd, wd).cpu().numpy()
+    dx = _dx(rt, dyd, wd).cpu().numpy()
+    y_ref = oracle.fwd_f32_refchain(x, w)
+    dx_ref = oracle.dx_f32_refchain(dy, w)
+    assert np.array_equal(y, y_ref), oracle.normalized_max_abs(y, y_ref)
+    assert np.array_equal(dx, dx_ref), oracle.normalized_max_abs(dx, dx_ref)
+    assert oracle.normalized_max_abs(y, oracle.fwd_f64(x, w)) < FWD_TOL
+    assert oracle.normalized_max_abs(dx, oracle.dx_f64(dy, w)) < FWD_TOL
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "B{}H{}L{}K{}".format(*s))
+def test_dk_atomic_and_deterministic(rt, shape):
+    B, H, L, K = shape
+    x, w, dy = _inputs(B, H, L, K, seed=2000 + B + H + L + K)
+    xd, dyd = _dev(x, dy)
+    ref = oracle.dk_f64(dy, x, K)
+    ga = _dk_atomic(rt, dyd, xd, K).cpu().numpy()
+    gd1 = _dk_det(rt, dyd, xd, K).cpu().numpy()
+    gd2 = _dk_det(rt, dyd, xd, K).cpu().numpy()
+    assert np.isfinite(ga).all() and np.isfinite(gd1).all()
+    assert oracle.normalized_max_abs(ga, ref) < DK_TOL
+    assert oracle.normalized_max_abs(gd1, ref) < DK_TOL
+    assert np.array_equal(gd1, gd2)  # run-to-run bitwise
+    for j in range(K):
+        lo, hi = oracle.valid_tap_range(L, K, j)
+        if hi <= lo:
+            assert np.all(ga[:, j] == 0.0) and np.all(gd1[:, j] == 0.0)
+
+
+def test_golden_c1_fixture(rt):
+    from pathlib import Path
+
+    d = np.load(Path(__file__).resolve().parent / "golden" / "c1_b64_h16_l48_k48.npz")
+    x, w, dy = (torch.from_numpy(d[k]) for k in ("x", "w", "dy"))
+    xd, wd, dyd = _dev(x, w, dy)
+    K = w.shape[1]
+    assert oracle.normalized_max_abs(_fwd(rt, xd, wd).cpu().numpy(), d["y"]) < FWD_TOL
+    assert oracle.normalized_max_abs(_dx(rt, dyd, wd).cpu().numpy(), d["dx"]) < FWD_TOL
+    assert oracle.normalized_max_abs(_dk_atomic(rt, dyd, xd, K).cpu().numpy(), d["dk64"]) < DK_TOL
+    assert oracle.normalized_max_abs(_dk_det(rt, dyd, xd, K).cpu().numpy(), d["dk64"]) < DK_TOL
+
+
+def test_golden_edge_fixtures(rt):
+    from pathlib import Path
+
+    d = np.load(Path(__file__).resolve().parent / "golden" / "edge_cases.npz")
+    names = sorted({k.split("/")[0] for k in d.files})
+    for n in names:
+        print(f"[fixture] {n}", flush=True)
+        x, w, dy = (torch.from_numpy(d[f"{n}/{k}"]) for k in ("x", "w", "dy"))
+        xd, wd, dyd = _dev(x, w, dy)
+        K = w.shape[1]
+        assert oracle.normalized_max_abs(_fwd(rt, xd, wd).cpu().numpy(), d[f"{n}/y64"]) < FWD_TOL
+        assert oracle.normalized_max_abs(_dx(rt, dyd, wd).cpu().numpy(), d[f"{n}/dx64"]) < FWD_TOL
+        assert oracle.normalized_max_abs(_dk_atomic(rt, dyd, xd, K).cpu().numpy(), d[f"{n}/dk64"]) < DK_TOL
+        assert oracle.normalized_max_abs(_dk_det(rt, dyd, xd, K).cpu().numpy(), d[f"{n}/dk64"]) < DK_TOL
+
+
+@pytest.mark.parametrize("wpb", [1, 2, 4, 8, 16])
+def test_every_waves_per_block_gives_the_same_bits(wpb):
+    from pathtile_amd import runtime
+
+    B, H, L, K = 200, 24, 48, 48
+    x, w, dy = _inputs(B, H, L, K, seed=7)
+    xd, wd, dyd = _dev(x, w, dy)
+    r = runtime.HipWarpRuntime(waves_per_block=wpb)
+    y = _fwd(r, xd, wd).cpu().numpy()
+    dx = _dx(r, dyd, wd).cpu().numpy()
+    assert np.array_equal(y, oracle.fwd_f32_refchain(x, w))
+    assert np.array_equal(dx, oracle.dx_f32_refchain(dy, w))
+
+
+@pytest.mark.parametrize("threads", [64, 128, 192, 256, 320, 384, 512, 768])
+def test_every_dk_block_size(threads):
+    from pathtile_amd import runtime
+
+    B, H, L, K = 1000, 12, 48, 48
+    x, w, dy = _inputs(B, H, L, K, seed=8)
+    xd, dyd = _dev(x, dy)
+    ref = oracle.dk_f64(dy, x, K)
+    r = runtime.HipWarpRuntime(bwdk_block=threads)
+    assert oracle.normalized_max_abs(_dk_atomic(r, dyd, xd, K).cpu().numpy(), ref) < DK_TOL
+    g1 = _dk_det(r, dyd, xd, K).cpu().numpy()
+    assert oracle.normalized_max_abs(g1, ref) < DK_TOL
+    assert np.array_equal(g1, _dk_det(r, dyd, xd, K).cpu().numpy())
+
+
+def test_atomic_dk_accumulates_into_gk(rt):
+    """The reference's contract: the atomic kernel adds into gk
+    (kernels/warp_tiled_ampere.py:890-893)."""
+    B, H, L, K = 256, 8, 48, 16
+    x, w, dy = _inputs(B, H, L, K, seed=9)
+    xd, dyd = _dev(x, dy)
+    ref = oracle.dk_f64(dy, x, K)
+    gk = torch.zeros(H, K, device="cuda:0")
+    rt.launch_bwd_weight(dyd, xd, gk, K)
+    rt.launch_bwd_weight(dyd, xd, gk, K)
+    assert oracle.normalized_max_abs(gk.cpu().numpy(), 2 * ref) < DK_TOL
+    rt.launch_bwd_weight(dyd, xd, gk, K, zero_first=True)
+    assert oracle.normalized_max_abs(gk.cpu().numpy(), ref) < DK_TOL
+
+
+def test_primary_shape_sampled_rows_and_full_dk(rt):
+    """B=16384 H=128 L=48 K=48: FWD/dX bit-exact on 256 sampled batch rows
+    (all channels), dK against FP64 over the full batch."""
+    B, H, L, K = 16384, 128, 48, 48
+    x, w, dy = _inputs(B, H, L, K, seed=42)
+    xd, wd, dyd = _dev(x, w, dy)
+    y = _fwd(rt, xd, wd)
+    dx = _dx(rt, dyd, wd)
+    idx = torch.from_numpy(np.random.default_rng(0).choice(B, 256, replace=False))
+    ys, dxs = y[idx.cuda()].cpu().numpy(), dx[idx.cuda()].cpu().numpy()
+    assert np.array_equal(ys, oracle.fwd_f32_refchain(x[idx], w))
+    assert np.array_equal(dxs, oracle.dx_f32_refchain(dy[idx], w))
+    ref = oracle.dk_f64(dy, x, K)
+    assert oracle.normalized_max_abs(_dk_atomic(rt, dyd, xd, K).cpu().numpy(), ref) < DK_TOL
+    g1 = _dk_det(rt, dyd, xd, K).cpu().numpy()
+    assert oracle.normalized_max_abs(g1, ref) < DK_TOL
+    assert np.array_equal(g1, _dk_det(rt, dyd, xd, K).cpu().numpy())
+    # size-independent: the adjoint identity <FWD(x), dY> = <x, DX(dY)> in FP64
+    left = float((y.double() * dyd.double()).sum())
+    right = float((xd.double() * dx.double()).sum())
+    assert abs(left - right) <= 1e-6 * math.sqrt(float((y.double() ** 2).sum()) * float((dyd.double() ** 2).sum()))
+
+
+def test_misaligned_and_noncontiguous_inputs(rt):
+    """A storage offset that breaks 16-byte alignment takes the dword path;
+    results stay bit-exact."""
+    B, H, L, K = 64, 6, 48, 48
+    x, w, dy = _inputs(B, H, L, K, seed=10)
+    flat = torch.zeros(x.numel() + 1, device="cuda:0")
+    flat[1:] = x.reshape(-1).cuda()
+    xm = flat[1:].view(B, H, L)  # 4-byte aligned only
+    assert xm.data_ptr() % 16 != 0
+    y = _fwd(rt, xm, w.cuda()).cpu().numpy()
+    assert np.array_equal(y, oracle.fwd_f32_refchain(x, w))
+
+
+def test_autograd_depthconvampere_and_shared(rt):
+    from pathtile_amd import runtime
+    from pathtile_amd.kernels import warp_tiled as wt
+
+    runtime.install_runtime(rt)
+    B, H, L, K = 96, 10, 48, 48
+    x, w, dy = _inputs(B, H, L, K, seed=11)
+    _, gx_ref, gk_ref = oracle.torch_grads(x.double(), w.double(), dy.double())
+    for fn in (runtime.depthwise_conv_ampere, wt.depthwise_conv_shared):
+        xd = x.cuda().requires_grad_(True)
+        wd = w.cuda().requires_grad_(True)
+        y = fn(xd, wd)
+        assert np.array_equal(y.detach().cpu().numpy(), oracle.fwd_f32_refchain(x, w))
+        gx, gk = torch.autograd.grad(y, (xd, wd), dy.cuda())
+        assert oracle.normalized_max_abs(gx.cpu().numpy(), gx_ref.numpy()) < FWD_TOL
+        assert oracle.normalized_max_abs(gk.cpu().numpy(), gk_ref.numpy()) < DK_TOL
+    wt.reset_timing_collectors()
+    xd = x.cuda().requires_grad_(True)
+    y = wt.DepthwiseConvShared.apply(xd, w.cuda().requires_grad_(True))
+    y.backward(dy.cuda())
+    assert len(wt.FWD_TIMES) == len(wt.BWD_IN_TIMES) == len(wt.BWD_K_TIMES) == 1
+    assert all(t > 0 for t in wt.FWD_TIMES + wt.BWD_IN_TIMES + wt.BWD_K_TIMES)
+
+
+def test_api_errors_on_gpu_tensors():
+    from pathtile_amd.kernels import warp_tiled as wt
+
+    x = torch.zeros(2, 3, 8, device="cuda:0")
+    k = torch.zeros(3, 4, device="cuda:0")
+    with pytest.raises(TypeError, match="x must be float32"):
+        wt.depthwise_conv_shared(x.double(), k)
+    with pytest.raises(TypeError, match="kernel must be float32"):
+        wt.depthwise_conv_shared(x, k.double())
+    with pytest.raises(ValueError, match=r"x must be \[B,H,L\]"):
+        wt.depthwise_conv_shared(x[0], k)
+    with pytest.raises(ValueError, match=r"kernel must be \[H,K\]"):
+        wt.depthwise_conv_shared(x, k[0])
+    with pytest.raises(ValueError, match="Channel mismatch: x H=3, kernel H=2"):
+        wt.depthwise_conv_shared(x, k[:2])
+    with pytest.raises(ValueError, match="L<=48, K<=48"):
+        wt.depthwise_conv_shared(torch.zeros(1, 3, 49, device="cuda:0"), k)
+
+
+def test_empty_batch(rt):
+    x = torch.zeros(0, 4, 16, device="cuda:0")
+    w = torch.randn(4, 5, device="cuda:0")
+    y = torch.empty_like(x)
+    rt.launch_fwd(x, w, y)
+    gk = torch.full((4, 5), 7.0, device="cuda:0")
+    rt.launch_bwd_weight(x, x, gk, 5, zero_first=True)
+    assert torch.all(gk == 0)
+    gk.fill_(7.0)
+    rt.launch_bwd_weight_deterministic(x, x, gk, 5)
+    assert torch.all(gk == 0)
