@@ -56,6 +56,10 @@ def parse_args(argv=None):
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-runs", type=int, default=5)
+    p.add_argument("--copy-probe", type=int, default=0, metavar="N",
+                   help="after timing, run N plain device copies of x into y "
+                        "(known bytes: 2 * B*H*L*4 per copy) to calibrate "
+                        "rocprofv3 FETCH_SIZE / WRITE_SIZE")
     return p.parse_args(argv)
 
 
@@ -321,6 +325,12 @@ def main(argv=None) -> int:
             "algorithmic_bytes": nbytes,
         },
     }
+    if args.copy_probe:
+        for _ in range(args.copy_probe):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        line["copy_probe"] = {"copies": args.copy_probe, "bytes_read_per_copy": x.numel() * 4,
+                              "bytes_written_per_copy": x.numel() * 4}
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         line["cpu_baseline"] = cpu_baseline(x_cpu, w_cpu, dy_cpu, args.cpu_runs)
