@@ -18,8 +18,20 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
-SRC = PKG / "csrc" / "dwconv1d.hip"
+CSRC = PKG / "csrc"
+# One translation unit per dispatch table (compiled in parallel) + host side.
+SOURCES = [
+    "dwconv1d_abi.hip",
+    "inst_fwd_v.hip",
+    "inst_fwd_s.hip",
+    "inst_dx_v.hip",
+    "inst_dx_s.hip",
+    "inst_dk_v.hip",
+    "inst_dk_s.hip",
+    "inst_dk_mfma.hip",
+]
 INCLUDE = ROOT / "include"
+BUILD_DIR = PKG / "_build"
 LIB = PKG / "libpathtile_hip.so"
 ARCH = os.environ.get("PATHTILE_OFFLOAD_ARCH", "gfx950")
 
@@ -27,7 +39,6 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     f"--offload-arch={ARCH}",
     # Packed FP32 (v_pk_fma_f32 and friends) stays off on this pool.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -45,24 +56,39 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def build(verbose: bool = False, output: Path | None = None) -> Path:
-    """Compile the HIP sources into ``pathtile_amd/libpathtile_hip.so``."""
+def _compile(src: str) -> Path:
+    obj = BUILD_DIR / (Path(src).stem + ".o")
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", "-o", str(obj), str(CSRC / src)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError("hipcc failed:\n" + " ".join(cmd) + "\n" + proc.stdout + proc.stderr)
+    return obj
+
+
+def build(verbose: bool = False, output: Path | None = None, jobs: int | None = None) -> Path:
+    """Compile the HIP sources (one hipcc per translation unit, in parallel)
+    and link ``pathtile_amd/libpathtile_hip.so``."""
+    from concurrent.futures import ThreadPoolExecutor
+
     out = Path(output) if output else LIB
-    tmp = out.with_name(out.name + f".tmp{os.getpid()}")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-o", str(tmp), str(SRC)]
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
     t0 = time.time()
+    jobs = jobs or min(len(SOURCES), max(1, os.cpu_count() or 1), 16)
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(_compile, SOURCES))
+    tmp = out.with_name(out.name + f".tmp{os.getpid()}")
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp),
+           *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         try:
             tmp.unlink()
         except FileNotFoundError:
             pass
-        raise RuntimeError(
-            "hipcc failed:\n" + " ".join(cmd) + "\n" + proc.stdout + proc.stderr
-        )
+        raise RuntimeError("link failed:\n" + " ".join(cmd) + "\n" + proc.stdout + proc.stderr)
     os.replace(tmp, out)
     if verbose:
-        print(f"[pathtile_amd.build] {out} in {time.time() - t0:.1f}s", flush=True)
+        print(f"[pathtile_amd.build] {out} in {time.time() - t0:.1f}s ({jobs} jobs)", flush=True)
     return out
 
 

@@ -1,0 +1,421 @@
+// dwconv1d_abi.hip — host side of the depthwise Conv1D library: argument
+// checks, launch geometry, dispatch and the C ABI of include/pathtile_hip.h.
+// The kernels live in dwconv1d_kernels.hpp and are instantiated in the
+// inst_*.hip translation units.
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "dwconv1d_kernels.hpp"
+#include "dwconv1d_tables.hpp"
+#include "pathtile_hip.h"
+
+namespace pt {
+
+// Pass 2 of the deterministic DK: one wave per coefficient, lanes sum the
+// batch-tile partials in a fixed order, then a fixed wave reduction.
+__global__ __launch_bounds__(256) void dk_reduce_kernel(
+    const float* __restrict__ partials, float* __restrict__ dk, int ncoef,
+    int nbt) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int coef = blockIdx.x * (blockDim.x / kWave) + (int)(threadIdx.x / kWave);
+  if (coef >= ncoef) return;
+  const float* p = partials + (size_t)coef * (size_t)nbt;
+  float acc = 0.0f;
+  for (int q = lane; q < nbt; q += kWave) acc += p[q];
+  acc = wave_sum(acc);
+  if (lane == 0) dk[coef] = acc;
+}
+
+__global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p,
+                                                        int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+
+// ---------------------------------------------------------------------------
+// Dispatch helpers
+// ---------------------------------------------------------------------------
+static int mfma_index(int L) { return (L + 15) / 16 - 1; }
+static size_t mfma_lds_per_wave(int L) {
+  const int dim = 16 * (mfma_index(L) + 1);
+  return (size_t)dim * (size_t)(dim + 1) * sizeof(float);
+}
+static int lbucket_index(int L) { return (L + 7) / 8 - 1; }
+static int kbucket_index(int K) {
+  for (int i = 0; i < kNumKB; ++i)
+    if (K <= kKBuckets[i]) return i;
+  return kNumKB - 1;
+}
+
+// ---------------------------------------------------------------------------
+// Host-side validation and launch geometry
+// ---------------------------------------------------------------------------
+static int check_shape(int B, int H, int L, int K) {
+  if (B < 0 || H < 0 || L < 1 || K < 1) return PT_ERR_SHAPE;
+  if (L > kMaxL || K > kMaxK) return PT_ERR_SHAPE;
+  const long long elems = (long long)B * (long long)H * (long long)L;
+  if (elems >= (1LL << 31)) return PT_ERR_SHAPE;
+  if ((long long)H * K * 4 >= (1LL << 31)) return PT_ERR_SHAPE;
+  // a wave's 64-row tile must span < 2 GiB (buffer offsets, see kOob)
+  if ((long long)kWave * H * L * 4 >= (1LL << 31)) return PT_ERR_SHAPE;
+  return PT_OK;
+}
+
+static bool aligned(const void* p, uintptr_t a) {
+  return ((uintptr_t)p & (a - 1)) == 0;
+}
+
+// --- device queries (cached per device / per kernel) -----------------------
+static int num_cus() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    dev = 0;
+  }
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+          hipSuccess ||
+      n <= 0) {
+    (void)hipGetLastError();
+    n = 256;
+  }
+  if (dev >= 0 && dev < 64) cache[dev] = n;
+  return n;
+}
+
+struct OccEntry {
+  const void* fn;
+  int block;
+  size_t lds;
+  int blocks;
+};
+static std::mutex g_occ_mu;
+static OccEntry g_occ[512];
+static int g_occ_n = 0;
+
+// Resident workgroups per CU for (kernel, block size, dynamic LDS).
+static int blocks_per_cu(const void* fn, int block, size_t lds) {
+  {
+    std::lock_guard<std::mutex> lk(g_occ_mu);
+    for (int i = 0; i < g_occ_n; ++i)
+      if (g_occ[i].fn == fn && g_occ[i].block == block && g_occ[i].lds == lds)
+        return g_occ[i].blocks;
+  }
+  int nb = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, block, lds) !=
+          hipSuccess ||
+      nb <= 0) {
+    (void)hipGetLastError();
+    nb = 1;
+  }
+  std::lock_guard<std::mutex> lk(g_occ_mu);
+  if (g_occ_n < 512) g_occ[g_occ_n++] = OccEntry{fn, block, lds, nb};
+  return nb;
+}
+
+// --- DK algorithm ----------------------------------------------------------
+// VALU (lane-per-row) or matrix-core (batch-contraction GEMM) kernel. The
+// matrix-core kernel computes every (t, s) pair of the row window, so it wins
+// for wide tap windows; PATHTILE_DK_ALGO=valu|mfma overrides the choice.
+enum DkAlgo { kDkValu = 0, kDkMfma = 1 };
+
+static DkAlgo dk_algo(int L, int K) {
+  const char* env = getenv("PATHTILE_DK_ALGO");
+  if (env && strcmp(env, "valu") == 0) return kDkValu;
+  if (env && strcmp(env, "mfma") == 0) return kDkMfma;
+  (void)L;
+  return K >= 16 ? kDkMfma : kDkValu;
+}
+
+// A DK workgroup covers one channel and a batch tile. Its size is fixed from
+// the shape alone (not the device), so the deterministic variant's workspace
+// size can be queried without a device. The tile is chosen so the grid holds
+// about 4096 waves (16 per CU on 256 CUs), which keeps atomics per tap low
+// (H * nbt * K total) without starving the CUs.
+constexpr long long kNominalWaves = 4096;
+
+struct DkGeom {
+  DkAlgo algo;
+  int wpb;
+  int rows_per_wave;  // VALU: 64-sample chunks per wave; MFMA: samples
+  int nbt;
+  long long nblocks;
+};
+
+static DkGeom dk_geometry(int B, int H, int L, int K, int threads) {
+  DkGeom g;
+  g.algo = dk_algo(L, K);
+  g.wpb = threads / kWave;
+  const long long wpb = g.wpb;
+  if (g.algo == kDkValu) {
+    const long long chunks_per_h = ((long long)B + kWave - 1) / kWave;
+    const long long total = chunks_per_h * (long long)H;
+    long long R = total / (wpb * 2048);
+    if (R < 1) R = 1;
+    if (R > 16) R = 16;
+    const long long rmax = (chunks_per_h + wpb - 1) / wpb;
+    if (R > rmax) R = rmax < 1 ? 1 : rmax;
+    g.rows_per_wave = (int)R;
+    const long long tile = wpb * R * kWave;
+    g.nbt = (int)(((long long)B + tile - 1) / tile);
+  } else {
+    long long rpw = ((long long)B * H + kNominalWaves - 1) / kNominalWaves;
+    rpw = (rpw + 15) / 16 * 16;
+    if (rpw < 16) rpw = 16;
+    const long long rmax = (((long long)B + wpb - 1) / wpb + 15) / 16 * 16;
+    if (rpw > rmax) rpw = rmax;
+    g.rows_per_wave = (int)rpw;
+    const long long tile = wpb * rpw;
+    g.nbt = (int)(((long long)B + tile - 1) / tile);
+  }
+  if (g.nbt < 1) g.nbt = 1;
+  g.nblocks = (long long)g.nbt * H;
+  return g;
+}
+
+static bool valid_wpb(int wpb) {
+  return wpb == 1 || wpb == 2 || wpb == 4 || wpb == 8 || wpb == 16;
+}
+
+static bool valid_dk_threads(int t) {
+  return t >= kWave && t <= kMaxDkThreads && (t % kWave) == 0;
+}
+
+static int launch(const void* fn, uint32_t grid, uint32_t block, size_t lds,
+                  void* stream, void** args) {
+  hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(block), args, lds,
+                                 (hipStream_t)stream);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return PT_ERR_HIP;
+  }
+  return PT_OK;
+}
+
+static int zero_fill(float* p, int n, void* stream) {
+  if (n <= 0) return PT_OK;
+  void* args[] = {&p, &n};
+  const uint32_t grid = (uint32_t)((n + 255) / 256);
+  return launch((const void*)&fill_zero_kernel, grid, 256, 0, stream, args);
+}
+
+static int rows_path(bool dx, const float* in, const float* w, float* out,
+                     int B, int H, int L, int K, int wpb, void* stream) {
+  int st = check_shape(B, H, L, K);
+  if (st != PT_OK) return st;
+  if (!valid_wpb(wpb)) return PT_ERR_CONFIG;
+  if (B == 0 || H == 0) return PT_OK;  // empty tensors may have NULL data
+  if (!in || !w || !out) return PT_ERR_NULL;
+  if (!aligned(in, 4) || !aligned(w, 4) || !aligned(out, 4))
+    return PT_ERR_ALIGN;
+  const bool vec = (L % 4 == 0) && aligned(in, 16) && aligned(out, 16);
+  const int li = lbucket_index(L), ki = kbucket_index(K);
+  RowsFn fn = dx ? (vec ? kDxTableV : kDxTableS)[li][ki]
+                 : (vec ? kFwdTableV : kFwdTableS)[li][ki];
+  const size_t lds = (size_t)wpb * kStageBytes;
+  const int ngroups = (H + wpb - 1) / wpb;
+  const long long nchunks = ((long long)B + kWave - 1) / kWave;
+  // Tiles per wave: spread H * nchunks tiles over one round of resident
+  // waves, so each wave streams several tiles with its next tile's loads in
+  // flight.
+  const long long resident = (long long)blocks_per_cu((const void*)fn,
+                                                      wpb * kWave, lds) *
+                             wpb * num_cus();
+  long long tpw = ((long long)H * nchunks + resident - 1) / resident;
+  if (tpw < 1) tpw = 1;
+  if (tpw > nchunks) tpw = nchunks;
+  const long long ncg = (nchunks + tpw - 1) / tpw;
+  const long long nb = ncg * ngroups;
+  if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
+  uint32_t nblocks = (uint32_t)nb;
+  int tpw_i = (int)tpw;
+  void* args[] = {&in, &w, &out, &B, &H, &L, &K, &wpb, (void*)&ngroups,
+                  &tpw_i, &nblocks};
+  return launch((const void*)fn, nblocks, (uint32_t)(wpb * kWave), lds, stream,
+                args);
+}
+
+static int dk_path(bool det, const float* gy, const float* x, float* dst,
+                   int B, int H, int L, int K, int threads, const DkGeom& g,
+                   void* stream) {
+  uint32_t nblocks = (uint32_t)g.nblocks;
+  int rpw = g.rows_per_wave, nbt = g.nbt, d = det ? 1 : 0;
+  if (g.algo == kDkMfma) {
+    DkMfmaFn fn = kDkMfmaTable[mfma_index(L)];
+    void* args[] = {&gy, &x, &dst, &B, &H, &L, &K, &rpw, &nbt, &nblocks, &d};
+    return launch((const void*)fn, nblocks, (uint32_t)threads,
+                  (size_t)g.wpb * mfma_lds_per_wave(L), stream, args);
+  }
+  const bool vec = (L % 4 == 0) && aligned(gy, 16) && aligned(x, 16);
+  DkFn fn = (vec ? kDkTableV : kDkTableS)[lbucket_index(L)][kbucket_index(K)];
+  void* args[] = {&gy, &x, &dst, &B, &H, &L, &K, &rpw, &nbt, &nblocks, &d};
+  return launch((const void*)fn, nblocks, (uint32_t)threads,
+                (size_t)g.wpb * kStageBytes, stream, args);
+}
+
+static const void* kernel_for(int kernel_id, int L, int K) {
+  if (L < 1 || L > kMaxL || K < 1 || K > kMaxK) return nullptr;
+  const int li = lbucket_index(L), ki = kbucket_index(K);
+  switch (kernel_id) {
+    case PT_KERNEL_FWD: return (const void*)kFwdTableV[li][ki];
+    case PT_KERNEL_DX: return (const void*)kDxTableV[li][ki];
+    case PT_KERNEL_DK:
+      return dk_algo(L, K) == kDkMfma ? (const void*)kDkMfmaTable[mfma_index(L)]
+                                      : (const void*)kDkTableV[li][ki];
+    case PT_KERNEL_DK_REDUCE: return (const void*)&dk_reduce_kernel;
+    default: return nullptr;
+  }
+}
+
+}  // namespace pt
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int pt_abi_version(void) { return PT_ABI_VERSION; }
+
+const char* pt_status_string(int status) {
+  switch (status) {
+    case PT_OK: return "ok";
+    case PT_ERR_NULL: return "null pointer argument";
+    case PT_ERR_SHAPE: return "invalid shape (need 1<=L<=48, 1<=K<=48, B,H>=0, B*H*L<2^31)";
+    case PT_ERR_CONFIG: return "unsupported launch configuration";
+    case PT_ERR_WORKSPACE: return "workspace missing or too small";
+    case PT_ERR_HIP: return "HIP runtime launch error";
+    case PT_ERR_ALIGN: return "pointer not 4-byte aligned";
+    default: return "unknown status";
+  }
+}
+
+int pt_dwconv1d_fwd_f32(const float* x, const float* w, float* y, int B, int H,
+                        int L, int K, int waves_per_block, void* stream) {
+  return pt::rows_path(false, x, w, y, B, H, L, K, waves_per_block, stream);
+}
+
+int pt_dwconv1d_dx_f32(const float* dy, const float* w, float* dx, int B,
+                       int H, int L, int K, int waves_per_block, void* stream) {
+  return pt::rows_path(true, dy, w, dx, B, H, L, K, waves_per_block, stream);
+}
+
+int pt_dwconv1d_dk_atomic_f32(const float* dy, const float* x, float* dk,
+                              int B, int H, int L, int K,
+                              int threads_per_block, int zero_first,
+                              void* stream) {
+  int st = pt::check_shape(B, H, L, K);
+  if (st != PT_OK) return st;
+  if (!pt::valid_dk_threads(threads_per_block)) return PT_ERR_CONFIG;
+  if (H == 0) return PT_OK;  // empty tensors may have NULL data
+  if (!dk) return PT_ERR_NULL;
+  if (!pt::aligned(dk, 4)) return PT_ERR_ALIGN;
+  if (zero_first) {
+    st = pt::zero_fill(dk, H * K, stream);
+    if (st != PT_OK) return st;
+  }
+  if (B == 0) return PT_OK;
+  if (!dy || !x) return PT_ERR_NULL;
+  if (!pt::aligned(dy, 4) || !pt::aligned(x, 4)) return PT_ERR_ALIGN;
+  const pt::DkGeom g = pt::dk_geometry(B, H, L, K, threads_per_block);
+  if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
+  return pt::dk_path(false, dy, x, dk, B, H, L, K, threads_per_block, g,
+                     stream);
+}
+
+int pt_dwconv1d_dk_det_workspace_bytes(int B, int H, int L, int K,
+                                       int threads_per_block, size_t* bytes) {
+  if (!bytes) return PT_ERR_NULL;
+  int st = pt::check_shape(B, H, L, K);
+  if (st != PT_OK) return st;
+  if (!pt::valid_dk_threads(threads_per_block)) return PT_ERR_CONFIG;
+  if (B == 0 || H == 0) {
+    *bytes = 0;
+    return PT_OK;
+  }
+  const pt::DkGeom g = pt::dk_geometry(B, H, L, K, threads_per_block);
+  *bytes = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
+  return PT_OK;
+}
+
+int pt_dwconv1d_dk_det_f32(const float* dy, const float* x, float* dk,
+                           void* workspace, size_t workspace_bytes, int B,
+                           int H, int L, int K, int threads_per_block,
+                           void* stream) {
+  int st = pt::check_shape(B, H, L, K);
+  if (st != PT_OK) return st;
+  if (!pt::valid_dk_threads(threads_per_block)) return PT_ERR_CONFIG;
+  if (H == 0) return PT_OK;  // empty tensors may have NULL data
+  if (!dk) return PT_ERR_NULL;
+  if (!pt::aligned(dk, 4)) return PT_ERR_ALIGN;
+  if (B == 0) return pt::zero_fill(dk, H * K, stream);
+  if (!dy || !x) return PT_ERR_NULL;
+  if (!pt::aligned(dy, 4) || !pt::aligned(x, 4)) return PT_ERR_ALIGN;
+  const pt::DkGeom g = pt::dk_geometry(B, H, L, K, threads_per_block);
+  if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
+  const size_t need = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
+  if (!workspace || workspace_bytes < need) return PT_ERR_WORKSPACE;
+  if (!pt::aligned(workspace, 4)) return PT_ERR_ALIGN;
+  float* partials = (float*)workspace;
+  st = pt::dk_path(true, dy, x, partials, B, H, L, K, threads_per_block, g,
+                   stream);
+  if (st != PT_OK) return st;
+  int ncoef = H * K;
+  int nbt = g.nbt;
+  const float* cp = partials;
+  void* args[] = {&cp, &dk, &ncoef, &nbt};
+  const uint32_t grid = (uint32_t)((ncoef + 3) / 4);
+  return pt::launch((const void*)&pt::dk_reduce_kernel, grid, 256, 0, stream,
+                    args);
+}
+
+int pt_kernel_attributes(int kernel_id, int L, int K, int* regs,
+                         int* lds_bytes, int* scratch_bytes,
+                         int* max_threads) {
+  const void* fn = pt::kernel_for(kernel_id, L, K);
+  if (!fn) return PT_ERR_CONFIG;
+  hipFuncAttributes a;
+  if (hipFuncGetAttributes(&a, fn) != hipSuccess) {
+    (void)hipGetLastError();
+    return PT_ERR_HIP;
+  }
+  if (regs) *regs = a.numRegs;
+  if (lds_bytes) *lds_bytes = (int)a.sharedSizeBytes;
+  if (scratch_bytes) *scratch_bytes = (int)a.localSizeBytes;
+  if (max_threads) *max_threads = a.maxThreadsPerBlock;
+  return PT_OK;
+}
+
+int pt_dynamic_lds_bytes(int kernel_id, int L, int K, int block_config,
+                         int* lds_bytes) {
+  if (!lds_bytes) return PT_ERR_NULL;
+  if (L < 1 || L > pt::kMaxL || K < 1 || K > pt::kMaxK) return PT_ERR_SHAPE;
+  switch (kernel_id) {
+    case PT_KERNEL_FWD:
+    case PT_KERNEL_DX:
+      if (!pt::valid_wpb(block_config)) return PT_ERR_CONFIG;
+      *lds_bytes = block_config * pt::kStageBytes;
+      return PT_OK;
+    case PT_KERNEL_DK:
+      if (!pt::valid_dk_threads(block_config)) return PT_ERR_CONFIG;
+      *lds_bytes = (int)((block_config / pt::kWave) *
+                         (pt::dk_algo(L, K) == pt::kDkMfma
+                              ? pt::mfma_lds_per_wave(L)
+                              : (size_t)pt::kStageBytes));
+      return PT_OK;
+    case PT_KERNEL_DK_REDUCE:
+      *lds_bytes = 0;
+      return PT_OK;
+    default:
+      return PT_ERR_CONFIG;
+  }
+}
+
+}  // extern "C"

@@ -1,4 +1,4 @@
-// dwconv1d.hip — depthwise Conv1D for short rows (L <= 48, K <= 48), FP32,
+// dwconv1d_kernels.hpp — device code of the depthwise Conv1D for short rows (L <= 48, K <= 48), FP32,
 // written for MI355X (gfx950, CDNA4, wave64).
 //
 // Paths (semantics of kernels/warp_tiled_ampere.py:372-619 in the reference):
@@ -36,6 +36,8 @@
 // one store per tap into a [H, K, num_btiles] workspace followed by a
 // fixed-order reduction kernel (deterministic variant,
 // kernels/warp_tiled_noatomic_optimized.py:881-1160).
+
+#pragma once
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -269,20 +271,35 @@ struct TileIO {
     wave_lds_sync();
   }
 
-  // Whole tile HBM -> lanes (row r -> lane r, dst[0 .. LMAX)).
+  // Whole tile HBM -> registers (all chunks' loads in flight at once).
+  __device__ static __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rs,
+                                                   uint32_t rstride, int nrows,
+                                                   int L, int lane, int vec,
+                                                   float4* buf) {
+    static_for<0, G::nchunks>([&](auto cc) {
+      constexpr int c = decltype(cc)::value;
+      load<c>(rs, rstride, nrows, L, lane, vec, buf + 4 * c);
+    });
+  }
+
+  // Registers of load_tile -> lanes (row r -> lane r, dst[0 .. LMAX)).
+  __device__ static __forceinline__ void transpose_tile(float* stage, int lane,
+                                                        const float4* buf,
+                                                        float* dst) {
+    static_for<0, G::nchunks>([&](auto cc) {
+      constexpr int c = decltype(cc)::value;
+      transpose<c>(stage, lane, buf + 4 * c, dst + kChunk * c);
+    });
+  }
+
+  // Whole tile HBM -> lanes.
   __device__ static __forceinline__ void load_rows(__amdgpu_buffer_rsrc_t rs,
                                                    uint32_t rstride, int nrows,
                                                    int L, int lane, int vec,
                                                    float* stage, float* dst) {
     float4 buf[LMAX / 4];
-    static_for<0, G::nchunks>([&](auto cc) {
-      constexpr int c = decltype(cc)::value;
-      load<c>(rs, rstride, nrows, L, lane, vec, buf + 4 * c);
-    });
-    static_for<0, G::nchunks>([&](auto cc) {
-      constexpr int c = decltype(cc)::value;
-      transpose<c>(stage, lane, buf + 4 * c, dst + kChunk * c);
-    });
+    load_tile(rs, rstride, nrows, L, lane, vec, buf);
+    transpose_tile(stage, lane, buf, dst);
   }
 
   // One chunk HBM -> lanes.
@@ -320,15 +337,19 @@ __device__ __forceinline__ void load_taps(const float* __restrict__ w, int h,
 }
 
 // ---------------------------------------------------------------------------
-// FWD / DX: one 64-row tile per wave. Workgroup = `wpb` waves on consecutive
-// channels of the same 64-sample batch chunk; grid = ceil(H/wpb) channel
-// groups x ceil(B/64) chunks, flattened and XCD-remapped.
+// FWD / DX. A wave owns channel h and `tpw` consecutive 64-sample batch
+// chunks (tiles); while it computes tile i, the HBM loads of tile i+1 are
+// already in flight in registers. Workgroup = `wpb` waves on consecutive
+// channels of the same chunk range (their rows are adjacent in memory);
+// grid = ceil(H/wpb) channel groups x ceil(nchunks/tpw) chunk groups,
+// flattened and XCD-remapped.
 // ---------------------------------------------------------------------------
-template <int LMAX, int KB, bool DX>
+template <int LMAX, int KB, bool DX, bool VEC>
 __global__ __launch_bounds__(1024) void dwconv_rows_kernel(
     const float* __restrict__ in, const float* __restrict__ w,
     float* __restrict__ out, int B, int H, int L, int K, int wpb, int ngroups,
-    uint32_t nblocks, int vec) {
+    int tpw, uint32_t nblocks) {
+  constexpr int vec = VEC ? 1 : 0;
   using W = Window<LMAX, KB, DX>;
   using IO = TileIO<LMAX>;
   using G = RowGeo<LMAX>;
@@ -338,43 +359,58 @@ __global__ __launch_bounds__(1024) void dwconv_rows_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t blk = xcd_remap(blockIdx.x, nblocks);
   const int group = (int)(blk % (uint32_t)ngroups);
-  const int chunk = (int)(blk / (uint32_t)ngroups);
+  const int cgroup = (int)(blk / (uint32_t)ngroups);
   const int h = group * wpb + wave;
   if (h >= H) return;  // wave-uniform; no workgroup barrier below
-  const int b0 = chunk * kWave;
-  const int nrows = min(kWave, B - b0);
+  const int nchunks = (B + kWave - 1) / kWave;
+  const int c_begin = cgroup * tpw;
+  const int c_end = min(nchunks, c_begin + tpw);
   const uint32_t rstride = (uint32_t)H * (uint32_t)L;
-  const size_t row0 = ((size_t)b0 * (size_t)H + (size_t)h) * (size_t)L;
+  const size_t hoff = (size_t)h * (size_t)L;
+  const size_t chunk_elems = (size_t)kWave * rstride;
   float* stage = lds + wave * kStageFloats;
 
   float wt[W::n];
   load_taps<W::lo, W::n, DX>(w, h, H, K, lane, wt);
 
-  float xr[LMAX];
-  IO::load_rows(make_rsrc(in + row0), rstride, nrows, L, lane, vec, stage, xr);
+  float4 buf[LMAX / 4];
+  IO::load_tile(make_rsrc(in + (size_t)c_begin * chunk_elems + hoff), rstride,
+                min(kWave, B - c_begin * kWave), L, lane, vec, buf);
 
-  const __amdgpu_buffer_rsrc_t orsrc = make_rsrc(out + row0);
-  // Per output: the reference's fmaf chain, taps in reference order
-  // (FWD: j = p + m ascending <=> i ascending; DX: j = p - m ascending <=>
-  // i descending). Computed and stored one 16-column chunk at a time.
-  static_for<0, G::nchunks>([&](auto cc) {
-    constexpr int c = decltype(cc)::value;
-    constexpr int nc = G::cols(c);
-    float yc[kChunk];
-#pragma unroll
-    for (int tt = 0; tt < nc; ++tt) {
-      const int t = kChunk * c + tt;
-      float acc = 0.0f;
-#pragma unroll
-      for (int ii = 0; ii < W::n; ++ii) {
-        const int i = DX ? (W::n - 1 - ii) : ii;
-        const int s = t + W::lo + i;
-        if (s >= 0 && s < LMAX) acc = fmaf(xr[s], wt[i], acc);
-      }
-      yc[tt] = acc;
+  for (int c0 = c_begin; c0 < c_end; ++c0) {
+    // readfirstlane keeps per-tile bases opaque to loop strength reduction.
+    const int c = __builtin_amdgcn_readfirstlane(c0);
+    const int nrows = min(kWave, B - c * kWave);
+    float xr[LMAX];
+    IO::transpose_tile(stage, lane, buf, xr);
+    if (c + 1 < c_end) {
+      IO::load_tile(make_rsrc(in + (size_t)(c + 1) * chunk_elems + hoff),
+                    rstride, min(kWave, B - (c + 1) * kWave), L, lane, vec, buf);
     }
-    IO::template store<c>(orsrc, rstride, nrows, L, lane, vec, stage, yc);
-  });
+    const __amdgpu_buffer_rsrc_t orsrc =
+        make_rsrc(out + (size_t)c * chunk_elems + hoff);
+    // Per output: the reference's fmaf chain, taps in reference order
+    // (FWD: j = p + m ascending <=> i ascending; DX: j = p - m ascending <=>
+    // i descending). Computed and stored one 16-column chunk at a time.
+    static_for<0, G::nchunks>([&](auto cc) {
+      constexpr int cx = decltype(cc)::value;
+      constexpr int nc = G::cols(cx);
+      float yc[kChunk];
+#pragma unroll
+      for (int tt = 0; tt < nc; ++tt) {
+        const int t = kChunk * cx + tt;
+        float acc = 0.0f;
+#pragma unroll
+        for (int ii = 0; ii < W::n; ++ii) {
+          const int i = DX ? (W::n - 1 - ii) : ii;
+          const int s = t + W::lo + i;
+          if (s >= 0 && s < LMAX) acc = fmaf(xr[s], wt[i], acc);
+        }
+        yc[tt] = acc;
+      }
+      IO::template store<cx>(orsrc, rstride, nrows, L, lane, vec, stage, yc);
+    });
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -404,11 +440,12 @@ __device__ __forceinline__ float wave_sum(float v) {
 // a time and is consumed at once. det == 0: one atomic add per tap per
 // workgroup into dk. det != 0: partials[(h*K + j) * nbt + bt] (no atomics).
 // ---------------------------------------------------------------------------
-template <int LMAX, int KB>
+template <int LMAX, int KB, bool VEC>
 __global__ __launch_bounds__(kMaxDkThreads) void dwconv_dk_kernel(
     const float* __restrict__ gy, const float* __restrict__ x,
     float* __restrict__ dst, int B, int H, int L, int K, int R, int nbt,
-    uint32_t nblocks, int vec, int det) {
+    uint32_t nblocks, int det) {
+  constexpr int vec = VEC ? 1 : 0;
   using W = Window<LMAX, KB, false>;
   using IO = TileIO<LMAX>;
   using G = RowGeo<LMAX>;
@@ -483,331 +520,127 @@ __global__ __launch_bounds__(kMaxDkThreads) void dwconv_dk_kernel(
   }
 }
 
-// Pass 2 of the deterministic DK: one wave per coefficient, lanes sum the
-// batch-tile partials in a fixed order, then a fixed wave reduction.
-__global__ __launch_bounds__(256) void dk_reduce_kernel(
-    const float* __restrict__ partials, float* __restrict__ dk, int ncoef,
-    int nbt) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int coef = blockIdx.x * (blockDim.x / kWave) + (int)(threadIdx.x / kWave);
-  if (coef >= ncoef) return;
-  const float* p = partials + (size_t)coef * (size_t)nbt;
-  float acc = 0.0f;
-  for (int q = lane; q < nbt; q += kWave) acc += p[q];
-  acc = wave_sum(acc);
-  if (lane == 0) dk[coef] = acc;
-}
-
-__global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p,
-                                                        int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0.0f;
-}
-
 // ---------------------------------------------------------------------------
-// Dispatch tables: row buckets 8..48 (step 8) x tap buckets below.
+// DK on the matrix cores. For channel h, D[t][s] = sum_b dy[b,t] * x[b,s] is
+// a GEMM whose contraction runs over the batch, so v_mfma_f32_16x16x4_f32
+// takes its operands straight from row-major HBM: for a step of 4 samples,
+// lane l holds dy[b0 + l/16][16*tt + l%16] (A, 16 t x 4 b) and
+// x[b0 + l/16][16*ts + l%16] (B, 4 b x 16 s); D is NT x NT tiles of 16 x 16
+// (NT = LMAX/16), lane l, register r of a tile holding
+// D[16*tt + 4*(l/16) + r][16*ts + l%16]. After its rows, a wave writes D to
+// LDS and lane j sums the diagonal s - t = j - p over the valid t
+// (benchmark/diagnose_dk_correctness.py:21), in a fixed order. Workgroup =
+// (h, batch tile of wpb * rpw samples); then the same LDS reduction over
+// waves and per-workgroup atomic / partial store as the VALU kernel.
 // ---------------------------------------------------------------------------
-constexpr int kNumLB = 6;
-constexpr int kNumKB = 7;
-constexpr int kKBuckets[kNumKB] = {4, 8, 16, 24, 32, 40, 48};
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-using RowsFn = void (*)(const float*, const float*, float*, int, int, int, int,
-                        int, int, uint32_t, int);
-using DkFn = void (*)(const float*, const float*, float*, int, int, int, int,
-                      int, int, uint32_t, int, int);
-
-#define PT_ROWS_ROW(LM, DX)                                                   \
-  {                                                                           \
-    &dwconv_rows_kernel<LM, 4, DX>, &dwconv_rows_kernel<LM, 8, DX>,           \
-        &dwconv_rows_kernel<LM, 16, DX>, &dwconv_rows_kernel<LM, 24, DX>,     \
-        &dwconv_rows_kernel<LM, 32, DX>, &dwconv_rows_kernel<LM, 40, DX>,     \
-        &dwconv_rows_kernel<LM, 48, DX>                                       \
-  }
-#define PT_ROWS_TABLE(DX)                                                     \
-  {                                                                           \
-    PT_ROWS_ROW(8, DX), PT_ROWS_ROW(16, DX), PT_ROWS_ROW(24, DX),             \
-        PT_ROWS_ROW(32, DX), PT_ROWS_ROW(40, DX), PT_ROWS_ROW(48, DX)         \
-  }
-#define PT_DK_ROW(LM)                                                         \
-  {                                                                           \
-    &dwconv_dk_kernel<LM, 4>, &dwconv_dk_kernel<LM, 8>,                       \
-        &dwconv_dk_kernel<LM, 16>, &dwconv_dk_kernel<LM, 24>,                 \
-        &dwconv_dk_kernel<LM, 32>, &dwconv_dk_kernel<LM, 40>,                 \
-        &dwconv_dk_kernel<LM, 48>                                             \
-  }
-
-static const RowsFn kFwdTable[kNumLB][kNumKB] = PT_ROWS_TABLE(false);
-static const RowsFn kDxTable[kNumLB][kNumKB] = PT_ROWS_TABLE(true);
-static const DkFn kDkTable[kNumLB][kNumKB] = {PT_DK_ROW(8),  PT_DK_ROW(16),
-                                              PT_DK_ROW(24), PT_DK_ROW(32),
-                                              PT_DK_ROW(40), PT_DK_ROW(48)};
-
-static int lbucket_index(int L) { return (L + 7) / 8 - 1; }
-static int kbucket_index(int K) {
-  for (int i = 0; i < kNumKB; ++i)
-    if (K <= kKBuckets[i]) return i;
-  return kNumKB - 1;
-}
-
-// ---------------------------------------------------------------------------
-// Host-side validation and launch geometry
-// ---------------------------------------------------------------------------
-static int check_shape(int B, int H, int L, int K) {
-  if (B < 0 || H < 0 || L < 1 || K < 1) return PT_ERR_SHAPE;
-  if (L > kMaxL || K > kMaxK) return PT_ERR_SHAPE;
-  const long long elems = (long long)B * (long long)H * (long long)L;
-  if (elems >= (1LL << 31)) return PT_ERR_SHAPE;
-  if ((long long)H * K * 4 >= (1LL << 31)) return PT_ERR_SHAPE;
-  // a wave's 64-row tile must span < 2 GiB (buffer offsets, see kOob)
-  if ((long long)kWave * H * L * 4 >= (1LL << 31)) return PT_ERR_SHAPE;
-  return PT_OK;
-}
-
-static bool aligned(const void* p, uintptr_t a) {
-  return ((uintptr_t)p & (a - 1)) == 0;
-}
-
-// Samples per wave chunk is 64; a DK workgroup covers wpb * R chunks. R is
-// chosen from the shape so that the grid holds about 2048 workgroups' worth
-// of chunks (8 per CU), which keeps atomics per tap low (H * nbt * K total)
-// without starving the 256 CUs.
-struct DkGeom {
-  int wpb, R, nbt;
-  long long nblocks;
+template <int LMAX>
+struct MfmaGeo {
+  static constexpr int nt = (LMAX + 15) / 16;   // 16-wide tiles per side
+  static constexpr int dim = 16 * nt;
+  static constexpr int dstride = dim + 1;       // LDS row stride of D
+  static constexpr int dfloats = dim * dstride; // per-wave D in LDS
 };
 
-static DkGeom dk_geometry(int B, int H, int threads) {
-  DkGeom g;
-  g.wpb = threads / kWave;
-  const long long chunks_per_h = ((long long)B + kWave - 1) / kWave;
-  const long long total = chunks_per_h * (long long)H;
-  long long R = total / ((long long)g.wpb * 2048);
-  if (R < 1) R = 1;
-  if (R > 16) R = 16;
-  const long long per_wg = (long long)g.wpb * R;
-  if (R > (chunks_per_h + g.wpb - 1) / g.wpb) {
-    R = (chunks_per_h + g.wpb - 1) / g.wpb;
-    if (R < 1) R = 1;
+template <int LMAX>
+__global__ __launch_bounds__(1024) void dwconv_dk_mfma_kernel(
+    const float* __restrict__ gy, const float* __restrict__ x,
+    float* __restrict__ dst, int B, int H, int L, int K, int rpw, int nbt,
+    uint32_t nblocks, int det) {
+  using M = MfmaGeo<LMAX>;
+  constexpr int NT = M::nt;
+  constexpr int kUnroll = 4;                    // 4-sample steps per iteration
+  extern __shared__ float lds[];
+  __shared__ float red[kMaxWaves][kMaxK];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wpb = blockDim.x / kWave;
+  const uint32_t blk = xcd_remap(blockIdx.x, nblocks);
+  const int h = (int)(blk % (uint32_t)H);
+  const int bt = (int)(blk / (uint32_t)H);
+  const uint32_t rstride = (uint32_t)H * (uint32_t)L;
+
+  const int b_begin = bt * wpb * rpw + wave * rpw;
+  const int b_end = min(B, b_begin + rpw);
+  const int nrow = max(0, b_end - b_begin);
+
+  f32x4 acc[NT][NT];
+#pragma unroll
+  for (int a = 0; a < NT; ++a)
+#pragma unroll
+    for (int b = 0; b < NT; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (nrow > 0) {
+    const size_t row0 = ((size_t)b_begin * (size_t)H + (size_t)h) * (size_t)L;
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(gy + row0);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + row0);
+    const int kq = lane >> 4;   // sample within a 4-sample step
+    const int col = lane & 15;  // column within a 16-wide tile
+    const uint32_t off = ((uint32_t)kq * rstride + (uint32_t)col) * 4u;
+    const uint32_t step_bytes = 4u * rstride * 4u;
+    const int nsteps = (nrow + 3) / 4;
+    for (int s0 = 0; s0 < nsteps; s0 += kUnroll) {
+      const int sb = __builtin_amdgcn_readfirstlane(s0);
+      float av[kUnroll][NT], bv[kUnroll][NT];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const uint32_t soff = (uint32_t)(sb + u) * step_bytes;
+        const bool row_ok = (sb + u) * 4 + kq < nrow;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+          const bool ok = row_ok && 16 * tt + col < L;
+          const uint32_t o = ok ? off + 64u * tt : kOob;
+          av[u][tt] = buf_load1(gr, o, soff);
+          bv[u][tt] = buf_load1(xr, o, soff);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+        for (int a = 0; a < NT; ++a)
+#pragma unroll
+          for (int b = 0; b < NT; ++b)
+            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                av[u][a], bv[u][b], acc[a][b], 0, 0, 0);
+    }
   }
-  (void)per_wg;
-  g.R = (int)R;
-  const long long tile = (long long)g.wpb * g.R * kWave;
-  g.nbt = (int)(((long long)B + tile - 1) / tile);
-  if (g.nbt < 1) g.nbt = 1;
-  g.nblocks = (long long)g.nbt * H;
-  return g;
-}
 
-static bool valid_wpb(int wpb) {
-  return wpb == 1 || wpb == 2 || wpb == 4 || wpb == 8 || wpb == 16;
-}
-
-static bool valid_dk_threads(int t) {
-  return t >= kWave && t <= kMaxDkThreads && (t % kWave) == 0;
-}
-
-static int launch(const void* fn, uint32_t grid, uint32_t block, size_t lds,
-                  void* stream, void** args) {
-  hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(block), args, lds,
-                                 (hipStream_t)stream);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return PT_ERR_HIP;
+  // D -> LDS, then diagonal sums (lane j: tap j).
+  float* dmat = lds + wave * M::dfloats;
+  {
+    const int rq = 4 * (lane >> 4);
+    const int col = lane & 15;
+#pragma unroll
+    for (int a = 0; a < NT; ++a)
+#pragma unroll
+      for (int b = 0; b < NT; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          dmat[(16 * a + rq + r) * M::dstride + 16 * b + col] = acc[a][b][r];
   }
-  return PT_OK;
-}
+  wave_lds_sync();
+  if (lane < K) {
+    const int m = lane - (K >> 1);
+    const int t0 = max(0, -m);
+    const int t1 = min(L, L - m);
+    float v = 0.0f;
+    for (int t = t0; t < t1; ++t) v += dmat[t * M::dstride + t + m];
+    red[wave][lane] = v;
+  }
+  __syncthreads();
 
-static int zero_fill(float* p, int n, void* stream) {
-  if (n <= 0) return PT_OK;
-  void* args[] = {&p, &n};
-  const uint32_t grid = (uint32_t)((n + 255) / 256);
-  return launch((const void*)&fill_zero_kernel, grid, 256, 0, stream, args);
-}
-
-static int rows_path(bool dx, const float* in, const float* w, float* out,
-                     int B, int H, int L, int K, int wpb, void* stream) {
-  int st = check_shape(B, H, L, K);
-  if (st != PT_OK) return st;
-  if (!valid_wpb(wpb)) return PT_ERR_CONFIG;
-  if (B == 0 || H == 0) return PT_OK;  // empty tensors may have NULL data
-  if (!in || !w || !out) return PT_ERR_NULL;
-  if (!aligned(in, 4) || !aligned(w, 4) || !aligned(out, 4))
-    return PT_ERR_ALIGN;
-  const int ngroups = (H + wpb - 1) / wpb;
-  const long long nchunks = ((long long)B + kWave - 1) / kWave;
-  const long long nb = nchunks * ngroups;
-  if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
-  uint32_t nblocks = (uint32_t)nb;
-  int vec = (L % 4 == 0) && aligned(in, 16) && aligned(out, 16);
-  RowsFn fn = (dx ? kDxTable : kFwdTable)[lbucket_index(L)][kbucket_index(K)];
-  void* args[] = {&in, &w, &out, &B, &H, &L, &K, &wpb, (void*)&ngroups,
-                  &nblocks, &vec};
-  return launch((const void*)fn, nblocks, (uint32_t)(wpb * kWave),
-                (size_t)wpb * kStageBytes, stream, args);
-}
-
-static int dk_path(bool det, const float* gy, const float* x, float* dst,
-                   int B, int H, int L, int K, int threads, const DkGeom& g,
-                   void* stream) {
-  uint32_t nblocks = (uint32_t)g.nblocks;
-  int vec = (L % 4 == 0) && aligned(gy, 16) && aligned(x, 16);
-  int R = g.R, nbt = g.nbt, d = det ? 1 : 0;
-  DkFn fn = kDkTable[lbucket_index(L)][kbucket_index(K)];
-  void* args[] = {&gy, &x, &dst, &B, &H, &L, &K, &R, &nbt, &nblocks, &vec, &d};
-  return launch((const void*)fn, nblocks, (uint32_t)threads,
-                (size_t)g.wpb * kStageBytes, stream, args);
-}
-
-static const void* kernel_for(int kernel_id, int L, int K) {
-  if (L < 1 || L > kMaxL || K < 1 || K > kMaxK) return nullptr;
-  const int li = lbucket_index(L), ki = kbucket_index(K);
-  switch (kernel_id) {
-    case PT_KERNEL_FWD: return (const void*)kFwdTable[li][ki];
-    case PT_KERNEL_DX: return (const void*)kDxTable[li][ki];
-    case PT_KERNEL_DK: return (const void*)kDkTable[li][ki];
-    case PT_KERNEL_DK_REDUCE: return (const void*)&dk_reduce_kernel;
-    default: return nullptr;
+  const int j = threadIdx.x;
+  if (j < K) {
+    float v = 0.0f;
+    for (int wv = 0; wv < wpb; ++wv) v += red[wv][j];
+    if (det) {
+      dst[((size_t)h * K + j) * (size_t)nbt + bt] = v;
+    } else {
+      atomicAdd(dst + (size_t)h * K + j, v);
+    }
   }
 }
 
 }  // namespace pt
-
-// ---------------------------------------------------------------------------
-// C ABI
-// ---------------------------------------------------------------------------
-extern "C" {
-
-int pt_abi_version(void) { return PT_ABI_VERSION; }
-
-const char* pt_status_string(int status) {
-  switch (status) {
-    case PT_OK: return "ok";
-    case PT_ERR_NULL: return "null pointer argument";
-    case PT_ERR_SHAPE: return "invalid shape (need 1<=L<=48, 1<=K<=48, B,H>=0, B*H*L<2^31)";
-    case PT_ERR_CONFIG: return "unsupported launch configuration";
-    case PT_ERR_WORKSPACE: return "workspace missing or too small";
-    case PT_ERR_HIP: return "HIP runtime launch error";
-    case PT_ERR_ALIGN: return "pointer not 4-byte aligned";
-    default: return "unknown status";
-  }
-}
-
-int pt_dwconv1d_fwd_f32(const float* x, const float* w, float* y, int B, int H,
-                        int L, int K, int waves_per_block, void* stream) {
-  return pt::rows_path(false, x, w, y, B, H, L, K, waves_per_block, stream);
-}
-
-int pt_dwconv1d_dx_f32(const float* dy, const float* w, float* dx, int B,
-                       int H, int L, int K, int waves_per_block, void* stream) {
-  return pt::rows_path(true, dy, w, dx, B, H, L, K, waves_per_block, stream);
-}
-
-int pt_dwconv1d_dk_atomic_f32(const float* dy, const float* x, float* dk,
-                              int B, int H, int L, int K,
-                              int threads_per_block, int zero_first,
-                              void* stream) {
-  int st = pt::check_shape(B, H, L, K);
-  if (st != PT_OK) return st;
-  if (!pt::valid_dk_threads(threads_per_block)) return PT_ERR_CONFIG;
-  if (H == 0) return PT_OK;  // empty tensors may have NULL data
-  if (!dk) return PT_ERR_NULL;
-  if (!pt::aligned(dk, 4)) return PT_ERR_ALIGN;
-  if (zero_first) {
-    st = pt::zero_fill(dk, H * K, stream);
-    if (st != PT_OK) return st;
-  }
-  if (B == 0) return PT_OK;
-  if (!dy || !x) return PT_ERR_NULL;
-  if (!pt::aligned(dy, 4) || !pt::aligned(x, 4)) return PT_ERR_ALIGN;
-  const pt::DkGeom g = pt::dk_geometry(B, H, threads_per_block);
-  if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
-  return pt::dk_path(false, dy, x, dk, B, H, L, K, threads_per_block, g,
-                     stream);
-}
-
-int pt_dwconv1d_dk_det_workspace_bytes(int B, int H, int L, int K,
-                                       int threads_per_block, size_t* bytes) {
-  if (!bytes) return PT_ERR_NULL;
-  int st = pt::check_shape(B, H, L, K);
-  if (st != PT_OK) return st;
-  if (!pt::valid_dk_threads(threads_per_block)) return PT_ERR_CONFIG;
-  if (B == 0 || H == 0) {
-    *bytes = 0;
-    return PT_OK;
-  }
-  const pt::DkGeom g = pt::dk_geometry(B, H, threads_per_block);
-  *bytes = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
-  return PT_OK;
-}
-
-int pt_dwconv1d_dk_det_f32(const float* dy, const float* x, float* dk,
-                           void* workspace, size_t workspace_bytes, int B,
-                           int H, int L, int K, int threads_per_block,
-                           void* stream) {
-  int st = pt::check_shape(B, H, L, K);
-  if (st != PT_OK) return st;
-  if (!pt::valid_dk_threads(threads_per_block)) return PT_ERR_CONFIG;
-  if (H == 0) return PT_OK;  // empty tensors may have NULL data
-  if (!dk) return PT_ERR_NULL;
-  if (!pt::aligned(dk, 4)) return PT_ERR_ALIGN;
-  if (B == 0) return pt::zero_fill(dk, H * K, stream);
-  if (!dy || !x) return PT_ERR_NULL;
-  if (!pt::aligned(dy, 4) || !pt::aligned(x, 4)) return PT_ERR_ALIGN;
-  const pt::DkGeom g = pt::dk_geometry(B, H, threads_per_block);
-  if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
-  const size_t need = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
-  if (!workspace || workspace_bytes < need) return PT_ERR_WORKSPACE;
-  if (!pt::aligned(workspace, 4)) return PT_ERR_ALIGN;
-  float* partials = (float*)workspace;
-  st = pt::dk_path(true, dy, x, partials, B, H, L, K, threads_per_block, g,
-                   stream);
-  if (st != PT_OK) return st;
-  int ncoef = H * K;
-  int nbt = g.nbt;
-  const float* cp = partials;
-  void* args[] = {&cp, &dk, &ncoef, &nbt};
-  const uint32_t grid = (uint32_t)((ncoef + 3) / 4);
-  return pt::launch((const void*)&pt::dk_reduce_kernel, grid, 256, 0, stream,
-                    args);
-}
-
-int pt_kernel_attributes(int kernel_id, int L, int K, int* regs,
-                         int* lds_bytes, int* scratch_bytes,
-                         int* max_threads) {
-  const void* fn = pt::kernel_for(kernel_id, L, K);
-  if (!fn) return PT_ERR_CONFIG;
-  hipFuncAttributes a;
-  if (hipFuncGetAttributes(&a, fn) != hipSuccess) {
-    (void)hipGetLastError();
-    return PT_ERR_HIP;
-  }
-  if (regs) *regs = a.numRegs;
-  if (lds_bytes) *lds_bytes = (int)a.sharedSizeBytes;
-  if (scratch_bytes) *scratch_bytes = (int)a.localSizeBytes;
-  if (max_threads) *max_threads = a.maxThreadsPerBlock;
-  return PT_OK;
-}
-
-int pt_dynamic_lds_bytes(int kernel_id, int L, int K, int block_config,
-                         int* lds_bytes) {
-  if (!lds_bytes) return PT_ERR_NULL;
-  if (L < 1 || L > pt::kMaxL || K < 1 || K > pt::kMaxK) return PT_ERR_SHAPE;
-  switch (kernel_id) {
-    case PT_KERNEL_FWD:
-    case PT_KERNEL_DX:
-      if (!pt::valid_wpb(block_config)) return PT_ERR_CONFIG;
-      *lds_bytes = block_config * pt::kStageBytes;
-      return PT_OK;
-    case PT_KERNEL_DK:
-      if (!pt::valid_dk_threads(block_config)) return PT_ERR_CONFIG;
-      *lds_bytes = (block_config / pt::kWave) * pt::kStageBytes;
-      return PT_OK;
-    case PT_KERNEL_DK_REDUCE:
-      *lds_bytes = 0;
-      return PT_OK;
-    default:
-      return PT_ERR_CONFIG;
-  }
-}
-
-}  // extern "C"

@@ -1,0 +1,32 @@
+// dwconv1d_tables.hpp — dispatch tables of the depthwise Conv1D kernels.
+// Each table is defined (and its kernels instantiated) in its own
+// translation unit so the build compiles them in parallel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pt {
+
+constexpr int kNumLB = 6;  // row buckets 8, 16, ..., 48
+constexpr int kNumKB = 7;  // tap buckets below
+constexpr int kKBuckets[kNumKB] = {4, 8, 16, 24, 32, 40, 48};
+
+using RowsFn = void (*)(const float*, const float*, float*, int, int, int, int,
+                        int, int, int, uint32_t);
+using DkFn = void (*)(const float*, const float*, float*, int, int, int, int,
+                      int, int, uint32_t, int);
+using DkMfmaFn = void (*)(const float*, const float*, float*, int, int, int,
+                          int, int, int, uint32_t, int);
+
+// [row bucket][tap bucket]; V = 16-byte aligned rows (dwordx4), S = dword.
+extern const RowsFn kFwdTableV[kNumLB][kNumKB];
+extern const RowsFn kFwdTableS[kNumLB][kNumKB];
+extern const RowsFn kDxTableV[kNumLB][kNumKB];
+extern const RowsFn kDxTableS[kNumLB][kNumKB];
+extern const DkFn kDkTableV[kNumLB][kNumKB];
+extern const DkFn kDkTableS[kNumLB][kNumKB];
+// matrix-core DK by row bucket 16, 32, 48
+extern const DkMfmaFn kDkMfmaTable[3];
+
+}  // namespace pt

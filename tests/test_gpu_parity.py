@@ -85,6 +85,8 @@ SHAPES = [
     (5, 3, 48, 1),
     (129, 2, 45, 40),
     (64, 128, 48, 48),
+    (8000, 64, 48, 48),   # several tiles per wave, ragged last chunk group
+    (8000, 64, 37, 8),    # same, dword row path
 ]
 
 
@@ -103,8 +105,13 @@ def test_fwd_dx_bit_exact_and_fp64(rt, shape):
     assert oracle.normalized_max_abs(dx, oracle.dx_f64(dy, w)) < FWD_TOL
 
 
+@pytest.mark.parametrize("algo", ["auto", "valu", "mfma"])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "B{}H{}L{}K{}".format(*s))
-def test_dk_atomic_and_deterministic(rt, shape):
+def test_dk_atomic_and_deterministic(rt, shape, algo, monkeypatch):
+    """Both DK algorithms (VALU lane-per-row and matrix-core batch GEMM);
+    the library reads PATHTILE_DK_ALGO on every call."""
+    if algo != "auto":
+        monkeypatch.setenv("PATHTILE_DK_ALGO", algo)
     B, H, L, K = shape
     x, w, dy = _inputs(B, H, L, K, seed=2000 + B + H + L + K)
     xd, dyd = _dev(x, dy)
