@@ -207,6 +207,40 @@ static int zero_fill(float* p, int n, void* stream) {
   return launch((const void*)&fill_zero_kernel, grid, 256, 0, stream, args);
 }
 
+// LDS of one FWD/DX wave: a 64-row tile at padded stride LMAX + 4.
+static size_t rows_lds_per_wave(int L) {
+  const int lmax = 8 * (lbucket_index(L) + 1);
+  return (size_t)kWave * (size_t)(lmax + 4) * sizeof(float);
+}
+
+static int max_lds_per_block() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    dev = 0;
+  }
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock,
+                            dev) != hipSuccess ||
+      n <= 0) {
+    (void)hipGetLastError();
+    n = 64 * 1024;
+  }
+  if (dev >= 0 && dev < 64) cache[dev] = n;
+  return n;
+}
+
+static long long gcd_ll(long long a, long long b) {
+  while (b) {
+    const long long t = a % b;
+    a = b;
+    b = t;
+  }
+  return a;
+}
+
 static int rows_path(bool dx, const float* in, const float* w, float* out,
                      int B, int H, int L, int K, int wpb, void* stream) {
   int st = check_shape(B, H, L, K);
@@ -216,29 +250,32 @@ static int rows_path(bool dx, const float* in, const float* w, float* out,
   if (!in || !w || !out) return PT_ERR_NULL;
   if (!aligned(in, 4) || !aligned(w, 4) || !aligned(out, 4))
     return PT_ERR_ALIGN;
+  const size_t lds = (size_t)wpb * rows_lds_per_wave(L);
+  if (lds > (size_t)max_lds_per_block()) return PT_ERR_CONFIG;
   const bool vec = (L % 4 == 0) && aligned(in, 16) && aligned(out, 16);
+  if (wpb * kWave > rows_max_threads(8 * (lbucket_index(L) + 1), vec))
+    return PT_ERR_CONFIG;
   const int li = lbucket_index(L), ki = kbucket_index(K);
   RowsFn fn = dx ? (vec ? kDxTableV : kDxTableS)[li][ki]
                  : (vec ? kFwdTableV : kFwdTableS)[li][ki];
-  const size_t lds = (size_t)wpb * kStageBytes;
-  const int ngroups = (H + wpb - 1) / wpb;
-  const long long nchunks = ((long long)B + kWave - 1) / kWave;
-  // Tiles per wave: spread H * nchunks tiles over one round of resident
-  // waves, so each wave streams several tiles with its next tile's loads in
-  // flight.
-  const long long resident = (long long)blocks_per_cu((const void*)fn,
-                                                      wpb * kWave, lds) *
-                             wpb * num_cus();
-  long long tpw = ((long long)H * nchunks + resident - 1) / resident;
-  if (tpw < 1) tpw = 1;
-  if (tpw > nchunks) tpw = nchunks;
-  const long long ncg = (nchunks + tpw - 1) / tpw;
-  const long long nb = ncg * ngroups;
+  const long long R = (long long)B * H;
+  const long long ntiles = (R + kWave - 1) / kWave;
+  // Persistent grid: one round of resident workgroups, no more than there
+  // are tiles. Wave g takes tiles g, g + G, ...; lane i's channel stays
+  // fixed when G is a multiple of P = H / gcd(H, 64), so prefer such G.
+  long long nb = (long long)blocks_per_cu((const void*)fn, wpb * kWave, lds) *
+                 num_cus();
+  const long long need = (ntiles + wpb - 1) / wpb;
+  if (nb > need) nb = need;
+  const long long P = (long long)H / gcd_ll(H, kWave);
+  const long long Q = P / gcd_ll(P, wpb);  // blocks per channel period
+  if (Q > 1 && nb >= Q) nb = nb / Q * Q;
+  if (nb < 1) nb = 1;
   if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
   uint32_t nblocks = (uint32_t)nb;
-  int tpw_i = (int)tpw;
-  void* args[] = {&in, &w, &out, &B, &H, &L, &K, &wpb, (void*)&ngroups,
-                  &tpw_i, &nblocks};
+  uint32_t uR = (uint32_t)R, uT = (uint32_t)ntiles;
+  uint32_t lmagic = (uint32_t)(((1u << 20) + (uint32_t)L - 1) / (uint32_t)L);
+  void* args[] = {&in, &w, &out, &H, &L, &K, &uR, &uT, &lmagic};
   return launch((const void*)fn, nblocks, (uint32_t)(wpb * kWave), lds, stream,
                 args);
 }
@@ -401,7 +438,7 @@ int pt_dynamic_lds_bytes(int kernel_id, int L, int K, int block_config,
     case PT_KERNEL_FWD:
     case PT_KERNEL_DX:
       if (!pt::valid_wpb(block_config)) return PT_ERR_CONFIG;
-      *lds_bytes = block_config * pt::kStageBytes;
+      *lds_bytes = (int)(block_config * pt::rows_lds_per_wave(L));
       return PT_OK;
     case PT_KERNEL_DK:
       if (!pt::valid_dk_threads(block_config)) return PT_ERR_CONFIG;

@@ -337,79 +337,206 @@ __device__ __forceinline__ void load_taps(const float* __restrict__ w, int h,
 }
 
 // ---------------------------------------------------------------------------
-// FWD / DX. A wave owns channel h and `tpw` consecutive 64-sample batch
-// chunks (tiles); while it computes tile i, the HBM loads of tile i+1 are
-// already in flight in registers. Workgroup = `wpb` waves on consecutive
-// channels of the same chunk range (their rows are adjacent in memory);
-// grid = ceil(H/wpb) channel groups x ceil(nchunks/tpw) chunk groups,
-// flattened and XCD-remapped.
+// FWD / DX on contiguous tiles. [B, H, L] is read as R = B*H consecutive
+// rows of L floats; a tile is 64 consecutive rows (64*L*4 bytes, 256-byte
+// aligned), one per lane, so every HBM load/store instruction of a wave
+// covers 1 KiB of contiguous memory (dwordx4) and tiles never share a cache
+// line. Lane i's row r0 + i belongs to channel (r0 + i) % H; its taps sit in
+// VGPRs. The grid is persistent: wave g takes tiles g, g + G, g + 2G, ...
+// with G a multiple of H / gcd(H, 64) where possible, so a lane keeps its
+// channel (and its taps) for the whole kernel.
+//
+// Per tile: flat loads -> LDS (padded row stride S = LMAX + 4 floats, so the
+// ds_read_b128 of a lane's own row is bank-conflict free) -> own row into
+// VGPRs -> fmaf chain -> own output row into LDS -> flat reads -> stores.
+// The rows past the end of the tensor are outside the buffer resource's
+// num_records: their loads read 0 and their stores are dropped.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_n(const float* base,
+                                                              uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0,
+                                           (int)bytes, kRsrcWord3);
+}
+
+// Row / column of flat element e (< 64 * 48) of a tile with row length L:
+// row = floor(e * ceil(2^20 / L) / 2^20) is exact for e < 3072, L <= 48.
+__device__ __forceinline__ void flat_rc(uint32_t e, uint32_t L, uint32_t lmagic,
+                                        uint32_t& row, uint32_t& col) {
+  row = (e * lmagic) >> 20;
+  col = e - row * L;
+}
+
+// Lane-varying taps: lane's channel h, window offsets LO .. LO+N-1, zero
+// where j = p + m (FWD) or p - m (DX) falls outside [0, K).
+template <int LO, int N, bool DX>
+__device__ __forceinline__ void load_lane_taps(const float* __restrict__ w,
+                                               int h, int K, float* wt) {
+  const int p = K >> 1;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(w);
+  const uint32_t base = (uint32_t)h * (uint32_t)K;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int m = LO + i;
+    const int j = DX ? (p - m) : (p + m);
+    const bool ok = (unsigned)j < (unsigned)K;
+    wt[i] = buf_load1(r, ok ? (base + (uint32_t)j) * 4u : kOob, 0);
+  }
+}
+
+// Largest workgroup of the FWD/DX kernel. For LMAX >= 40 the LDS tile
+// (64 * (LMAX + 4) floats per wave) caps a CU at 12 waves anyway, so the
+// kernel may use the 168 VGPRs of 3 waves per SIMD (taps and row both live
+// in VGPRs); the dword path (rows not 16-byte aligned, an edge case) gets the
+// same budget for its per-element address arithmetic.
+constexpr int rows_max_threads(int lmax, bool vec) {
+  return (lmax >= 40 || !vec) ? 768 : 1024;
+}
+
 template <int LMAX, int KB, bool DX, bool VEC>
-__global__ __launch_bounds__(1024) void dwconv_rows_kernel(
+__global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kernel(
     const float* __restrict__ in, const float* __restrict__ w,
-    float* __restrict__ out, int B, int H, int L, int K, int wpb, int ngroups,
-    int tpw, uint32_t nblocks) {
-  constexpr int vec = VEC ? 1 : 0;
+    float* __restrict__ out, int H, int L, int K, uint32_t R, uint32_t ntiles,
+    uint32_t lmagic) {
   using W = Window<LMAX, KB, DX>;
-  using IO = TileIO<LMAX>;
-  using G = RowGeo<LMAX>;
+  constexpr int S = LMAX + 4;     // padded LDS row stride (floats)
+  constexpr int NV = LMAX / 4;    // dwordx4 steps per lane (vector path)
   extern __shared__ float lds[];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const uint32_t blk = xcd_remap(blockIdx.x, nblocks);
-  const int group = (int)(blk % (uint32_t)ngroups);
-  const int cgroup = (int)(blk / (uint32_t)ngroups);
-  const int h = group * wpb + wave;
-  if (h >= H) return;  // wave-uniform; no workgroup barrier below
-  const int nchunks = (B + kWave - 1) / kWave;
-  const int c_begin = cgroup * tpw;
-  const int c_end = min(nchunks, c_begin + tpw);
-  const uint32_t rstride = (uint32_t)H * (uint32_t)L;
-  const size_t hoff = (size_t)h * (size_t)L;
-  const size_t chunk_elems = (size_t)kWave * rstride;
-  float* stage = lds + wave * kStageFloats;
+  const uint32_t wpb = blockDim.x / kWave;
+  const uint32_t gwave = blockIdx.x * wpb + (uint32_t)wave;
+  const uint32_t nwaves = gridDim.x * wpb;
+  const uint32_t uL = (uint32_t)L;
+  const uint32_t tile_elems = (uint32_t)kWave * uL;
+  float* tile = lds + wave * (kWave * S);
 
   float wt[W::n];
-  load_taps<W::lo, W::n, DX>(w, h, H, K, lane, wt);
+  int hcur = -1;
 
-  float4 buf[LMAX / 4];
-  IO::load_tile(make_rsrc(in + (size_t)c_begin * chunk_elems + hoff), rstride,
-                min(kWave, B - c_begin * kWave), L, lane, vec, buf);
-
-  for (int c0 = c_begin; c0 < c_end; ++c0) {
+  for (uint32_t t0 = gwave; t0 < ntiles; t0 += nwaves) {
     // readfirstlane keeps per-tile bases opaque to loop strength reduction.
-    const int c = __builtin_amdgcn_readfirstlane(c0);
-    const int nrows = min(kWave, B - c * kWave);
-    float xr[LMAX];
-    IO::transpose_tile(stage, lane, buf, xr);
-    if (c + 1 < c_end) {
-      IO::load_tile(make_rsrc(in + (size_t)(c + 1) * chunk_elems + hoff),
-                    rstride, min(kWave, B - (c + 1) * kWave), L, lane, vec, buf);
-    }
-    const __amdgpu_buffer_rsrc_t orsrc =
-        make_rsrc(out + (size_t)c * chunk_elems + hoff);
-    // Per output: the reference's fmaf chain, taps in reference order
-    // (FWD: j = p + m ascending <=> i ascending; DX: j = p - m ascending <=>
-    // i descending). Computed and stored one 16-column chunk at a time.
-    static_for<0, G::nchunks>([&](auto cc) {
-      constexpr int cx = decltype(cc)::value;
-      constexpr int nc = G::cols(cx);
-      float yc[kChunk];
+    const uint32_t t = __builtin_amdgcn_readfirstlane(t0);
+    const uint32_t r0 = t * kWave;
+    const uint32_t nr = min((uint32_t)kWave, R - r0);
+    const uint32_t vbytes = nr * uL * 4u;
+    const size_t e0 = (size_t)r0 * (size_t)uL;
+    const __amdgpu_buffer_rsrc_t rin = make_rsrc_n(in + e0, vbytes);
+    const __amdgpu_buffer_rsrc_t rout = make_rsrc_n(out + e0, vbytes);
+
+    // Flat loads (all in flight at once), then scatter into padded rows.
+    if constexpr (VEC) {
+      float4 v[NV];
 #pragma unroll
-      for (int tt = 0; tt < nc; ++tt) {
-        const int t = kChunk * cx + tt;
-        float acc = 0.0f;
+      for (int k = 0; k < NV; ++k)
+        v[k] = buf_load4(rin, (uint32_t)(kWave * k + lane) * 16u, 0);
 #pragma unroll
-        for (int ii = 0; ii < W::n; ++ii) {
-          const int i = DX ? (W::n - 1 - ii) : ii;
-          const int s = t + W::lo + i;
-          if (s >= 0 && s < LMAX) acc = fmaf(xr[s], wt[i], acc);
+      for (int k = 0; k < NV; ++k) {
+        const uint32_t e = (uint32_t)(kWave * k + lane) * 4u;
+        if (e < tile_elems) {
+          uint32_t row, col;
+          flat_rc(e, uL, lmagic, row, col);
+          *reinterpret_cast<float4*>(tile + row * S + col) = v[k];
         }
-        yc[tt] = acc;
       }
-      IO::template store<cx>(orsrc, rstride, nrows, L, lane, vec, stage, yc);
-    });
+    } else {
+      // dword path (rows not 16-byte aligned): groups of 16 loads, each
+      // scattered before the next group is issued. The empty asm makes the
+      // lane index opaque inside the tile loop, so the 2 * LMAX per-element
+      // addresses are recomputed per tile instead of being hoisted out of the
+      // loop and pinned in VGPRs.
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+#pragma unroll
+      for (int g = 0; g < LMAX; g += 16) {
+        constexpr int kG = 16;
+        float v[kG];
+#pragma unroll
+        for (int k = 0; k < kG; ++k)
+          if (g + k < LMAX)
+            v[k] = buf_load1(rin, (uint32_t)(kWave * (g + k) + ln) * 4u, 0);
+#pragma unroll
+        for (int k = 0; k < kG; ++k) {
+          const uint32_t e = (uint32_t)(kWave * (g + k) + ln);
+          if (g + k < LMAX && e < tile_elems) {
+            uint32_t row, col;
+            flat_rc(e, uL, lmagic, row, col);
+            tile[row * S + col] = v[k];
+          }
+        }
+      }
+    }
+
+    // Channel of this lane's row; reload the taps when any lane's changed.
+    const int h = (int)((r0 + (uint32_t)lane) % (uint32_t)H);
+    if (__builtin_amdgcn_ballot_w64(h != hcur)) {
+      load_lane_taps<W::lo, W::n, DX>(w, h, K, wt);
+      hcur = h;
+    }
+
+    wave_lds_sync();
+    float xr[LMAX];
+#pragma unroll
+    for (int q = 0; q < NV; ++q) {
+      const float4 x4 = *reinterpret_cast<const float4*>(tile + lane * S + 4 * q);
+      xr[4 * q + 0] = x4.x;
+      xr[4 * q + 1] = x4.y;
+      xr[4 * q + 2] = x4.z;
+      xr[4 * q + 3] = x4.w;
+    }
+    if (L != LMAX) {  // columns >= L were not loaded in this tile
+#pragma unroll
+      for (int s = 0; s < LMAX; ++s) xr[s] = s < L ? xr[s] : 0.0f;
+    }
+    wave_lds_sync();
+
+    // The reference's fmaf chain per output, taps in reference order
+    // (FWD: j = p + m ascending <=> i ascending; DX: j = p - m ascending
+    // <=> i descending); four outputs at a time (four independent chains)
+    // go to the lane's own row.
+#pragma unroll
+    for (int t4 = 0; t4 < LMAX; t4 += 4) {
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ii = 0; ii < W::n; ++ii) {
+        const int i = DX ? (W::n - 1 - ii) : ii;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int s = t4 + u + W::lo + i;
+          if (s >= 0 && s < LMAX) acc[u] = fmaf(xr[s], wt[i], acc[u]);
+        }
+      }
+      *reinterpret_cast<float4*>(tile + lane * S + t4) =
+          make_float4(acc[0], acc[1], acc[2], acc[3]);
+    }
+    wave_lds_sync();
+
+    // Flat reads of the output rows, contiguous stores.
+    if constexpr (VEC) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const uint32_t e = (uint32_t)(kWave * k + lane) * 4u;
+        if (e < tile_elems) {
+          uint32_t row, col;
+          flat_rc(e, uL, lmagic, row, col);
+          const float4 y4 = *reinterpret_cast<const float4*>(tile + row * S + col);
+          buf_store4(y4, rout, e * 4u, 0);
+        }
+      }
+    } else {
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+#pragma unroll
+      for (int k = 0; k < LMAX; ++k) {
+        const uint32_t e = (uint32_t)(kWave * k + ln);
+        if (e < tile_elems) {
+          uint32_t row, col;
+          flat_rc(e, uL, lmagic, row, col);
+          buf_store1(tile[row * S + col], rout, e * 4u, 0);
+        }
+      }
+    }
+    wave_lds_sync();
   }
 }
 

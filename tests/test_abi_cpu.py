@@ -141,3 +141,27 @@ def test_library_is_not_linked_to_the_oracle():
                             text=True, check=True).stdout
     assert "oracle" not in needed
     assert "libamdhip64.so" in needed
+
+
+def test_flat_tile_row_magic_is_exact():
+    """The FWD/DX kernels split a flat tile element e (< 64 * 48) into
+    (row, col) as row = (e * ceil(2^20 / L)) >> 20; exact for every L <= 48."""
+    for L in range(1, 49):
+        magic = ((1 << 20) + L - 1) // L
+        for e in range(64 * L):
+            row = (e * magic) >> 20
+            assert row == e // L, (L, e)
+            assert (e * magic) < (1 << 32)
+
+
+def test_xcd_remap_is_a_bijection():
+    """Workgroup renumbering used by the dK kernels (8 XCDs, round-robin)."""
+    import random
+
+    def remap(p, n):
+        q, r = divmod(n, 8)
+        x, i = p % 8, p // 8
+        return x * (q + 1) + i if x < r else r * (q + 1) + (x - r) * q + i
+
+    for n in list(range(1, 130)) + [random.Random(1).randint(1, 50000) for _ in range(20)]:
+        assert sorted(remap(p, n) for p in range(n)) == list(range(n))
