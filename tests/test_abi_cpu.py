@@ -128,7 +128,7 @@ def test_workspace_bytes(lib):
     assert st == _lib.PT_OK and out.value == 0
     lds = ctypes.c_int(0)
     assert lib.pt_dynamic_lds_bytes(_lib.PT_KERNEL_FWD, 48, 48, 8, ctypes.byref(lds)) == 0
-    assert lds.value == 8 * 5120
+    assert lds.value == 8 * 64 * (48 + 4) * 4  # 64-row tile, padded stride
     assert lib.pt_dynamic_lds_bytes(_lib.PT_KERNEL_FWD, 48, 48, 3, ctypes.byref(lds)) == _lib.PT_ERR_CONFIG
 
 
