@@ -245,33 +245,40 @@ def main(argv=None) -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    coll = runtime.KernelEventCollector()
-    coll.enabled = True
+    # The contract's K steps (FWD, dX, zero + dK interleaved), wall-clocked
+    # between two synchronisations.
+    step_coll = runtime.KernelEventCollector()
+    step_coll.enabled = True
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step(coll)
+        step(step_coll)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
+    srows = step_coll.rows(synchronize=True)
+    step_paths = {ph: mean([r["runtime_ms"] for r in srows if r["phase"] == ph])
+                  for ph in ("fwd", "bwd_input", "bwd_weight")}
+
+    # Per-path loops, the reference's protocol (kernels/warp_tiled_ampere.py:
+    # 1059-1070; benchmark/benchmark_pathtile_candidate_sweep.py:274-317):
+    # K x FWD, then K x dX, then K x (zero outside the event + dK); plus dK
+    # including the zero-init as one call and the deterministic dK.
+    coll = runtime.KernelEventCollector()
+    coll.enabled = True
+    for _ in range(args.steps):
+        rt.launch_fwd(x, w, y, coll)
+    for _ in range(args.steps):
+        rt.launch_bwd_input(dy, w, dx, coll)
+    for _ in range(args.steps):
+        gk.zero_()
+        rt.launch_bwd_weight(dy, x, gk, K, coll)
+    for _ in range(args.steps):
+        rt.launch_bwd_weight(dy, x, gk, K, coll, zero_first=True)
+    for _ in range(args.steps):
+        rt.launch_bwd_weight_deterministic(dy, x, gk, K, coll)
     rows = coll.rows(synchronize=True)
     per = {ph: [r["runtime_ms"] for r in rows if r["phase"] == ph]
-           for ph in ("fwd", "bwd_input", "bwd_weight")}
+           for ph in ("fwd", "bwd_input", "bwd_weight", "bwd_weight_zero", "bwd_weight_det")}
     assert all(len(v) == args.steps for v in per.values())
-
-    # dK including the zero-init (one call: fill kernel + atomic kernel) and
-    # the deterministic two-pass dK, timed the same way after the steps.
-    extra = runtime.KernelEventCollector()
-    extra.enabled = True
-    for _ in range(args.warmup):
-        rt.launch_bwd_weight(dy, x, gk, K, zero_first=True)
-        rt.launch_bwd_weight_deterministic(dy, x, gk, K)
-    torch.cuda.synchronize()
-    for _ in range(args.steps):
-        rt.launch_bwd_weight(dy, x, gk, K, extra, zero_first=True)
-    for _ in range(args.steps):
-        rt.launch_bwd_weight_deterministic(dy, x, gk, K, extra)
-    erows = extra.rows(synchronize=True)
-    per["bwd_weight_zero"] = [r["runtime_ms"] for r in erows if r["phase"] == "bwd_weight_zero"]
-    per["bwd_weight_det"] = [r["runtime_ms"] for r in erows if r["phase"] == "bwd_weight_det"]
 
     nbytes = runtime.minimum_algorithmic_bytes(B, H, L, K)
     paths = {}
@@ -308,6 +315,11 @@ def main(argv=None) -> int:
             "dk_threads_per_block": cfg["dk_threads_per_block"],
             "launch_config_source": cfg["source"],
         },
+        "protocol": ("value = sum of per-path mean kernel times, each path in its own "
+                     "loop of `steps` launches (reference protocol); ms_per_step = wall "
+                     "time of `steps` interleaved FWD/dX/zero+dK steps"),
+        "step_paths_ms": {k: round(v, 5) for k, v in step_paths.items()},
+        "step_aggregate_ms": round(sum(step_paths.values()), 5),
         "aggregate_gbps": round(3 * nbytes / (agg / 1e3) / 1e9, 1),
         "aggregate_pct_peak": round(100 * 3 * nbytes / (agg / 1e3) / 1e9 / PEAK_HBM_GBPS, 2),
         "algorithmic_bytes_per_path": nbytes,

@@ -42,10 +42,6 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p,
 // Dispatch helpers
 // ---------------------------------------------------------------------------
 static int mfma_index(int L) { return (L + 15) / 16 - 1; }
-static size_t mfma_lds_per_wave(int L) {
-  const int dim = 16 * (mfma_index(L) + 1);
-  return (size_t)dim * (size_t)(dim + 1) * sizeof(float);
-}
 static int lbucket_index(int L) { return (L + 7) / 8 - 1; }
 static int kbucket_index(int K) {
   for (int i = 0; i < kNumKB; ++i)
@@ -122,25 +118,27 @@ static int blocks_per_cu(const void* fn, int block, size_t lds) {
 }
 
 // --- DK algorithm ----------------------------------------------------------
-// VALU (lane-per-row) or matrix-core (batch-contraction GEMM) kernel. The
-// matrix-core kernel computes every (t, s) pair of the row window, so it wins
-// for wide tap windows; PATHTILE_DK_ALGO=valu|mfma overrides the choice.
+// Matrix-core (batch-contraction GEMM) kernel by default: it computes every
+// (t, s) pair of the row window, which costs the matrix cores ~72 cycles per
+// row at L = 48 whatever K is, well under the time the row takes to stream
+// from HBM. The VALU lane-per-row kernel (the reference's structure) stays
+// selectable with PATHTILE_DK_ALGO=valu for comparison.
 enum DkAlgo { kDkValu = 0, kDkMfma = 1 };
 
 static DkAlgo dk_algo(int L, int K) {
   const char* env = getenv("PATHTILE_DK_ALGO");
-  if (env && strcmp(env, "valu") == 0) return kDkValu;
-  if (env && strcmp(env, "mfma") == 0) return kDkMfma;
   (void)L;
-  return K >= 16 ? kDkMfma : kDkValu;
+  (void)K;
+  if (env && strcmp(env, "valu") == 0) return kDkValu;
+  return kDkMfma;
 }
 
 // A DK workgroup covers one channel and a batch tile. Its size is fixed from
 // the shape alone (not the device), so the deterministic variant's workspace
-// size can be queried without a device. The tile is chosen so the grid holds
-// about 4096 waves (16 per CU on 256 CUs), which keeps atomics per tap low
-// (H * nbt * K total) without starving the CUs.
-constexpr long long kNominalWaves = 4096;
+// size can be queried without a device. Small batch tiles (about 128 rows per
+// wave at large shapes) keep the rows in flight across the XCDs within a
+// compact address range, which streams better than long per-wave runs.
+constexpr long long kDkRowsDivisor = 16384;
 
 struct DkGeom {
   DkAlgo algo;
@@ -155,21 +153,22 @@ static DkGeom dk_geometry(int B, int H, int L, int K, int threads) {
   g.algo = dk_algo(L, K);
   g.wpb = threads / kWave;
   const long long wpb = g.wpb;
+  const long long rows = (long long)B * H;
   if (g.algo == kDkValu) {
-    const long long chunks_per_h = ((long long)B + kWave - 1) / kWave;
-    const long long total = chunks_per_h * (long long)H;
-    long long R = total / (wpb * 2048);
+    long long R = (rows / kDkRowsDivisor + kWave - 1) / kWave;  // chunks
     if (R < 1) R = 1;
-    if (R > 16) R = 16;
+    if (R > 2) R = 2;
+    const long long chunks_per_h = ((long long)B + kWave - 1) / kWave;
     const long long rmax = (chunks_per_h + wpb - 1) / wpb;
     if (R > rmax) R = rmax < 1 ? 1 : rmax;
     g.rows_per_wave = (int)R;
     const long long tile = wpb * R * kWave;
     g.nbt = (int)(((long long)B + tile - 1) / tile);
   } else {
-    long long rpw = ((long long)B * H + kNominalWaves - 1) / kNominalWaves;
+    long long rpw = (rows + kDkRowsDivisor - 1) / kDkRowsDivisor;
     rpw = (rpw + 15) / 16 * 16;
     if (rpw < 16) rpw = 16;
+    if (rpw > 128) rpw = 128;
     const long long rmax = (((long long)B + wpb - 1) / wpb + 15) / 16 * 16;
     if (rpw > rmax) rpw = rmax;
     g.rows_per_wave = (int)rpw;
@@ -288,8 +287,8 @@ static int dk_path(bool det, const float* gy, const float* x, float* dst,
   if (g.algo == kDkMfma) {
     DkMfmaFn fn = kDkMfmaTable[mfma_index(L)];
     void* args[] = {&gy, &x, &dst, &B, &H, &L, &K, &rpw, &nbt, &nblocks, &d};
-    return launch((const void*)fn, nblocks, (uint32_t)threads,
-                  (size_t)g.wpb * mfma_lds_per_wave(L), stream, args);
+    return launch((const void*)fn, nblocks, (uint32_t)threads, 0, stream,
+                  args);
   }
   const bool vec = (L % 4 == 0) && aligned(gy, 16) && aligned(x, 16);
   DkFn fn = (vec ? kDkTableV : kDkTableS)[lbucket_index(L)][kbucket_index(K)];
@@ -442,10 +441,9 @@ int pt_dynamic_lds_bytes(int kernel_id, int L, int K, int block_config,
       return PT_OK;
     case PT_KERNEL_DK:
       if (!pt::valid_dk_threads(block_config)) return PT_ERR_CONFIG;
-      *lds_bytes = (int)((block_config / pt::kWave) *
-                         (pt::dk_algo(L, K) == pt::kDkMfma
-                              ? pt::mfma_lds_per_wave(L)
-                              : (size_t)pt::kStageBytes));
+      *lds_bytes = pt::dk_algo(L, K) == pt::kDkMfma
+                       ? 0  // the matrix-core DK uses static LDS only
+                       : (int)((block_config / pt::kWave) * pt::kStageBytes);
       return PT_OK;
     case PT_KERNEL_DK_REDUCE:
       *lds_bytes = 0;

@@ -128,24 +128,34 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t kOob = 0x80000000u;         // >= num_records
 constexpr int kNumRecords = 0x7fffffff;
 constexpr int kRsrcWord3 = 0x00020000;         // gfx9: 32-bit data format
+// Cache-policy bits of buffer instructions (gfx940+: bit 0 = sc0, bit 1 = nt,
+// bit 4 = sc1). The streamed tensors are touched once per kernel, so their
+// loads and stores are non-temporal: they neither displace other data nor
+// leave dirty lines for the next kernel to write back.
+constexpr int kCpolNone = 0;
+constexpr int kCpolNT = 2;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0,
                                            kNumRecords, kRsrcWord3);
 }
 
+template <int CPOL = kCpolNone>
 __device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r,
                                             uint32_t voff, uint32_t soff) {
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, CPOL);
   return make_float4(__uint_as_float(v.x), __uint_as_float(v.y),
                      __uint_as_float(v.z), __uint_as_float(v.w));
 }
 
+template <int CPOL = kCpolNone>
 __device__ __forceinline__ float buf_load1(__amdgpu_buffer_rsrc_t r,
                                            uint32_t voff, uint32_t soff) {
-  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+  return __uint_as_float(
+      __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, CPOL));
 }
 
+template <int CPOL = kCpolNone>
 __device__ __forceinline__ void buf_store4(float4 v, __amdgpu_buffer_rsrc_t r,
                                            uint32_t voff, uint32_t soff) {
   u32x4 u;
@@ -153,12 +163,14 @@ __device__ __forceinline__ void buf_store4(float4 v, __amdgpu_buffer_rsrc_t r,
   u.y = __float_as_uint(v.y);
   u.z = __float_as_uint(v.z);
   u.w = __float_as_uint(v.w);
-  __builtin_amdgcn_raw_buffer_store_b128(u, r, voff, soff, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(u, r, voff, soff, CPOL);
 }
 
+template <int CPOL = kCpolNone>
 __device__ __forceinline__ void buf_store1(float v, __amdgpu_buffer_rsrc_t r,
                                            uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, voff, soff, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, voff, soff,
+                                        CPOL);
 }
 
 // ---------------------------------------------------------------------------
@@ -189,12 +201,12 @@ struct TileIO {
       const uint32_t soff = (uint32_t)(k * rpi) * rstride * 4u;
       const bool row_ok = r0 < nrows - k * rpi;
       if (vec) {
-        buf[k] = buf_load4(rs, row_ok && col < L ? off : kOob, soff);
+        buf[k] = buf_load4<kCpolNT>(rs, row_ok && col < L ? off : kOob, soff);
       } else {
-        buf[k].x = buf_load1(rs, row_ok && col + 0 < L ? off + 0u : kOob, soff);
-        buf[k].y = buf_load1(rs, row_ok && col + 1 < L ? off + 4u : kOob, soff);
-        buf[k].z = buf_load1(rs, row_ok && col + 2 < L ? off + 8u : kOob, soff);
-        buf[k].w = buf_load1(rs, row_ok && col + 3 < L ? off + 12u : kOob, soff);
+        buf[k].x = buf_load1<kCpolNT>(rs, row_ok && col + 0 < L ? off + 0u : kOob, soff);
+        buf[k].y = buf_load1<kCpolNT>(rs, row_ok && col + 1 < L ? off + 4u : kOob, soff);
+        buf[k].z = buf_load1<kCpolNT>(rs, row_ok && col + 2 < L ? off + 8u : kOob, soff);
+        buf[k].w = buf_load1<kCpolNT>(rs, row_ok && col + 3 < L ? off + 12u : kOob, soff);
       }
     }
   }
@@ -392,7 +404,8 @@ constexpr int rows_max_threads(int lmax, bool vec) {
   return (lmax >= 40 || !vec) ? 768 : 1024;
 }
 
-template <int LMAX, int KB, bool DX, bool VEC>
+template <int LMAX, int KB, bool DX, bool VEC, int LOAD_CPOL = kCpolNT,
+          int STORE_CPOL = kCpolNT>
 __global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kernel(
     const float* __restrict__ in, const float* __restrict__ w,
     float* __restrict__ out, int H, int L, int K, uint32_t R, uint32_t ntiles,
@@ -429,7 +442,7 @@ __global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kerne
       float4 v[NV];
 #pragma unroll
       for (int k = 0; k < NV; ++k)
-        v[k] = buf_load4(rin, (uint32_t)(kWave * k + lane) * 16u, 0);
+        v[k] = buf_load4<LOAD_CPOL>(rin, (uint32_t)(kWave * k + lane) * 16u, 0);
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
         const uint32_t e = (uint32_t)(kWave * k + lane) * 4u;
@@ -454,7 +467,7 @@ __global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kerne
 #pragma unroll
         for (int k = 0; k < kG; ++k)
           if (g + k < LMAX)
-            v[k] = buf_load1(rin, (uint32_t)(kWave * (g + k) + ln) * 4u, 0);
+            v[k] = buf_load1<LOAD_CPOL>(rin, (uint32_t)(kWave * (g + k) + ln) * 4u, 0);
 #pragma unroll
         for (int k = 0; k < kG; ++k) {
           const uint32_t e = (uint32_t)(kWave * (g + k) + ln);
@@ -520,7 +533,7 @@ __global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kerne
           uint32_t row, col;
           flat_rc(e, uL, lmagic, row, col);
           const float4 y4 = *reinterpret_cast<const float4*>(tile + row * S + col);
-          buf_store4(y4, rout, e * 4u, 0);
+          buf_store4<STORE_CPOL>(y4, rout, e * 4u, 0);
         }
       }
     } else {
@@ -532,7 +545,7 @@ __global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kerne
         if (e < tile_elems) {
           uint32_t row, col;
           flat_rc(e, uL, lmagic, row, col);
-          buf_store1(tile[row * S + col], rout, e * 4u, 0);
+          buf_store1<STORE_CPOL>(tile[row * S + col], rout, e * 4u, 0);
         }
       }
     }
@@ -670,16 +683,15 @@ struct MfmaGeo {
   static constexpr int dfloats = dim * dstride; // per-wave D in LDS
 };
 
-template <int LMAX>
+template <int LMAX, int LOAD_CPOL = kCpolNone>
 __global__ __launch_bounds__(1024) void dwconv_dk_mfma_kernel(
     const float* __restrict__ gy, const float* __restrict__ x,
     float* __restrict__ dst, int B, int H, int L, int K, int rpw, int nbt,
     uint32_t nblocks, int det) {
   using M = MfmaGeo<LMAX>;
   constexpr int NT = M::nt;
-  constexpr int kUnroll = 4;                    // 4-sample steps per iteration
-  extern __shared__ float lds[];
-  __shared__ float red[kMaxWaves][kMaxK];
+  constexpr int kSteps = 4;  // 4-sample steps per load group (16 samples)
+  __shared__ float dsum[M::dfloats];  // workgroup sum of the waves' D
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -707,61 +719,75 @@ __global__ __launch_bounds__(1024) void dwconv_dk_mfma_kernel(
     const int col = lane & 15;  // column within a 16-wide tile
     const uint32_t off = ((uint32_t)kq * rstride + (uint32_t)col) * 4u;
     const uint32_t step_bytes = 4u * rstride * 4u;
-    const int nsteps = (nrow + 3) / 4;
-    for (int s0 = 0; s0 < nsteps; s0 += kUnroll) {
-      const int sb = __builtin_amdgcn_readfirstlane(s0);
-      float av[kUnroll][NT], bv[kUnroll][NT];
+    const int ngroups = (nrow + 4 * kSteps - 1) / (4 * kSteps);
+
+    // Operands of one group of kSteps steps (16 samples).
+    auto load_group = [&](int g, float (&av)[kSteps][NT], float (&bv)[kSteps][NT]) {
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const uint32_t soff = (uint32_t)(sb + u) * step_bytes;
-        const bool row_ok = (sb + u) * 4 + kq < nrow;
+      for (int u = 0; u < kSteps; ++u) {
+        const int step = g * kSteps + u;
+        const uint32_t soff = (uint32_t)step * step_bytes;
+        const bool row_ok = step * 4 + kq < nrow;
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt) {
           const bool ok = row_ok && 16 * tt + col < L;
           const uint32_t o = ok ? off + 64u * tt : kOob;
-          av[u][tt] = buf_load1(gr, o, soff);
-          bv[u][tt] = buf_load1(xr, o, soff);
+          av[u][tt] = buf_load1<LOAD_CPOL>(gr, o, soff);
+          bv[u][tt] = buf_load1<LOAD_CPOL>(xr, o, soff);
         }
       }
+    };
+    auto mfma_group = [&](const float (&av)[kSteps][NT], const float (&bv)[kSteps][NT]) {
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u)
+      for (int u = 0; u < kSteps; ++u)
 #pragma unroll
         for (int a = 0; a < NT; ++a)
 #pragma unroll
           for (int b = 0; b < NT; ++b)
             acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(
                 av[u][a], bv[u][b], acc[a][b], 0, 0, 0);
+    };
+
+    // Two register buffers: the loads of group g + 1 are in flight while the
+    // matrix cores consume group g.
+    float a0[kSteps][NT], b0[kSteps][NT], a1[kSteps][NT], b1[kSteps][NT];
+    load_group(0, a0, b0);
+    for (int g0 = 0; g0 < ngroups; g0 += 2) {
+      const int g = __builtin_amdgcn_readfirstlane(g0);
+      if (g + 1 < ngroups) load_group(g + 1, a1, b1);
+      mfma_group(a0, b0);
+      if (g + 1 >= ngroups) break;
+      if (g + 2 < ngroups) load_group(g + 2, a0, b0);
+      mfma_group(a1, b1);
     }
   }
 
-  // D -> LDS, then diagonal sums (lane j: tap j).
-  float* dmat = lds + wave * M::dfloats;
-  {
-    const int rq = 4 * (lane >> 4);
-    const int col = lane & 15;
+  // Sum the waves' D in a fixed order (wave 0, 1, ...), then one diagonal
+  // reduction per workgroup: thread j sums D[t][t + j - p] over valid t.
+  const int rq = 4 * (lane >> 4);
+  const int cl = lane & 15;
+  for (int wv = 0; wv < wpb; ++wv) {
+    if (wave == wv) {
 #pragma unroll
-    for (int a = 0; a < NT; ++a)
+      for (int a = 0; a < NT; ++a)
 #pragma unroll
-      for (int b = 0; b < NT; ++b)
+        for (int b = 0; b < NT; ++b)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          dmat[(16 * a + rq + r) * M::dstride + 16 * b + col] = acc[a][b][r];
+          for (int r = 0; r < 4; ++r) {
+            float* d = dsum + (16 * a + rq + r) * M::dstride + 16 * b + cl;
+            *d = (wv == 0) ? acc[a][b][r] : *d + acc[a][b][r];
+          }
+    }
+    __syncthreads();
   }
-  wave_lds_sync();
-  if (lane < K) {
-    const int m = lane - (K >> 1);
-    const int t0 = max(0, -m);
-    const int t1 = min(L, L - m);
-    float v = 0.0f;
-    for (int t = t0; t < t1; ++t) v += dmat[t * M::dstride + t + m];
-    red[wave][lane] = v;
-  }
-  __syncthreads();
 
   const int j = threadIdx.x;
   if (j < K) {
+    const int m = j - (K >> 1);
+    const int t0 = max(0, -m);
+    const int t1 = min(L, L - m);
     float v = 0.0f;
-    for (int wv = 0; wv < wpb; ++wv) v += red[wv][j];
+    for (int t = t0; t < t1; ++t) v += dsum[t * M::dstride + t + m];
     if (det) {
       dst[((size_t)h * K + j) * (size_t)nbt + bt] = v;
     } else {

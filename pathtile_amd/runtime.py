@@ -51,7 +51,7 @@ DEFAULT_BWDK_BTILE = 64  # samples per wave chunk (one per lane)
 # The reference packs 4 taps per thread (:64-66); here each lane packs the
 # whole tap window of its channel (both rows are register resident).
 DEFAULT_BWDK_KPACK = 4
-DEFAULT_BWDK_BLOCK = 256
+DEFAULT_BWDK_BLOCK = 128
 
 ALLOWED_WAVES = (1, 2, 4, 8, 16)
 MAX_BWDK_BLOCK = 768

@@ -158,11 +158,11 @@ def test_golden_edge_fixtures(rt):
         assert oracle.normalized_max_abs(_dk_det(rt, dyd, xd, K).cpu().numpy(), d[f"{n}/dk64"]) < DK_TOL
 
 
-@pytest.mark.parametrize("wpb", [1, 2, 4, 8, 16])
-def test_every_waves_per_block_gives_the_same_bits(wpb):
+@pytest.mark.parametrize("wpb,L", [(1, 48), (2, 48), (4, 48), (8, 48), (16, 32), (8, 37)])
+def test_every_waves_per_block_gives_the_same_bits(wpb, L):
     from pathtile_amd import runtime
 
-    B, H, L, K = 200, 24, 48, 48
+    B, H, K = 200, 24, 48
     x, w, dy = _inputs(B, H, L, K, seed=7)
     xd, wd, dyd = _dev(x, w, dy)
     r = runtime.HipWarpRuntime(waves_per_block=wpb)
@@ -185,6 +185,18 @@ def test_every_dk_block_size(threads):
     g1 = _dk_det(r, dyd, xd, K).cpu().numpy()
     assert oracle.normalized_max_abs(g1, ref) < DK_TOL
     assert np.array_equal(g1, _dk_det(r, dyd, xd, K).cpu().numpy())
+
+
+def test_oversized_workgroup_is_rejected():
+    """16 waves x a 64-row tile at L=48 needs 213 KiB of LDS: refused before
+    launch with the library's configuration error."""
+    from pathtile_amd import runtime
+
+    r = runtime.HipWarpRuntime(waves_per_block=16)
+    x = torch.zeros(64, 4, 48, device="cuda:0")
+    w = torch.zeros(4, 48, device="cuda:0")
+    with pytest.raises(ValueError, match="unsupported launch configuration"):
+        r.launch_fwd(x, w, torch.empty_like(x))
 
 
 def test_atomic_dk_accumulates_into_gk(rt):
