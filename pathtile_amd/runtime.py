@@ -42,16 +42,30 @@ DEFAULT_H = 128
 DEFAULT_L = 48
 DEFAULT_K = 48
 
-# Launch defaults = the frozen PathTile policy for MI355X
-# (pathtile_amd/tune/frozen_policy.json; re-selected by the tuner).
-DEFAULT_WAVES_PER_BLOCK = 4
-DEFAULT_DX_WAVES_PER_BLOCK = 4
+# Launch defaults: the frozen PathTile policy for MI355X when the tuner has
+# installed one (pathtile_amd/tune/frozen_policy.json), else these values.
+FROZEN_POLICY_PATH = __import__("pathlib").Path(__file__).resolve().parent / "tune" / "frozen_policy.json"
+
+
+def _frozen_policy() -> dict:
+    try:
+        import json
+
+        return dict(json.loads(FROZEN_POLICY_PATH.read_text()).get("selected", {}))
+    except (OSError, ValueError):
+        return {}
+
+
+_POLICY = _frozen_policy()
+DEFAULT_WAVES_PER_BLOCK = int(_POLICY.get("fwd_waves_per_block", 4))
+DEFAULT_DX_WAVES_PER_BLOCK = int(_POLICY.get("dx_waves_per_block", 4))
 DEFAULT_WARPS_PER_BLOCK = DEFAULT_WAVES_PER_BLOCK
 DEFAULT_BWDK_BTILE = 64  # samples per wave chunk (one per lane)
 # The reference packs 4 taps per thread (:64-66); here each lane packs the
-# whole tap window of its channel (both rows are register resident).
+# whole tap window of its channel (both rows are register resident), and the
+# default matrix-core dK contracts over the batch instead.
 DEFAULT_BWDK_KPACK = 4
-DEFAULT_BWDK_BLOCK = 128
+DEFAULT_BWDK_BLOCK = int(_POLICY.get("dk_threads_per_block", 128))
 
 ALLOWED_WAVES = (1, 2, 4, 8, 16)
 MAX_BWDK_BLOCK = 768
@@ -301,7 +315,11 @@ class HipWarpRuntime:
         *,
         dx_waves_per_block: int | None = None,
     ) -> None:
-        dxw = waves_per_block if dx_waves_per_block is None else dx_waves_per_block
+        if dx_waves_per_block is None:
+            dx_waves_per_block = (DEFAULT_DX_WAVES_PER_BLOCK
+                                  if waves_per_block == DEFAULT_WAVES_PER_BLOCK
+                                  else waves_per_block)
+        dxw = dx_waves_per_block
         for value in (waves_per_block, dxw):
             if value not in ALLOWED_WAVES:
                 raise ValueError("waves_per_block must be one of 1,2,4,8,16")

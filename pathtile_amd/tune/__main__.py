@@ -1,0 +1,155 @@
+"""CLI of the PathTile tuner.
+
+    python -m pathtile_amd.tune all    [--trials 3 --warmup 50 --runs 100]
+        GPU: tuning trials -> freeze the per-path policy -> held-out trials
+        -> regret report; with --install the policy becomes the runtime's
+        launch default (pathtile_amd/tune/frozen_policy.json).
+    python -m pathtile_amd.tune report [--out DIR]
+        CPU: recompute the policy from the tuning CSVs, verify it matches the
+        frozen one and predates every held-out trial, rewrite the report.
+"""
+
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+from . import select
+from .shapes import SEED, draw_shapes
+
+PKG = Path(__file__).resolve().parent
+DEFAULT_OUT = PKG / "results"
+INSTALLED_POLICY = PKG / "frozen_policy.json"
+
+
+def _write_csv(path: Path, rows: list[dict]) -> None:
+    if not rows:
+        path.write_text("")
+        return
+    keys = list(rows[0].keys())
+    for r in rows[1:]:
+        for k in r:
+            if k not in keys:
+                keys.append(k)
+    with path.open("w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=keys)
+        w.writeheader()
+        w.writerows(rows)
+
+
+def _read_csv(path: Path) -> list[dict]:
+    with path.open() as f:
+        rows = list(csv.DictReader(f))
+    for r in rows:
+        for k in ("B", "H", "L", "K", "candidate_value", "trial_id", "n"):
+            if k in r and r[k] != "":
+                r[k] = int(float(r[k]))
+        for k in ("mean_ms",):
+            if k in r:
+                r[k] = float(r[k])
+    return rows
+
+
+def _git_rev() -> str:
+    try:
+        return subprocess.run(["git", "rev-parse", "HEAD"], cwd=PKG, capture_output=True,
+                              text=True, check=True).stdout.strip()
+    except Exception:
+        return "unknown"
+
+
+def _run_phase(name, cases, args, out: Path, log) -> list[dict]:
+    from .sweep import run_trial
+
+    rows, validation, metas = [], [], []
+    for trial in range(1, args.trials + 1):
+        res = run_trial(cases, trial, args.warmup, args.runs, args.seed, log=log)
+        _write_csv(out / f"{name}_trial{trial}.csv", res["summary"])
+        rows += res["summary"]
+        validation += res["validation"]
+        metas.append(res["metadata"])
+    _write_csv(out / f"{name}_validation.csv", validation)
+    (out / f"{name}_metadata.json").write_text(json.dumps(metas, indent=2))
+    return rows
+
+
+def build_report(out: Path, policy: dict) -> dict:
+    """Regret tables from the CSVs in `out` (no device needed)."""
+    train = select.mean_of_trials(sum((_read_csv(p) for p in sorted(out.glob("train_trial*.csv"))), []))
+    hold = select.mean_of_trials(sum((_read_csv(p) for p in sorted(out.glob("holdout_trial*.csv"))), []))
+    recomputed = select.select_policy(train)
+    if recomputed != policy["selected"]:
+        raise AssertionError(f"frozen policy {policy['selected']} != training-only reconstruction {recomputed}")
+    metas = json.loads((out / "holdout_metadata.json").read_text())
+    select.verify_frozen_before_holdout(policy, [m["created_at_utc"] for m in metas])
+    train_per, train_sum = select.holdout_regret(train, recomputed)
+    hold_per, hold_sum = select.holdout_regret(hold, recomputed)
+    _write_csv(out / "train_per_shape.csv", train_per)
+    _write_csv(out / "holdout_per_shape.csv", hold_per)
+    report = {"policy": recomputed, "train": train_sum, "holdout": hold_sum,
+              "device_name": policy.get("device_name")}
+    (out / "report.json").write_text(json.dumps(report, indent=2))
+    return report
+
+
+def main(argv=None) -> int:
+    p = argparse.ArgumentParser(prog="python -m pathtile_amd.tune")
+    p.add_argument("command", choices=["all", "report"])
+    p.add_argument("--out", type=Path, default=DEFAULT_OUT)
+    p.add_argument("--trials", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=50)
+    p.add_argument("--runs", type=int, default=100)
+    p.add_argument("--seed", type=int, default=0, help="base input seed (shapes use a fixed seed)")
+    p.add_argument("--install", action="store_true",
+                   help="write the frozen policy to pathtile_amd/tune/frozen_policy.json")
+    args = p.parse_args(argv)
+    out = args.out
+    out.mkdir(parents=True, exist_ok=True)
+
+    def log(msg):
+        print(msg, flush=True)
+
+    if args.command == "all":
+        if args.trials < 1 or args.warmup < 1 or args.runs < 2:
+            raise SystemExit("Use at least one trial, one warm-up and two measured runs")
+        import torch
+
+        train_cases, holdout_cases = draw_shapes()
+        log(f"[tune] {len(train_cases)} tuning shapes, {len(holdout_cases)} held out (shape seed {SEED})")
+        train_rows = _run_phase("train", train_cases, args, out, log)
+        selected = select.select_policy(select.mean_of_trials(train_rows))
+        policy = {
+            "selected": selected,
+            "frozen_before_holdout": True,
+            "frozen_at_utc": __import__("datetime").datetime.now(
+                __import__("datetime").timezone.utc).isoformat(),
+            "device_name": torch.cuda.get_device_name(0),
+            "git_rev": _git_rev(),
+            "shape_seed": SEED,
+            "train_shapes": [c.config_id for c in train_cases],
+            "holdout_shapes": [c.config_id for c in holdout_cases],
+            "objective": "per path: argmin over candidates of the sum of mean kernel ms over the "
+                         "tuning shapes; ties to the smaller value",
+            "protocol": {"trials": args.trials, "warmup": args.warmup, "runs": args.runs},
+        }
+        (out / "frozen_policy.json").write_text(json.dumps(policy, indent=2))
+        log(f"[tune] frozen policy {selected}")
+        _run_phase("holdout", holdout_cases, args, out, log)
+        report = build_report(out, policy)
+        log(json.dumps(report, indent=2))
+        if args.install:
+            INSTALLED_POLICY.write_text(json.dumps(policy, indent=2))
+        return 0
+
+    policy = json.loads((out / "frozen_policy.json").read_text())
+    report = build_report(out, policy)
+    print(json.dumps(report, indent=2))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,208 @@
+"""PathTile candidate sweep on one MI355X (needs a GPU).
+
+Follows the reference's measurement contract
+(benchmark/benchmark_pathtile_candidate_sweep.py:153-317, 493-712;
+artifact/REPRODUCIBILITY.md:81-93, 130-131):
+* candidates: FWD/dX wavefronts per workgroup, dK threads per workgroup;
+  every candidate is validated against PyTorch on the GPU at
+  B = min(B, 128) with full H, L, K before it is timed;
+* per (shape, candidate): warm-up launches, then `runs` launches each
+  bracketed by events on the launch stream; dK's output is zeroed outside
+  the event;
+* trials repeat the sweep with candidate and shape order reversed on even
+  trials; the summary is the mean of trial means.
+Unlike the reference (a fresh nvcc JIT per candidate), every candidate is a
+runtime argument of the one prebuilt library, so a sweep compiles nothing.
+"""
+
+from __future__ import annotations
+
+import math
+import platform
+import socket
+import time
+import zlib
+from datetime import datetime, timezone
+
+import torch
+import torch.nn.functional as F
+
+from .. import runtime as rt
+from .shapes import ShapeCase
+
+FWD_DX_KIND = "waves_per_block"
+DK_KIND = "dk_threads_per_block"
+# 64-lane wavefronts per workgroup. 16 waves (1024 threads) does not fit the
+# LDS tile of rows longer than 32, which the grid contains, so it is not a
+# candidate (it would be missing on those shapes).
+FWD_DX_CANDIDATES = (1, 2, 4, 8)
+DK_CANDIDATES = (64, 128, 192, 256, 384, 512)
+
+
+def utc_now() -> str:
+    return datetime.now(timezone.utc).isoformat()
+
+
+def stats(values) -> dict:
+    """benchmark/benchmark_pathtile_candidate_sweep.py:77-106."""
+    v = sorted(float(x) for x in values)
+    n = len(v)
+    if n == 0:
+        raise ValueError("Cannot summarize an empty measurement group")
+    mean = sum(v) / n
+    std = math.sqrt(sum((x - mean) ** 2 for x in v) / (n - 1)) if n > 1 else 0.0
+    sem = std / math.sqrt(n) if n > 1 else 0.0
+
+    def q(p):
+        pos = p * (n - 1)
+        lo, hi = math.floor(pos), math.ceil(pos)
+        return v[lo] + (v[hi] - v[lo]) * (pos - lo)
+
+    return {"n": n, "mean_ms": mean, "median_ms": q(0.5), "std_ms": std, "sem_ms": sem,
+            "ci95_low_ms": mean - 1.96 * sem, "ci95_high_ms": mean + 1.96 * sem,
+            "min_ms": v[0], "p05_ms": q(0.05), "p95_ms": q(0.95), "max_ms": v[-1]}
+
+
+def case_seed(base_seed: int, case: ShapeCase) -> int:
+    """benchmark/benchmark_pathtile_candidate_sweep.py:109-110."""
+    return int(base_seed + zlib.crc32(case.config_id.encode("utf-8")))
+
+
+def make_inputs(case: ShapeCase, seed: int, batch_override: int | None = None):
+    """x, w, dY on the GPU from a seeded generator: x, dY ~ N(0,1),
+    w ~ N(0, 1/K) (the reference draws w ~ N(0,1), :113-124)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    B = int(case.B if batch_override is None else batch_override)
+    x = torch.randn(B, case.H, case.L, device="cuda", generator=g)
+    w = torch.randn(case.H, case.K, device="cuda", generator=g) / math.sqrt(case.K)
+    dy = torch.randn(B, case.H, case.L, device="cuda", generator=g)
+    return x, w, dy
+
+
+def _torch_same(x, k):
+    K = int(k.shape[1])
+    left = K // 2
+    return F.conv1d(F.pad(x, (left, K - 1 - left)), k.unsqueeze(1), groups=int(x.shape[1]))
+
+
+def make_runtime(kind: str, value: int) -> rt.HipWarpRuntime:
+    if kind == FWD_DX_KIND:
+        return rt.HipWarpRuntime(waves_per_block=value, dx_waves_per_block=value)
+    return rt.HipWarpRuntime(bwdk_block=value)
+
+
+def validate_candidate(runtime, case: ShapeCase, seed: int, kind: str, value: int) -> list[dict]:
+    """Candidate vs PyTorch (FP64 on the GPU) at B = min(B, 128)
+    (benchmark/benchmark_pathtile_candidate_sweep.py:153-243). Tolerances:
+    the reference's allclose bars and the build's own bars (FWD/dX <= 1e-5,
+    dK <= 1e-4 max-abs-scaled)."""
+    vb = min(case.B, 128)
+    x, k, gy = make_inputs(case, seed, batch_override=vb)
+    xr = x.double().requires_grad_(True)
+    kr = k.double().requires_grad_(True)
+    yr = _torch_same(xr, kr)
+    gx_r, gk_r = torch.autograd.grad(yr, (xr, kr), gy.double())
+    rows = []
+
+    def row(phase, actual, expected, atol, rtol, bar):
+        err = float((actual.double() - expected).abs().max() / expected.abs().max().clamp_min(1e-12))
+        ok = bool(torch.allclose(actual.double(), expected, atol=atol, rtol=rtol)) and err <= bar
+        rows.append({**case.as_dict(), "candidate_kind": kind, "candidate_value": value,
+                     "validation_B": vb, "phase": phase, "normalized_max_abs": err, "allclose": ok})
+
+    if kind == FWD_DX_KIND:
+        y = torch.empty_like(x)
+        gx = torch.empty_like(x)
+        runtime.launch_fwd(x, k, y)
+        runtime.launch_bwd_input(gy, k, gx)
+        row("fwd", y, yr.detach(), 2e-3, 2e-3, 1e-5)
+        row("bwd_input", gx, gx_r, 2e-3, 2e-3, 1e-5)
+    else:
+        gk = torch.zeros_like(k)
+        runtime.launch_bwd_weight(gy, x, gk, case.K)
+        row("bwd_weight", gk, gk_r, 1e-2, 5e-4, 1e-4)
+    torch.cuda.synchronize()
+    return rows
+
+
+def measure_candidate(runtime, kind: str, x, k, gy, warmup: int, runs: int) -> dict[str, list[float]]:
+    """Warm-up, then `runs` event-timed launches per path
+    (benchmark/benchmark_pathtile_candidate_sweep.py:246-317)."""
+    K = int(k.shape[1])
+    coll = rt.KernelEventCollector()
+    coll.enabled = True
+    if kind == FWD_DX_KIND:
+        y = torch.empty_like(x)
+        gx = torch.empty_like(x)
+        for _ in range(warmup):
+            runtime.launch_fwd(x, k, y)
+            runtime.launch_bwd_input(gy, k, gx)
+        torch.cuda.synchronize()
+        for _ in range(runs):
+            runtime.launch_fwd(x, k, y, coll)
+        for _ in range(runs):
+            runtime.launch_bwd_input(gy, k, gx, coll)
+    else:
+        gk = torch.zeros_like(k)
+        for _ in range(warmup):
+            gk.zero_()
+            runtime.launch_bwd_weight(gy, x, gk, K)
+        torch.cuda.synchronize()
+        for _ in range(runs):
+            gk.zero_()
+            runtime.launch_bwd_weight(gy, x, gk, K, coll)
+    out: dict[str, list[float]] = {}
+    for r in coll.rows(synchronize=True):
+        out.setdefault(r["phase"], []).append(r["runtime_ms"])
+    return out
+
+
+def candidate_specs(trial_id: int) -> list[tuple[str, int]]:
+    """benchmark/benchmark_pathtile_candidate_sweep.py:485-490."""
+    specs = [(FWD_DX_KIND, v) for v in FWD_DX_CANDIDATES]
+    specs += [(DK_KIND, v) for v in DK_CANDIDATES]
+    if trial_id % 2 == 0:
+        specs.reverse()
+    return specs
+
+
+def run_trial(cases: list[ShapeCase], trial_id: int, warmup: int, runs: int,
+              base_seed: int = 0, log=print) -> dict:
+    """One trial over all cases and candidates; returns summary rows,
+    validation rows and metadata (benchmark/benchmark_pathtile_candidate_
+    sweep.py:493-712)."""
+    if trial_id <= 0:
+        raise ValueError("trial_id must be positive")
+    created = utc_now()
+    order = list(reversed(cases)) if trial_id % 2 == 0 else list(cases)
+    specs = candidate_specs(trial_id)
+    runtimes = {(k, v): make_runtime(k, v) for k, v in specs}
+    summary, validation = [], []
+    t0 = time.time()
+    for case in order:
+        seed = case_seed(base_seed, case)
+        for kind, value in specs:
+            validation += validate_candidate(runtimes[(kind, value)], case, seed, kind, value)
+        x, k, gy = make_inputs(case, seed)
+        for kind, value in specs:
+            times = measure_candidate(runtimes[(kind, value)], kind, x, k, gy, warmup, runs)
+            for phase, vals in times.items():
+                summary.append({**case.as_dict(), "trial_id": trial_id, "candidate_kind": kind,
+                                "candidate_value": value, "phase": phase, **stats(vals)})
+        del x, k, gy
+        torch.cuda.empty_cache()
+        log(f"[tune] trial {trial_id} {case.config_id} done ({time.time() - t0:.1f}s)")
+    bad = [v for v in validation if not v["allclose"]]
+    if bad:
+        raise AssertionError(f"candidate correctness failure: {bad[:3]}")
+    meta = {
+        "trial_id": trial_id, "created_at_utc": created, "finished_at_utc": utc_now(),
+        "device_name": torch.cuda.get_device_name(0), "hostname": socket.gethostname(),
+        "python": platform.python_version(), "torch": torch.__version__,
+        "hip": torch.version.hip, "warmup": warmup, "runs": runs, "base_seed": base_seed,
+        "candidates": {"fwd_dx_waves_per_block": list(FWD_DX_CANDIDATES),
+                       "dk_threads_per_block": list(DK_CANDIDATES)},
+        "measurement_contract": "warm-up then event-timed launches per path on the launch "
+                                "stream; dK zero-fill outside the event; mean of trial means",
+    }
+    return {"summary": summary, "validation": validation, "metadata": meta}
