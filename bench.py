@@ -327,7 +327,8 @@ def main(argv=None) -> int:
         "correctness_gate": {k: float(f"{v:.3e}") for k, v in gate.items()},
         "roofline": {
             "kernel": {"fwd": "dwconv_rows_kernel<FWD>", "bwd_input": "dwconv_rows_kernel<DX>",
-                       "bwd_weight": "dwconv_dk_kernel"}[dominant],
+                       "bwd_weight": ("dwconv_dk_kernel" if os.environ.get("PATHTILE_DK_ALGO") == "valu"
+                                      else "dwconv_dk_mfma_kernel")}[dominant],
             "bound": "hbm",
             "achieved": ach,
             "peak": PEAK_HBM_GBPS,

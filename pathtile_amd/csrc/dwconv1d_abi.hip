@@ -133,11 +133,12 @@ static DkAlgo dk_algo(int L, int K) {
   return kDkMfma;
 }
 
-// A DK workgroup covers one channel and a batch tile. Its size is fixed from
-// the shape alone (not the device), so the deterministic variant's workspace
-// size can be queried without a device. Small batch tiles (about 128 rows per
-// wave at large shapes) keep the rows in flight across the XCDs within a
-// compact address range, which streams better than long per-wave runs.
+// A DK workgroup covers one channel and a batch tile of wpb waves x
+// rows_per_wave samples. Rows per wave depend on the shape alone (not on the
+// device), so the deterministic variant's workspace size needs no device:
+// about 128 at large shapes (long per-wave runs stream worse, and the waves
+// of the XCDs then stay within a compact address range), fewer at small
+// shapes so the grid still fills the GPU.
 constexpr long long kDkRowsDivisor = 16384;
 
 struct DkGeom {
@@ -154,27 +155,27 @@ static DkGeom dk_geometry(int B, int H, int L, int K, int threads) {
   g.wpb = threads / kWave;
   const long long wpb = g.wpb;
   const long long rows = (long long)B * H;
+  long long rpw = (rows + kDkRowsDivisor - 1) / kDkRowsDivisor;
+  long long tile;
   if (g.algo == kDkValu) {
-    long long R = (rows / kDkRowsDivisor + kWave - 1) / kWave;  // chunks
+    long long R = (rpw + kWave - 1) / kWave;  // 64-sample chunks per wave
     if (R < 1) R = 1;
     if (R > 2) R = 2;
     const long long chunks_per_h = ((long long)B + kWave - 1) / kWave;
     const long long rmax = (chunks_per_h + wpb - 1) / wpb;
     if (R > rmax) R = rmax < 1 ? 1 : rmax;
     g.rows_per_wave = (int)R;
-    const long long tile = wpb * R * kWave;
-    g.nbt = (int)(((long long)B + tile - 1) / tile);
+    tile = wpb * R * kWave;
   } else {
-    long long rpw = (rows + kDkRowsDivisor - 1) / kDkRowsDivisor;
     rpw = (rpw + 15) / 16 * 16;
     if (rpw < 16) rpw = 16;
     if (rpw > 128) rpw = 128;
     const long long rmax = (((long long)B + wpb - 1) / wpb + 15) / 16 * 16;
     if (rpw > rmax) rpw = rmax;
     g.rows_per_wave = (int)rpw;
-    const long long tile = wpb * rpw;
-    g.nbt = (int)(((long long)B + tile - 1) / tile);
+    tile = wpb * rpw;
   }
+  g.nbt = (int)(((long long)B + tile - 1) / tile);
   if (g.nbt < 1) g.nbt = 1;
   g.nblocks = (long long)g.nbt * H;
   return g;

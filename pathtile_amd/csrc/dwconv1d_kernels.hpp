@@ -786,8 +786,17 @@ __global__ __launch_bounds__(1024) void dwconv_dk_mfma_kernel(
     const int m = j - (K >> 1);
     const int t0 = max(0, -m);
     const int t1 = min(L, L - m);
-    float v = 0.0f;
-    for (int t = t0; t < t1; ++t) v += dsum[t * M::dstride + t + m];
+    // Four independent partial sums (t = t0 + 4i + q), combined in a fixed
+    // order: a shorter dependency chain, the same result every run.
+    // D[t][t + m] = dsum[t * dstride + t + m] = diag[t * (dstride + 1)].
+    float v4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float* diag = dsum + m;
+    for (int t = t0; t < t1; t += 4) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (t + q < t1) v4[q] += diag[(t + q) * (M::dstride + 1)];
+    }
+    const float v = (v4[0] + v4[1]) + (v4[2] + v4[3]);
     if (det) {
       dst[((size_t)h * K + j) * (size_t)nbt + bt] = v;
     } else {

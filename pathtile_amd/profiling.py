@@ -1,0 +1,237 @@
+"""Summaries of rocprofv3 results (rocpd SQLite ``*_results.db``) as Markdown.
+
+Three reports, each written for one workload:
+
+``trace``   kernel-trace statistics: calls and average/min/max duration per
+            kernel, plus the launch geometry and resources of the largest
+            dispatch of each kernel.
+``traffic`` HBM bytes per launch from two ``--pmc`` runs (``FETCH_SIZE`` in
+            one, ``WRITE_SIZE`` in the other).  Both counters are read in KiB
+            per dispatch.  They are scaled by what the same counter reads for
+            a plain device-to-device copy of known size (torch ``copy_`` →
+            ``__amd_rocclr_copyBuffer``); on MI355X ``FETCH_SIZE`` reads half
+            of the bytes a copy loads, ``WRITE_SIZE`` reads them exactly.
+``valu``    VALU instruction counts and the VALU-busy fraction from
+            ``SQ_INSTS_VALU`` / ``SQ_ACTIVE_INST_VALU`` / ``SQ_BUSY_CYCLES`` /
+            ``GRBM_GUI_ACTIVE``.
+
+Only the dispatches with the largest grid of each kernel are kept, so the
+small correctness-gate launches that run before the timed loops are left out.
+
+Usage::
+
+    python -m pathtile_amd.profiling trace   DB --command CMD --out FILE
+    python -m pathtile_amd.profiling traffic FETCH_DB WRITE_DB --kernel SUBSTR \
+        --tag fwd --algorithmic-bytes N --copy-bytes N --command CMD --out FILE
+    python -m pathtile_amd.profiling valu    DB --command CMD --out FILE \
+        --useful-fma N --clock-mhz F
+"""
+
+from __future__ import annotations
+
+import argparse
+import sqlite3
+import statistics
+from pathlib import Path
+
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+# MI355X: 256 CUs x 4 SIMDs; a wave64 VALU op occupies its SIMD16 for 4 cycles.
+NUM_SIMDS = 1024
+CYCLES_PER_WAVE_VALU = 4
+NUM_XCD = 8
+
+
+def short_name(name: str) -> str:
+    """Kernel name without the parameter list (template arguments kept)."""
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            return name[:i].replace("void ", "")
+    return name
+
+
+def _largest_dispatches(rows, key_grid):
+    """Keep, per kernel name, only the rows whose grid equals its maximum."""
+    best = {}
+    for r in rows:
+        best[r["name"]] = max(best.get(r["name"], 0), r[key_grid])
+    return [r for r in rows if r[key_grid] == best[r["name"]]]
+
+
+def kernel_rows(db: str):
+    con = sqlite3.connect(db)
+    con.row_factory = sqlite3.Row
+    rows = [dict(r) for r in con.execute(
+        "select name, duration, grid_x*grid_y*grid_z as grid, "
+        "workgroup_x*workgroup_y*workgroup_z as wg, lds_size, scratch_size, "
+        "vgpr_count, accum_vgpr_count, sgpr_count from kernels")]
+    con.close()
+    return rows
+
+
+def counter_rows(db: str, counter: str):
+    con = sqlite3.connect(db)
+    con.row_factory = sqlite3.Row
+    rows = [dict(r) for r in con.execute(
+        "select kernel_name as name, dispatch_id, grid_size as grid, value "
+        "from counters_collection where counter_name = ?", (counter,))]
+    con.close()
+    return rows
+
+
+def trace_report(db: str, command: str, match: str = "pt::") -> str:
+    rows = [r for r in kernel_rows(db) if match in r["name"] or r["name"] == COPY_KERNEL]
+    rows = _largest_dispatches(rows, "grid")
+    by = {}
+    for r in rows:
+        by.setdefault(r["name"], []).append(r)
+    out = ["| kernel | calls | avg us | min us | median us | max us | grid | wg | VGPR | AGPR | SGPR | LDS B | scratch B |",
+           "|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    for name, rs in sorted(by.items(), key=lambda kv: -sum(r["duration"] for r in kv[1])):
+        d = [r["duration"] / 1e3 for r in rs]
+        r0 = rs[0]
+        out.append(f"| `{short_name(name)}` | {len(rs)} | {statistics.mean(d):.2f} | {min(d):.2f} | "
+                   f"{statistics.median(d):.2f} | {max(d):.2f} | {r0['grid']} | {r0['wg']} | "
+                   f"{r0['vgpr_count']} | {r0['accum_vgpr_count']} | {r0['sgpr_count']} | "
+                   f"{r0['lds_size']} | {r0['scratch_size']} |")
+    head = ["Command:", "", "```", command, "```", "",
+            "Dispatches with each kernel's largest grid only (the timed loops; "
+            "the small correctness-gate launches are dropped).", ""]
+    return "\n".join(head + out) + "\n"
+
+
+def _mean_counter(db: str, counter: str, match: str):
+    rows = _largest_dispatches(
+        [r for r in counter_rows(db, counter) if match in r["name"]], "grid")
+    if not rows:
+        raise SystemExit(f"no {counter} rows for kernels matching {match!r} in {db}")
+    vals = [r["value"] for r in rows]
+    return statistics.mean(vals), min(vals), max(vals), len(vals), rows[0]["name"]
+
+
+def _copy_counter(db: str, counter: str):
+    """Counter value of the largest plain copy dispatch (KiB)."""
+    rows = [r for r in counter_rows(db, counter) if r["name"] == COPY_KERNEL]
+    if not rows:
+        raise SystemExit(f"no {COPY_KERNEL} dispatches in {db} (run bench.py with --copy-probe)")
+    top = max(r["value"] for r in rows)
+    vals = [r["value"] for r in rows if r["value"] > 0.9 * top]
+    return statistics.mean(vals), len(vals)
+
+
+def traffic_report(fetch_db: str, write_db: str, kernel: str, tag: str,
+                   algorithmic_bytes: int, copy_bytes: int, command: str) -> str:
+    kib = 1024.0
+    f_mean, f_min, f_max, f_n, name = _mean_counter(fetch_db, "FETCH_SIZE", kernel)
+    w_mean, w_min, w_max, w_n, _ = _mean_counter(write_db, "WRITE_SIZE", kernel)
+    cf, cf_n = _copy_counter(fetch_db, "FETCH_SIZE")
+    cw, cw_n = _copy_counter(write_db, "WRITE_SIZE")
+    fetch_factor = copy_bytes / (cf * kib)
+    write_factor = copy_bytes / (cw * kib)
+    fetch_bytes = f_mean * kib * fetch_factor
+    write_bytes = w_mean * kib * write_factor
+    lines = [
+        f"# HBM traffic per launch: {tag} (`{short_name(name)}`)", "",
+        "Commands (two separate passes, one counter each):", "", "```", command, "```", "",
+        "| counter | dispatches | mean KiB | min KiB | max KiB | copy probe KiB (n) | scale | bytes/launch |",
+        "|---|---|---|---|---|---|---|---|",
+        f"| FETCH_SIZE | {f_n} | {f_mean:.1f} | {f_min:.1f} | {f_max:.1f} | {cf:.1f} ({cf_n}) | "
+        f"{fetch_factor:.4f} | {fetch_bytes:.0f} |",
+        f"| WRITE_SIZE | {w_n} | {w_mean:.1f} | {w_min:.1f} | {w_max:.1f} | {cw:.1f} ({cw_n}) | "
+        f"{write_factor:.4f} | {write_bytes:.0f} |",
+        "",
+        f"Copy probe: {copy_bytes} bytes read and {copy_bytes} bytes written per copy; "
+        "scale = copy bytes / (counter KiB x 1024).",
+        f"Algorithmic bytes per launch: {algorithmic_bytes}; measured/algorithmic = "
+        f"{(fetch_bytes + write_bytes) / algorithmic_bytes:.4f}.",
+        "",
+        f"FETCH_BYTES_PER_LAUNCH: {fetch_bytes:.0f}",
+        f"WRITE_BYTES_PER_LAUNCH: {write_bytes:.0f}",
+        "",
+    ]
+    return "\n".join(lines)
+
+
+def valu_report(db: str, command: str, useful_fma: dict[str, int], clock_mhz: float,
+                match: str = "pt::") -> str:
+    counters = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_ACTIVE_INST_VALU", "SQ_BUSY_CYCLES",
+                "GRBM_GUI_ACTIVE", "SQ_WAVE_CYCLES")
+    per = {}
+    for c in counters:
+        rows = _largest_dispatches(
+            [r for r in counter_rows(db, c) if match in r["name"]], "grid")
+        for r in rows:
+            per.setdefault(r["name"], {}).setdefault(c, []).append(r["value"])
+    out = ["Command:", "", "```", command, "```", "",
+           f"VALU-busy = SQ_ACTIVE_INST_VALU x {CYCLES_PER_WAVE_VALU} / ({NUM_SIMDS} SIMDs x "
+           f"GRBM_GUI_ACTIVE / {NUM_XCD} XCDs). FP32 fraction = useful FP32 FLOPs / "
+           f"(duration x 78.6 TFLOP/s non-packed vector FP32 peak; packed FP32 is off in this "
+           f"build), duration = GRBM_GUI_ACTIVE / {NUM_XCD} / {clock_mhz:.0f} MHz.", "",
+           "| kernel | dispatches | waves | VALU insts | VALU insts / wave | VALU-busy | useful FMA | FP32 fraction |",
+           "|---|---|---|---|---|---|---|---|"]
+    for name, cs in per.items():
+        m = {c: statistics.mean(v) for c, v in cs.items()}
+        n = len(cs.get("SQ_INSTS_VALU", []))
+        gui = m["GRBM_GUI_ACTIVE"] / NUM_XCD
+        busy = m["SQ_ACTIVE_INST_VALU"] * CYCLES_PER_WAVE_VALU / (NUM_SIMDS * gui)
+        fma = next((v for k, v in useful_fma.items() if k in name), None)
+        if fma is not None:
+            secs = gui / (clock_mhz * 1e6)
+            frac = f"{2 * fma / secs / 78.6e12:.3f}"
+            fma_s = str(fma)
+        else:
+            frac, fma_s = "n/a", "n/a"
+        out.append(f"| `{short_name(name)}` | {n} | {m['SQ_WAVES']:.0f} | {m['SQ_INSTS_VALU']:.0f} | "
+                   f"{m['SQ_INSTS_VALU'] / max(m['SQ_WAVES'], 1):.0f} | {busy:.3f} | {fma_s} | {frac} |")
+    return "\n".join(out) + "\n"
+
+
+def main(argv=None) -> int:
+    p = argparse.ArgumentParser(prog="python -m pathtile_amd.profiling")
+    sub = p.add_subparsers(dest="cmd", required=True)
+    t = sub.add_parser("trace")
+    t.add_argument("db")
+    t.add_argument("--command", required=True)
+    t.add_argument("--title", default="Kernel trace")
+    t.add_argument("--out", required=True)
+    f = sub.add_parser("traffic")
+    f.add_argument("fetch_db")
+    f.add_argument("write_db")
+    f.add_argument("--kernel", required=True, help="substring of the kernel name")
+    f.add_argument("--tag", required=True)
+    f.add_argument("--algorithmic-bytes", type=int, required=True)
+    f.add_argument("--copy-bytes", type=int, required=True)
+    f.add_argument("--command", required=True)
+    f.add_argument("--out", required=True)
+    v = sub.add_parser("valu")
+    v.add_argument("db")
+    v.add_argument("--command", required=True)
+    v.add_argument("--useful-fma", action="append", default=[],
+                   help="KERNEL_SUBSTR=N useful FMAs per dispatch (repeatable)")
+    v.add_argument("--clock-mhz", type=float, default=2400.0)
+    v.add_argument("--title", default="VALU utilisation")
+    v.add_argument("--out", required=True)
+    a = p.parse_args(argv)
+    if a.cmd == "trace":
+        text = f"# {a.title}\n\n" + trace_report(a.db, a.command)
+    elif a.cmd == "traffic":
+        text = traffic_report(a.fetch_db, a.write_db, a.kernel, a.tag, a.algorithmic_bytes,
+                              a.copy_bytes, a.command)
+    else:
+        fma = {}
+        for item in a.useful_fma:
+            k, _, n = item.rpartition("=")
+            fma[k] = int(n)
+        text = f"# {a.title}\n\n" + valu_report(a.db, a.command, fma, a.clock_mhz)
+    Path(a.out).parent.mkdir(parents=True, exist_ok=True)
+    Path(a.out).write_text(text)
+    print(text)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -125,30 +125,55 @@ def validate_candidate(runtime, case: ShapeCase, seed: int, kind: str, value: in
     return rows
 
 
-def measure_candidate(runtime, kind: str, x, k, gy, warmup: int, runs: int) -> dict[str, list[float]]:
-    """Warm-up, then `runs` event-timed launches per path
-    (benchmark/benchmark_pathtile_candidate_sweep.py:246-317)."""
+# MI355X has a 256 MiB memory-side cache (MALL). Tensors of the smaller
+# tuning shapes fit in it, and back-to-back launches on the same buffers would
+# then time the cache, not HBM. Each candidate therefore cycles through enough
+# buffer sets (x, dY, y, dX) to exceed this footprint, so every launch streams
+# from HBM and pays for evicting the previous launches' outputs, as it does in
+# a training step.
+ROTATION_BYTES = 1 << 29
+
+
+def buffer_sets(x, gy) -> list[tuple]:
+    """(x, dY, y, dX) sets: the seeded inputs plus copies, enough to exceed
+    ROTATION_BYTES; copies hold the same values."""
+    per_set = 4 * x.numel() * x.element_size()
+    n = max(1, -(-ROTATION_BYTES // per_set))
+    sets = [(x, gy, torch.empty_like(x), torch.empty_like(x))]
+    for _ in range(n - 1):
+        sets.append((x.clone(), gy.clone(), torch.empty_like(x), torch.empty_like(x)))
+    return sets
+
+
+def measure_candidate(runtime, kind: str, sets: list[tuple], k, warmup: int,
+                      runs: int) -> dict[str, list[float]]:
+    """Warm-up, then `runs` event-timed launches per path, cycling through the
+    buffer sets (benchmark/benchmark_pathtile_candidate_sweep.py:246-317)."""
     K = int(k.shape[1])
     coll = rt.KernelEventCollector()
     coll.enabled = True
+    n = len(sets)
     if kind == FWD_DX_KIND:
-        y = torch.empty_like(x)
-        gx = torch.empty_like(x)
-        for _ in range(warmup):
+        for i in range(warmup):
+            x, gy, y, gx = sets[i % n]
             runtime.launch_fwd(x, k, y)
             runtime.launch_bwd_input(gy, k, gx)
         torch.cuda.synchronize()
-        for _ in range(runs):
+        for i in range(runs):
+            x, gy, y, gx = sets[i % n]
             runtime.launch_fwd(x, k, y, coll)
-        for _ in range(runs):
+        for i in range(runs):
+            x, gy, y, gx = sets[i % n]
             runtime.launch_bwd_input(gy, k, gx, coll)
     else:
         gk = torch.zeros_like(k)
-        for _ in range(warmup):
+        for i in range(warmup):
+            x, gy, _, _ = sets[i % n]
             gk.zero_()
             runtime.launch_bwd_weight(gy, x, gk, K)
         torch.cuda.synchronize()
-        for _ in range(runs):
+        for i in range(runs):
+            x, gy, _, _ = sets[i % n]
             gk.zero_()
             runtime.launch_bwd_weight(gy, x, gk, K, coll)
     out: dict[str, list[float]] = {}
@@ -184,12 +209,14 @@ def run_trial(cases: list[ShapeCase], trial_id: int, warmup: int, runs: int,
         for kind, value in specs:
             validation += validate_candidate(runtimes[(kind, value)], case, seed, kind, value)
         x, k, gy = make_inputs(case, seed)
+        sets = buffer_sets(x, gy)
         for kind, value in specs:
-            times = measure_candidate(runtimes[(kind, value)], kind, x, k, gy, warmup, runs)
+            times = measure_candidate(runtimes[(kind, value)], kind, sets, k, warmup, runs)
             for phase, vals in times.items():
                 summary.append({**case.as_dict(), "trial_id": trial_id, "candidate_kind": kind,
-                                "candidate_value": value, "phase": phase, **stats(vals)})
-        del x, k, gy
+                                "candidate_value": value, "phase": phase,
+                                "buffer_sets": len(sets), **stats(vals)})
+        del x, k, gy, sets
         torch.cuda.empty_cache()
         log(f"[tune] trial {trial_id} {case.config_id} done ({time.time() - t0:.1f}s)")
     bad = [v for v in validation if not v["allclose"]]
@@ -203,6 +230,7 @@ def run_trial(cases: list[ShapeCase], trial_id: int, warmup: int, runs: int,
         "candidates": {"fwd_dx_waves_per_block": list(FWD_DX_CANDIDATES),
                        "dk_threads_per_block": list(DK_CANDIDATES)},
         "measurement_contract": "warm-up then event-timed launches per path on the launch "
-                                "stream; dK zero-fill outside the event; mean of trial means",
+                                "stream, cycling buffer sets past the 256 MiB MALL; dK "
+                                "zero-fill outside the event; mean of trial means",
     }
     return {"summary": summary, "validation": validation, "metadata": meta}
