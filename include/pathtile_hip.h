@@ -81,7 +81,7 @@ int pt_dwconv1d_dx_f32(const float* dy, const float* w, float* dx, int B,
  * (kernels/warp_tiled_ampere.py:772-812). The reference requires the caller
  * to zero dk first (:890-893); zero_first != 0 clears dk on `stream` with a
  * fill kernel before the accumulation, so "dK including zero-init" is one
- * call. threads_per_block: a multiple of 64 in [64, 1024] (the counterpart of
+ * call. threads_per_block: a multiple of 64 in [64, 768] (the counterpart of
  * BWDK_BLOCK, :645-649). Summation order across workgroups is not fixed.
  */
 int pt_dwconv1d_dk_atomic_f32(const float* dy, const float* x, float* dk,

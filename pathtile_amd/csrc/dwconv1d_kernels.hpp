@@ -9,32 +9,36 @@
 //
 // Mapping (MI355X-first; the reference maps one row onto a 32-lane warp with
 // one output per lane and re-reads taps and row elements per FMA):
-//   * one LANE owns one whole (b,h) row, held in VGPRs;
-//   * one WAVE owns 64 rows of one channel h (64 consecutive b), so the taps
-//     of h are wave-uniform and live in SGPRs;
-//   * a row tile is moved between HBM and the lanes through a 5 KiB per-wave
-//     LDS transpose, 16 columns at a time: HBM side dwordx4 loads/stores
-//     where rows are 16-byte aligned (L % 4 == 0), dword otherwise; lane side
-//     ds_read/ds_write_b128 on a padded stride (20 floats) that is free of
-//     bank conflicts;
+//   * one LANE owns one whole (b,h) row, held in VGPRs, and computes all of
+//     its outputs;
+//   * FWD / DX (dwconv_rows_kernel): a WAVE owns a tile of 64 CONSECUTIVE
+//     rows r = b*H + h of the flat [B*H, L] tensor (64*L*4 contiguous bytes),
+//     so every HBM instruction of the wave moves 1 KiB of contiguous memory.
+//     The tile passes through a per-wave LDS transpose (row stride LMAX + 4
+//     floats, bank-conflict free for ds_read/ds_write_b128); each lane keeps
+//     the taps of its own channel (r % H) in VGPRs across a persistent grid;
+//   * DK (dwconv_dk_mfma_kernel, default): a WAVE owns a run of samples b of
+//     one channel h and contracts them on the matrix cores
+//     (v_mfma_f32_16x16x4_f32): D[t][s] = sum_b dy[b][t] * x[b][s]; the taps
+//     are the diagonal sums dk[j] = sum_t D[t][t + j - p];
+//   * DK (dwconv_dk_kernel, PATHTILE_DK_ALGO=valu): a WAVE owns 64 samples of
+//     one channel; a 16-column strided LDS transpose (TileIO) feeds each lane
+//     its row pair and the lane accumulates every tap on the VALU;
 //   * the inner loops are fully unrolled at compile time for a row bucket
 //     LMAX (8..48) and a tap bucket KB (4..48). Taps outside [0,K) are zero
-//     in SGPRs and row elements in [L, LMAX) are zero in VGPRs, so one
-//     instantiation serves every (L, K) of its bucket and the unrolled FMA
-//     chain only touches (t, m) pairs inside the LMAX window.
+//     and row elements in [L, LMAX) are zero in VGPRs, so one instantiation
+//     serves every (L, K) of its bucket and the unrolled FMA chain only
+//     touches (t, m) pairs inside the LMAX window.
 //
 // FWD and DX run the reference's per-output fmaf chain in the reference's tap
 // order (FWD: j ascending, kernels/warp_tiled_ampere.py:411-430; DX: j
 // ascending, :479-498). Padded terms are exact no-ops (fma(0,w,a) == a,
 // fma(x,0,a) == a for finite x), so outputs equal that chain bit for bit.
 //
-// DK: every lane accumulates all taps of its channel over the rows it owns
-// (the reference's 4-tap packing, :548-584, taken to the full window since
-// both rows are register resident), a DPP + bpermute wave reduction, an LDS
-// reduction across the waves of the workgroup, then either one
-// global_atomic_add_f32 per tap per workgroup (atomic variant, :611-614) or
-// one store per tap into a [H, K, num_btiles] workspace followed by a
-// fixed-order reduction kernel (deterministic variant,
+// DK reduces per workgroup, then either adds one global_atomic_add_f32 per
+// tap per workgroup (atomic variant, kernels/warp_tiled_ampere.py:611-614)
+// or stores one partial per tap into a [H, K, num_btiles] workspace that a
+// fixed-order reduction kernel sums (deterministic variant,
 // kernels/warp_tiled_noatomic_optimized.py:881-1160).
 
 #pragma once
