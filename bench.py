@@ -236,32 +236,52 @@ def main(argv=None) -> int:
     gate = correctness_gate(rt, x, w, dy)
     log(f"correctness gate vs torch (first 512 rows): {gate}")
 
-    def step(coll=None):
-        rt.launch_fwd(x, w, y, coll)
-        rt.launch_bwd_input(dy, w, dx, coll)
+    def step():
+        rt.launch_fwd(x, w, y)
+        rt.launch_bwd_input(dy, w, dx)
         gk.zero_()
-        rt.launch_bwd_weight(dy, x, gk, K, coll)
+        rt.launch_bwd_weight(dy, x, gk, K)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     # The contract's K steps (FWD, dX, zero + dK interleaved), wall-clocked
     # between two synchronisations.
-    step_coll = runtime.KernelEventCollector()
-    step_coll.enabled = True
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step(step_coll)
+        step()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
-    srows = step_coll.rows(synchronize=True)
-    step_paths = {ph: mean([r["runtime_ms"] for r in srows if r["phase"] == ph])
-                  for ph in ("fwd", "bwd_input", "bwd_weight")}
 
-    # Per-path loops, the reference's protocol (kernels/warp_tiled_ampere.py:
+    # Per-path loops: `steps` back-to-back launches of one path between two
+    # events recorded on the launch stream (torch's current stream, where the
+    # runtime enqueues), mean = elapsed / steps. The atomic dK loop does not
+    # re-zero gk (the kernel's work is the same; the zero-init is timed as its
+    # own path, "bwd_weight_zero", where it is part of the call).
+    stream = torch.cuda.current_stream(dev)
+    loops = {
+        "fwd": lambda: rt.launch_fwd(x, w, y),
+        "bwd_input": lambda: rt.launch_bwd_input(dy, w, dx),
+        "bwd_weight": lambda: rt.launch_bwd_weight(dy, x, gk, K),
+        "bwd_weight_zero": lambda: rt.launch_bwd_weight(dy, x, gk, K, zero_first=True),
+        "bwd_weight_det": lambda: rt.launch_bwd_weight_deterministic(dy, x, gk, K),
+    }
+    loop_ms = {}
+    for ph, fn in loops.items():
+        for _ in range(max(1, args.warmup // 4)):
+            fn()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        ev1.record(stream)
+        ev1.synchronize()
+        loop_ms[ph] = ev0.elapsed_time(ev1) / args.steps
+
+    # The reference's per-launch protocol (kernels/warp_tiled_ampere.py:
     # 1059-1070; benchmark/benchmark_pathtile_candidate_sweep.py:274-317):
-    # K x FWD, then K x dX, then K x (zero outside the event + dK); plus dK
-    # including the zero-init as one call and the deterministic dK.
+    # an event pair around every launch; dK re-zeroed outside the events.
     coll = runtime.KernelEventCollector()
     coll.enabled = True
     for _ in range(args.steps):
@@ -283,10 +303,12 @@ def main(argv=None) -> int:
     nbytes = runtime.minimum_algorithmic_bytes(B, H, L, K)
     paths = {}
     for ph, v in per.items():
-        ms = mean(v)
+        ms = loop_ms[ph]
         gbps = runtime.algorithmic_bandwidth_gbps(nbytes, ms)
-        paths[ph] = {"ms": round(ms, 5), "min_ms": round(min(v), 5),
-                     "gbps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_HBM_GBPS, 2)}
+        paths[ph] = {"ms": round(ms, 5),
+                     "gbps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_HBM_GBPS, 2),
+                     "per_launch_event_ms": round(mean(v), 5),
+                     "per_launch_event_min_ms": round(min(v), 5)}
     agg = paths["fwd"]["ms"] + paths["bwd_input"]["ms"] + paths["bwd_weight"]["ms"]
     dominant = max(("fwd", "bwd_input", "bwd_weight"), key=lambda k: paths[k]["ms"])
     tag = {"fwd": "fwd", "bwd_input": "dx", "bwd_weight": "dk"}[dominant]
@@ -315,11 +337,11 @@ def main(argv=None) -> int:
             "dk_threads_per_block": cfg["dk_threads_per_block"],
             "launch_config_source": cfg["source"],
         },
-        "protocol": ("value = sum of per-path mean kernel times, each path in its own "
-                     "loop of `steps` launches (reference protocol); ms_per_step = wall "
-                     "time of `steps` interleaved FWD/dX/zero+dK steps"),
-        "step_paths_ms": {k: round(v, 5) for k, v in step_paths.items()},
-        "step_aggregate_ms": round(sum(step_paths.values()), 5),
+        "protocol": ("value = FWD + dX + dK (atomic, excl. zero-init) mean launch times; "
+                     "each path runs `steps` back-to-back launches between two HIP events on "
+                     "the launch stream; paths.*.per_launch_event_ms = the reference's "
+                     "protocol (an event pair per launch); ms_per_step = wall time of "
+                     "`steps` interleaved FWD/dX/zero+dK steps"),
         "aggregate_gbps": round(3 * nbytes / (agg / 1e3) / 1e9, 1),
         "aggregate_pct_peak": round(100 * 3 * nbytes / (agg / 1e3) / 1e9 / PEAK_HBM_GBPS, 2),
         "algorithmic_bytes_per_path": nbytes,

@@ -123,7 +123,8 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t p, uint32_t n) {
 // ---------------------------------------------------------------------------
 // Buffer addressing. A tile is reached through a wave-uniform buffer
 // resource (base = the wave's row 0, in SGPRs), one 32-bit per-lane byte
-// offset (VGPR) and a wave-uniform per-step byte offset (soffset). Lanes
+// offset (VGPR) and, for loads only, a wave-uniform per-step byte offset
+// (soffset; stores take their whole offset in the VGPR, see buf_store4). Lanes
 // that must not touch memory use an offset past num_records: buffer loads
 // then return 0 and buffer stores are dropped, so no branches are needed.
 // The host guarantees 64 * H * L * 4 < 2^31 (a tile spans < 2 GiB).
@@ -159,22 +160,26 @@ __device__ __forceinline__ float buf_load1(__amdgpu_buffer_rsrc_t r,
       __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, CPOL));
 }
 
+// Stores take no SGPR offset (soffset is the constant 0). With a register
+// in soffset the compiler inserts no wait states between a dwordx3/x4 store
+// and a following VALU write of the store's data VGPRs; on gfx950 the store
+// then wrote the VALU result in place of its first dword. The whole byte
+// offset therefore travels in the VGPR offset.
 template <int CPOL = kCpolNone>
 __device__ __forceinline__ void buf_store4(float4 v, __amdgpu_buffer_rsrc_t r,
-                                           uint32_t voff, uint32_t soff) {
+                                           uint32_t voff) {
   u32x4 u;
   u.x = __float_as_uint(v.x);
   u.y = __float_as_uint(v.y);
   u.z = __float_as_uint(v.z);
   u.w = __float_as_uint(v.w);
-  __builtin_amdgcn_raw_buffer_store_b128(u, r, voff, soff, CPOL);
+  __builtin_amdgcn_raw_buffer_store_b128(u, r, voff, 0, CPOL);
 }
 
 template <int CPOL = kCpolNone>
 __device__ __forceinline__ void buf_store1(float v, __amdgpu_buffer_rsrc_t r,
-                                           uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, voff, soff,
-                                        CPOL);
+                                           uint32_t voff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, voff, 0, CPOL);
 }
 
 // ---------------------------------------------------------------------------
@@ -244,45 +249,6 @@ struct TileIO {
       dst[4 * i + 1] = v.y;
       dst[4 * i + 2] = v.z;
       dst[4 * i + 3] = v.w;
-    }
-    wave_lds_sync();
-  }
-
-  // Lane r holds columns [16C, 16C + cols) of row r in src[0 .. cols);
-  // write rows [0, nrows), columns < L to HBM with coalesced stores.
-  template <int C>
-  __device__ static __forceinline__ void store(__amdgpu_buffer_rsrc_t rs,
-                                               uint32_t rstride, int nrows,
-                                               int L, int lane, int vec,
-                                               float* stage, const float* src) {
-    constexpr int nc = G::cols(C);
-#pragma unroll
-    for (int i = 0; i < nc / 4; ++i) {
-      *reinterpret_cast<float4*>(stage + lane * kStride + 4 * i) =
-          make_float4(src[4 * i + 0], src[4 * i + 1], src[4 * i + 2],
-                      src[4 * i + 3]);
-    }
-    wave_lds_sync();
-    constexpr int qpr = nc / 4;
-    constexpr int rpi = kWave / qpr;
-    const int r0 = lane / qpr;
-    const int q = lane % qpr;
-    const int col = kChunk * C + 4 * q;
-    const uint32_t off = ((uint32_t)r0 * rstride + (uint32_t)col) * 4u;
-#pragma unroll
-    for (int k = 0; k < qpr; ++k) {
-      const float4 v = *reinterpret_cast<const float4*>(
-          stage + (rpi * k + r0) * kStride + 4 * q);
-      const uint32_t soff = (uint32_t)(k * rpi) * rstride * 4u;
-      const bool row_ok = r0 < nrows - k * rpi;
-      if (vec) {
-        buf_store4(v, rs, row_ok && col < L ? off : kOob, soff);
-      } else {
-        buf_store1(v.x, rs, row_ok && col + 0 < L ? off + 0u : kOob, soff);
-        buf_store1(v.y, rs, row_ok && col + 1 < L ? off + 4u : kOob, soff);
-        buf_store1(v.z, rs, row_ok && col + 2 < L ? off + 8u : kOob, soff);
-        buf_store1(v.w, rs, row_ok && col + 3 < L ? off + 12u : kOob, soff);
-      }
     }
     wave_lds_sync();
   }
@@ -537,7 +503,7 @@ __global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kerne
           uint32_t row, col;
           flat_rc(e, uL, lmagic, row, col);
           const float4 y4 = *reinterpret_cast<const float4*>(tile + row * S + col);
-          buf_store4<STORE_CPOL>(y4, rout, e * 4u, 0);
+          buf_store4<STORE_CPOL>(y4, rout, e * 4u);
         }
       }
     } else {
@@ -549,7 +515,7 @@ __global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kerne
         if (e < tile_elems) {
           uint32_t row, col;
           flat_rc(e, uL, lmagic, row, col);
-          buf_store1<STORE_CPOL>(tile[row * S + col], rout, e * 4u, 0);
+          buf_store1<STORE_CPOL>(tile[row * S + col], rout, e * 4u);
         }
       }
     }

@@ -118,12 +118,28 @@ def test_workspace_bytes(lib):
     from pathtile_amd import _lib
 
     out = ctypes.c_size_t(0)
-    st = lib.pt_dwconv1d_dk_det_workspace_bytes(16384, 128, 48, 48, 256, ctypes.byref(out))
-    assert st == _lib.PT_OK
-    # [H, K, num_btiles] floats; num_btiles * tile covers B
-    nbt = out.value // (128 * 48 * 4)
-    assert out.value == 128 * 48 * 4 * nbt and nbt >= 1
-    assert nbt * (256 // 64) * 64 >= 16384 / 16  # tiles cover the batch
+
+    def nbt(B, H, L, K, threads):
+        st = lib.pt_dwconv1d_dk_det_workspace_bytes(B, H, L, K, threads, ctypes.byref(out))
+        assert st == _lib.PT_OK
+        assert out.value % (H * K * 4) == 0  # [H, K, num_btiles] floats
+        return out.value // (H * K * 4)
+
+    # Batch tiles of (threads / 64) waves x rows-per-wave samples cover the
+    # batch with at most one partial tile; rows per wave come from the shape
+    # (16..128 samples, multiples of 16), not from the device.
+    for (B, H, L, K) in [(16384, 128, 48, 48), (16384, 64, 16, 3), (1000, 96, 37, 48),
+                         (32768, 256, 48, 4), (20, 4, 8, 3)]:
+        for threads in (64, 256, 768):
+            wpb = threads // 64
+            n = nbt(B, H, L, K, threads)
+            rpw_min = -(-B // (n * wpb))          # rows per wave needed to cover B
+            assert n >= 1
+            assert any(r * wpb * n >= B and r * wpb * (n - 1) < B
+                       for r in range(16, 129, 16)), (B, H, threads, n, rpw_min)
+    assert nbt(16384, 128, 48, 48, 256) == 32   # 128 samples per wave
+    assert nbt(16384, 64, 16, 3, 64) == 256     # B*H/16384 = 64 samples per wave
+    assert nbt(1000, 96, 37, 48, 64) == 63      # 16 samples per wave
     st = lib.pt_dwconv1d_dk_det_workspace_bytes(0, 4, 8, 3, 256, ctypes.byref(out))
     assert st == _lib.PT_OK and out.value == 0
     lds = ctypes.c_int(0)
