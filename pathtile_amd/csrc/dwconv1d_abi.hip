@@ -42,6 +42,14 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p,
 // Dispatch helpers
 // ---------------------------------------------------------------------------
 static int mfma_index(int L) { return (L + 15) / 16 - 1; }
+
+// Static LDS of dwconv_dk_mfma_kernel<LMAX> (the workgroup's D, LMAX x
+// (LMAX + 1) floats).
+static int dk_mfma_static_lds(int L) {
+  const int lmax = 16 * (mfma_index(L) + 1);
+  return lmax * (lmax + 1) * (int)sizeof(float);
+}
+
 static int lbucket_index(int L) { return (L + 7) / 8 - 1; }
 static int kbucket_index(int K) {
   for (int i = 0; i < kNumKB; ++i)
@@ -140,6 +148,7 @@ static DkAlgo dk_algo(int L, int K) {
 // of the XCDs then stay within a compact address range), fewer at small
 // shapes so the grid still fills the GPU.
 constexpr long long kDkRowsDivisor = 16384;
+constexpr double kDkMallBytes = 256.0 * 1024 * 1024;  // MI355X Infinity Cache
 
 struct DkGeom {
   DkAlgo algo;
@@ -167,10 +176,14 @@ static DkGeom dk_geometry(int B, int H, int L, int K, int threads) {
     g.rows_per_wave = (int)R;
     tile = wpb * R * kWave;
   } else {
-    rpw = (rpw + 15) / 16 * 16;
-    if (rpw < 16) rpw = 16;
-    if (rpw > 128) rpw = 128;
-    const long long rmax = (((long long)B + wpb - 1) / wpb + 15) / 16 * 16;
+    // Samples per load group of the MFMA kernel: 48 / 24 / 16 for row
+    // buckets 16 / 32 / 48; rows per wave are whole groups.
+    const long long grp = 48 / ((L + 15) / 16);
+    const long long rcap = (128 + grp - 1) / grp * grp;
+    rpw = (rpw + grp - 1) / grp * grp;
+    if (rpw < grp) rpw = grp;
+    if (rpw > rcap) rpw = rcap;
+    const long long rmax = (((long long)B + wpb - 1) / wpb + grp - 1) / grp * grp;
     if (rpw > rmax) rpw = rmax;
     g.rows_per_wave = (int)rpw;
     tile = wpb * rpw;
@@ -232,6 +245,61 @@ static int max_lds_per_block() {
   return n;
 }
 
+static int lds_per_cu() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    dev = 0;
+  }
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
+                            dev) != hipSuccess ||
+      n <= 0) {
+    (void)hipGetLastError();
+    n = max_lds_per_block();
+  }
+  if (dev >= 0 && dev < 64) cache[dev] = n;
+  return n;
+}
+
+// Dynamic LDS that makes exactly `bpc` workgroups fit on a CU (at least
+// `need` bytes, at most what one workgroup may allocate): the CU's LDS split
+// bpc ways, in 1 KiB units so allocation granules never round bpc shares
+// past the CU's capacity.
+static size_t lds_for_blocks_per_cu(size_t need, size_t static_bytes, int bpc) {
+  size_t share = (size_t)lds_per_cu() / (size_t)bpc / 1024 * 1024;
+  if (share > (size_t)max_lds_per_block()) share = (size_t)max_lds_per_block();
+  const size_t dyn = share > static_bytes ? share - static_bytes : 0;
+  return dyn > need ? dyn : need;
+}
+
+// Useful FMAs of one row: sum over taps j of the outputs t whose input
+// t + j - p lies in [0, L).
+static long long useful_fma_per_row(int L, int K) {
+  long long n = 0;
+  const int p = K / 2;
+  for (int j = 0; j < K; ++j) {
+    const int s = j - p;
+    const int lo = s < 0 ? -s : 0;
+    const int hi = s > 0 ? L - s : L;
+    if (hi > lo) n += hi - lo;
+  }
+  return n;
+}
+
+// Resident waves per CU for the FWD/DX kernel, measured on MI355X over every
+// (row bucket, tap bucket) at B16384 H128: two waves per SIMD when the FMA
+// chain is long (at least 0.7 L FMAs per element) so one wave's FMAs hide
+// the other's memory time, or when tiles are small (L <= 16); one wave per
+// SIMD otherwise, which streams HBM best. Waves per workgroup do not change
+// this count, so they barely change the time.
+static int rows_waves_per_cu(int L, int K) {
+  if (L <= 16) return 8;
+  return 10 * useful_fma_per_row(L, K) >= 7LL * L * L ? 8 : 4;
+}
+
 static long long gcd_ll(long long a, long long b) {
   while (b) {
     const long long t = a % b;
@@ -250,8 +318,10 @@ static int rows_path(bool dx, const float* in, const float* w, float* out,
   if (!in || !w || !out) return PT_ERR_NULL;
   if (!aligned(in, 4) || !aligned(w, 4) || !aligned(out, 4))
     return PT_ERR_ALIGN;
-  const size_t lds = (size_t)wpb * rows_lds_per_wave(L);
-  if (lds > (size_t)max_lds_per_block()) return PT_ERR_CONFIG;
+  const size_t lds_need = (size_t)wpb * rows_lds_per_wave(L);
+  if (lds_need > (size_t)max_lds_per_block()) return PT_ERR_CONFIG;
+  const int wpc = rows_waves_per_cu(L, K);
+  const size_t lds = lds_for_blocks_per_cu(lds_need, 0, wpb >= wpc ? 1 : wpc / wpb);
   const bool vec = (L % 4 == 0) && aligned(in, 16) && aligned(out, 16);
   if (wpb * kWave > rows_max_threads(8 * (lbucket_index(L) + 1), vec))
     return PT_ERR_CONFIG;
@@ -287,8 +357,17 @@ static int dk_path(bool det, const float* gy, const float* x, float* dst,
   int rpw = g.rows_per_wave, nbt = g.nbt, d = det ? 1 : 0;
   if (g.algo == kDkMfma) {
     DkMfmaFn fn = kDkMfmaTable[mfma_index(L)];
+    // One-wave workgroups on inputs larger than the 256 MiB MALL stream HBM
+    // best at 12 resident waves per CU (3 per SIMD) rather than the 16 the
+    // registers allow; smaller inputs are latency-bound and keep them all.
+    size_t lds = 0;
+    const double bytes = 8.0 * (double)B * (double)H * (double)L;
+    if (threads == kWave && bytes > kDkMallBytes) {
+      const size_t stat = (size_t)dk_mfma_static_lds(L);
+      lds = lds_for_blocks_per_cu(0, stat, 12);
+    }
     void* args[] = {&gy, &x, &dst, &B, &H, &L, &K, &rpw, &nbt, &nblocks, &d};
-    return launch((const void*)fn, nblocks, (uint32_t)threads, 0, stream,
+    return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream,
                   args);
   }
   const bool vec = (L % 4 == 0) && aligned(gy, 16) && aligned(x, 16);

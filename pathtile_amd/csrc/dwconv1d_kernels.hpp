@@ -660,7 +660,10 @@ __global__ __launch_bounds__(1024) void dwconv_dk_mfma_kernel(
     uint32_t nblocks, int det) {
   using M = MfmaGeo<LMAX>;
   constexpr int NT = M::nt;
-  constexpr int kSteps = 4;  // 4-sample steps per load group (16 samples)
+  // 4-sample steps per load group: 48 samples at LMAX = 16, 24 at 32, 16 at
+  // 48, so a group moves about the same bytes whatever the row length (the
+  // operand registers, 4 * kSteps * NT, stay at 48).
+  constexpr int kSteps = 12 / NT;
   __shared__ float dsum[M::dfloats];  // workgroup sum of the waves' D
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -691,7 +694,7 @@ __global__ __launch_bounds__(1024) void dwconv_dk_mfma_kernel(
     const uint32_t step_bytes = 4u * rstride * 4u;
     const int ngroups = (nrow + 4 * kSteps - 1) / (4 * kSteps);
 
-    // Operands of one group of kSteps steps (16 samples).
+    // Operands of one group of kSteps steps (4 * kSteps samples).
     auto load_group = [&](int g, float (&av)[kSteps][NT], float (&bv)[kSteps][NT]) {
 #pragma unroll
       for (int u = 0; u < kSteps; ++u) {

@@ -126,20 +126,24 @@ def test_workspace_bytes(lib):
         return out.value // (H * K * 4)
 
     # Batch tiles of (threads / 64) waves x rows-per-wave samples cover the
-    # batch with at most one partial tile; rows per wave come from the shape
-    # (16..128 samples, multiples of 16), not from the device.
+    # batch with at most one partial tile. Rows per wave come from the shape
+    # (not the device) and are whole load groups of the matrix-core kernel:
+    # 48 / 24 / 16 samples for rows of <= 16 / <= 32 / <= 48 floats, up to
+    # 128 samples rounded up to a whole group.
     for (B, H, L, K) in [(16384, 128, 48, 48), (16384, 64, 16, 3), (1000, 96, 37, 48),
-                         (32768, 256, 48, 4), (20, 4, 8, 3)]:
+                         (32768, 256, 48, 4), (20, 4, 8, 3), (4096, 128, 24, 8)]:
+        grp = 48 // (-(-L // 16))
+        top = 128
         for threads in (64, 256, 768):
             wpb = threads // 64
             n = nbt(B, H, L, K, threads)
-            rpw_min = -(-B // (n * wpb))          # rows per wave needed to cover B
             assert n >= 1
             assert any(r * wpb * n >= B and r * wpb * (n - 1) < B
-                       for r in range(16, 129, 16)), (B, H, threads, n, rpw_min)
+                       for r in range(grp, top + grp, grp)), (B, H, L, threads, n)
     assert nbt(16384, 128, 48, 48, 256) == 32   # 128 samples per wave
-    assert nbt(16384, 64, 16, 3, 64) == 256     # B*H/16384 = 64 samples per wave
-    assert nbt(1000, 96, 37, 48, 64) == 63      # 16 samples per wave
+    assert nbt(16384, 64, 16, 3, 64) == 171     # 64 samples -> 96, two groups of 48
+    assert nbt(16384, 64, 16, 3, 256) == 43     # four waves x 96 samples per tile
+    assert nbt(1000, 96, 37, 48, 64) == 63      # one group of 16 samples per wave
     st = lib.pt_dwconv1d_dk_det_workspace_bytes(0, 4, 8, 3, 256, ctypes.byref(out))
     assert st == _lib.PT_OK and out.value == 0
     lds = ctypes.c_int(0)
