@@ -50,6 +50,7 @@ extern "C" {
 #define PT_KERNEL_DX 1
 #define PT_KERNEL_DK 2
 #define PT_KERNEL_DK_REDUCE 3
+#define PT_KERNEL_DK_CG 4      /* channel-group DK (L % 4 == 0, H % (4 * waves) == 0) */
 
 /* Version of this ABI (PT_ABI_VERSION). */
 int pt_abi_version(void);

@@ -152,18 +152,51 @@ constexpr double kDkMallBytes = 256.0 * 1024 * 1024;  // MI355X Infinity Cache
 
 struct DkGeom {
   DkAlgo algo;
+  bool cg;            // channel-group kernel
   int wpb;
-  int rows_per_wave;  // VALU: 64-sample chunks per wave; MFMA: samples
-  int nbt;
-  long long nblocks;
+  int rows_per_wave;  // VALU: 64-sample chunks per wave; MFMA: samples;
+                      // channel-group: samples per workgroup
+  int nbt;            // partials per (h, j): batch tiles / sample ranges
+  long long nblocks;  // workgroups
 };
 
-static DkGeom dk_geometry(int B, int H, int L, int K, int threads) {
+// Channel-group DK: whole 16-byte aligned rows (L % 4 == 0) in groups of
+// kCgChannelsPerWave channels per wave, at most 8 waves per workgroup.
+static bool dk_cg_ok(int H, int L, int threads) {
+  const int wpb = threads / kWave;
+  return L % 4 == 0 && wpb <= 8 && H % (kCgChannelsPerWave * wpb) == 0;
+}
+
+// Interleaved sample ranges of the channel-group DK: the power of two
+// (8 .. 256) nearest to 2.5 MiB / (bytes of one 4-sample step of one
+// tensor), so a workgroup's successive steps lie about 2.5 MiB apart; that
+// stride measured best on MI355X from H = 64 to 256 and L = 16 to 48. It
+// depends on the shape only (not on the block size or the device).
+static long long cg_ranges(int B, int H, int L) {
+  const double step_bytes = 16.0 * (double)H * (double)L;
+  const double want = 2.5 * 1024 * 1024 / step_bytes;
+  long long nr = 8;
+  while (nr < 256 && (double)(nr * 2) <= want * 1.41421356) nr *= 2;
+  const long long tsteps = ((long long)B + kCgStep - 1) / kCgStep;
+  if (nr > tsteps) nr = tsteps;
+  return nr < 1 ? 1 : nr;
+}
+
+static DkGeom dk_geometry(int B, int H, int L, int K, int threads, bool vec16) {
   DkGeom g;
   g.algo = dk_algo(L, K);
   g.wpb = threads / kWave;
   const long long wpb = g.wpb;
   const long long rows = (long long)B * H;
+  g.cg = g.algo == kDkMfma && vec16 && dk_cg_ok(H, L, threads);
+  if (g.cg) {
+    const long long ngroups = (long long)H / (kCgChannelsPerWave * wpb);
+    const long long nr = cg_ranges(B, H, L);
+    g.rows_per_wave = 0;
+    g.nbt = (int)nr;
+    g.nblocks = ngroups * nr;
+    return g;
+  }
   long long rpw = (rows + kDkRowsDivisor - 1) / kDkRowsDivisor;
   long long tile;
   if (g.algo == kDkValu) {
@@ -355,6 +388,13 @@ static int dk_path(bool det, const float* gy, const float* x, float* dst,
                    void* stream) {
   uint32_t nblocks = (uint32_t)g.nblocks;
   int rpw = g.rows_per_wave, nbt = g.nbt, d = det ? 1 : 0;
+  if (g.cg) {
+    DkCgFn fn = kDkCgTable[mfma_index(L)];
+    const size_t lds = cg_lds_bytes(16 * (mfma_index(L) + 1), g.wpb, L);
+    void* args[] = {&gy, &x, &dst, &B, &H, &L, &K, &nbt, &nblocks, &d};
+    return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream,
+                  args);
+  }
   if (g.algo == kDkMfma) {
     DkMfmaFn fn = kDkMfmaTable[mfma_index(L)];
     // One-wave workgroups on inputs larger than the 256 MiB MALL stream HBM
@@ -387,6 +427,7 @@ static const void* kernel_for(int kernel_id, int L, int K) {
       return dk_algo(L, K) == kDkMfma ? (const void*)kDkMfmaTable[mfma_index(L)]
                                       : (const void*)kDkTableV[li][ki];
     case PT_KERNEL_DK_REDUCE: return (const void*)&dk_reduce_kernel;
+    case PT_KERNEL_DK_CG: return (const void*)kDkCgTable[mfma_index(L)];
     default: return nullptr;
   }
 }
@@ -440,7 +481,8 @@ int pt_dwconv1d_dk_atomic_f32(const float* dy, const float* x, float* dk,
   if (B == 0) return PT_OK;
   if (!dy || !x) return PT_ERR_NULL;
   if (!pt::aligned(dy, 4) || !pt::aligned(x, 4)) return PT_ERR_ALIGN;
-  const pt::DkGeom g = pt::dk_geometry(B, H, L, K, threads_per_block);
+  const pt::DkGeom g = pt::dk_geometry(
+      B, H, L, K, threads_per_block, pt::aligned(dy, 16) && pt::aligned(x, 16));
   if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
   return pt::dk_path(false, dy, x, dk, B, H, L, K, threads_per_block, g,
                      stream);
@@ -456,8 +498,12 @@ int pt_dwconv1d_dk_det_workspace_bytes(int B, int H, int L, int K,
     *bytes = 0;
     return PT_OK;
   }
-  const pt::DkGeom g = pt::dk_geometry(B, H, L, K, threads_per_block);
-  *bytes = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
+  // Either kernel may serve the call (the channel-group one needs 16-byte
+  // aligned inputs): size for the larger partial count.
+  const pt::DkGeom g0 = pt::dk_geometry(B, H, L, K, threads_per_block, false);
+  const pt::DkGeom g1 = pt::dk_geometry(B, H, L, K, threads_per_block, true);
+  const int nbt = g0.nbt > g1.nbt ? g0.nbt : g1.nbt;
+  *bytes = (size_t)H * (size_t)K * (size_t)nbt * sizeof(float);
   return PT_OK;
 }
 
@@ -474,7 +520,8 @@ int pt_dwconv1d_dk_det_f32(const float* dy, const float* x, float* dk,
   if (B == 0) return pt::zero_fill(dk, H * K, stream);
   if (!dy || !x) return PT_ERR_NULL;
   if (!pt::aligned(dy, 4) || !pt::aligned(x, 4)) return PT_ERR_ALIGN;
-  const pt::DkGeom g = pt::dk_geometry(B, H, L, K, threads_per_block);
+  const pt::DkGeom g = pt::dk_geometry(
+      B, H, L, K, threads_per_block, pt::aligned(dy, 16) && pt::aligned(x, 16));
   if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
   const size_t need = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
   if (!workspace || workspace_bytes < need) return PT_ERR_WORKSPACE;
@@ -527,6 +574,12 @@ int pt_dynamic_lds_bytes(int kernel_id, int L, int K, int block_config,
       return PT_OK;
     case PT_KERNEL_DK_REDUCE:
       *lds_bytes = 0;
+      return PT_OK;
+    case PT_KERNEL_DK_CG:
+      if (!pt::valid_dk_threads(block_config) || block_config > 8 * pt::kWave)
+        return PT_ERR_CONFIG;
+      *lds_bytes = (int)pt::cg_lds_bytes(16 * (pt::mfma_index(L) + 1),
+                                         block_config / pt::kWave, L);
       return PT_OK;
     default:
       return PT_ERR_CONFIG;

@@ -778,4 +778,240 @@ __global__ __launch_bounds__(1024) void dwconv_dk_mfma_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// DK on channel-group tiles (matrix cores). For a sample b the rows of
+// channels [g*HC, g*HC + HC) are one contiguous segment of HC * L floats, so
+// a workgroup that owns channel group g streams whole segments instead of
+// one 192-byte row per channel: full cache lines, and no line shared with a
+// channel that another workgroup reads.
+//
+// Workgroup (g, r) owns channel group g of HC = kCgChannelsPerWave * wpb
+// channels and the interleaved steps r, r + nranges, r + 2 nranges, ... of
+// 4 samples each. At any moment the running workgroups therefore cover one
+// compact window of nranges steps of the whole [b, :, :] tensor; the host
+// picks nranges so that a workgroup's successive steps lie about 2.5 MiB
+// apart (contiguous per-workgroup sample ranges instead put every workgroup
+// a fixed multi-MiB stride apart, and the time then swung by 30 % with that
+// stride on MI355X).
+//
+// Per step the workgroup loads both tensors' segments (dwordx4; rows are
+// 16-byte aligned, L % 4 == 0) into registers two steps ahead and into one
+// of two LDS stages while the matrix cores consume the other; wave w
+// accumulates D_c[t][s] = sum_b dy[b,c,t] * x[b,c,s] for its channels, then
+// reduces the diagonals of each D_c (dk[c, j] = sum_t D_c[t][t + j - p])
+// through a per-wave LDS tile: one atomic (or one partial) per tap and
+// channel per workgroup.
+// ---------------------------------------------------------------------------
+constexpr int kCgChannelsPerWave = 2;
+constexpr int kCgStep = 4;      // samples per stage (the MFMA K)
+constexpr int kCgPad = 16;      // floats between the samples of a stage
+constexpr int kCgDepth = 2;     // steps in flight in registers
+
+template <int LMAX>
+struct CgGeo {
+  static constexpr int nt = LMAX / 16;
+  static constexpr int dim = 16 * nt;
+  static constexpr int dstride = dim + 1;
+};
+
+// Dynamic LDS of the channel-group DK kernel: two stages of both tensors,
+// or, for the epilogue, one D tile per wave plus the workgroup's tap sums.
+__host__ __device__ constexpr size_t cg_lds_bytes(int lmax, int wpb, int L) {
+  const size_t stages =
+      (size_t)2 * 2 * kCgStep * (kCgChannelsPerWave * wpb * L + kCgPad);
+  const size_t dtile = (size_t)wpb * (16 * (lmax / 16)) * (16 * (lmax / 16) + 1) +
+                       (size_t)kCgChannelsPerWave * wpb * kMaxK;
+  return (stages > dtile ? stages : dtile) * sizeof(float);
+}
+
+template <int LMAX>
+__global__ __launch_bounds__(512) void dwconv_dk_cg_kernel(
+    const float* __restrict__ gy, const float* __restrict__ x,
+    float* __restrict__ dst, int B, int H, int L, int K, int nranges,
+    uint32_t nblocks, int det) {
+  using G = CgGeo<LMAX>;
+  constexpr int NT = G::nt;
+  constexpr int CPW = kCgChannelsPerWave;
+  constexpr int DEPTH = kCgDepth;
+  extern __shared__ float lds[];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wpb = blockDim.x / kWave;
+  const int nthreads = blockDim.x;
+  const int hc = CPW * wpb;
+  const int ngroups = H / hc;
+  const uint32_t blk = xcd_remap(blockIdx.x, nblocks);
+  const int g = (int)(blk % (uint32_t)ngroups);
+  const int r = (int)(blk / (uint32_t)ngroups);
+  const int tsteps = (B + kCgStep - 1) / kCgStep;
+  const int nsteps = r < tsteps ? (tsteps - 1 - r) / nranges + 1 : 0;
+
+  const int seg = hc * L;                     // floats per sample segment
+  const int seg4 = seg >> 2;                  // float4 per segment
+  const int sk = seg + kCgPad;                // LDS stride between samples
+  const int sz = kCgStep * sk;                // one tensor's stage
+  const int per = kCgStep * seg4;             // float4 per stage and tensor
+  constexpr int kNpt = (CPW * LMAX + kWave - 1) / kWave;  // per thread, tensor
+  const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;  // one sample
+  const uint32_t grp_bytes = (uint32_t)g * (uint32_t)seg * 4u;
+
+  // Loop-invariant part of each staged element: its sample within the
+  // step, its byte offset from the step's first sample, its LDS offset.
+  int ek[kNpt];
+  uint32_t eoff[kNpt], elds[kNpt];
+#pragma unroll
+  for (int i = 0; i < kNpt; ++i) {
+    const int e = i * nthreads + (int)threadIdx.x;
+    const int k = e < per ? e / seg4 : kCgStep;  // kCgStep: no element
+    const int q = e - (e / seg4) * seg4;
+    ek[i] = k;
+    eoff[i] = (uint32_t)k * row_bytes + grp_bytes + 16u * (uint32_t)q;
+    elds[i] = (uint32_t)(k * sk + 4 * q);
+  }
+
+  // Global -> registers for local step s (global step r + s * nranges):
+  // buffer resources rebased on the step's first sample; elements past the
+  // stage or past B read 0 (no branch).
+  float4 stg[DEPTH][2][kNpt];
+  auto load_step = [&](int s, float4 (&st)[2][kNpt]) {
+    const int bs = (r + s * nranges) * kCgStep;
+    const size_t r0 = (size_t)bs * (size_t)H * (size_t)L;
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(gy + r0);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + r0);
+    const int klim = min(kCgStep, B - bs);
+#pragma unroll
+    for (int i = 0; i < kNpt; ++i) {
+      const uint32_t o = ek[i] < klim ? eoff[i] : kOob;
+      st[0][i] = buf_load4(rg, o, 0);
+      st[1][i] = buf_load4(rx, o, 0);
+    }
+  };
+  auto store_stage = [&](int buf, const float4 (&st)[2][kNpt]) {
+    float* base = lds + buf * 2 * sz;
+#pragma unroll
+    for (int i = 0; i < kNpt; ++i) {
+      if (ek[i] < kCgStep) {
+        *reinterpret_cast<float4*>(base + elds[i]) = st[0][i];
+        *reinterpret_cast<float4*>(base + sz + elds[i]) = st[1][i];
+      }
+    }
+  };
+
+  f32x4 acc[CPW][NT][NT];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c)
+#pragma unroll
+    for (int a = 0; a < NT; ++a)
+#pragma unroll
+      for (int b = 0; b < NT; ++b) acc[c][a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int kq = lane >> 4;   // sample of the step
+  const int col = lane & 15;  // column within a 16-wide tile
+  auto mfma_step = [&](int s) {
+    const float* gdy = lds + (s & 1) * 2 * sz + kq * sk;
+    const float* gxx = gdy + sz;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const int cb = (wave * CPW + c) * L;
+      float av[NT], bv[NT];
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) {
+        // Columns >= L (rows shorter than the bucket) read a clamped
+        // address and are zeroed, without a branch.
+        const int cc = 16 * tt + col;
+        const int ca = cc < L ? cc : L - 1;
+        const float va = gdy[cb + ca], vb = gxx[cb + ca];
+        av[tt] = cc < L ? va : 0.f;
+        bv[tt] = cc < L ? vb : 0.f;
+      }
+#pragma unroll
+      for (int a = 0; a < NT; ++a)
+#pragma unroll
+        for (int b = 0; b < NT; ++b)
+          acc[c][a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a], bv[b],
+                                                              acc[c][a][b], 0, 0, 0);
+    }
+  };
+
+  if (nsteps > 0) {
+    // Local step s lives in stg[s % DEPTH] until it is stored to LDS stage
+    // s % 2; the loop is unrolled by DEPTH so register indices are static.
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+      if (d < nsteps) load_step(d, stg[d]);
+    store_stage(0, stg[0]);
+    if (DEPTH < nsteps) load_step(DEPTH, stg[0]);
+    __syncthreads();
+    for (int s0 = 0; s0 < nsteps; s0 += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        const int s = s0 + d;
+        if (s < nsteps) {
+          mfma_step(s);
+          if (s + 1 < nsteps) {
+            store_stage((s + 1) & 1, stg[(d + 1) % DEPTH]);
+            if (s + 1 + DEPTH < nsteps) load_step(s + 1 + DEPTH, stg[(d + 1) % DEPTH]);
+          }
+          __syncthreads();
+        }
+      }
+    }
+  }
+
+  // Per-wave epilogue: D_c through the wave's own LDS tile (the stages are
+  // free after the last barrier), then lane j < K sums D_c[t][t + j - p]
+  // over t in [t0, t1) in four fixed-order partial sums, all reads issued
+  // at once (the t loop is unrolled over the bucket, out-of-range terms
+  // masked). The workgroup's channels are consecutive, so its hc x K tap
+  // sums are one contiguous block of dk: they are collected in LDS and added
+  // with one coalesced atomic per element (a few cache lines per workgroup,
+  // not one line operation per wave and channel, which contended badly at
+  // small K).
+  float* dt = lds + wave * (G::dim * G::dstride);
+  float* taps = lds + wpb * (G::dim * G::dstride);  // [hc][K]
+  const int rq = 4 * (lane >> 4);
+  const int cl = lane & 15;
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+#pragma unroll
+    for (int a = 0; a < NT; ++a)
+#pragma unroll
+      for (int b = 0; b < NT; ++b)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          dt[(16 * a + rq + rr) * G::dstride + 16 * b + cl] = acc[c][a][b][rr];
+    wave_lds_sync();
+    const int hl = wave * CPW + c;  // channel within the group
+    if (lane < K) {
+      const int j = lane;
+      const int m = j - (K >> 1);
+      const int t0 = max(0, -m);
+      const int t1 = min(L, L - m);
+      float v4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int t = 0; t < G::dim; ++t) {
+        // D_c[t][t + m] = dt[m + t * (dstride + 1)]; masked terms read a
+        // clamped in-tile address (a tap may have no valid t at all).
+        int idx = m + t * (G::dstride + 1);
+        idx = idx < 0 ? 0 : (idx < G::dim * G::dstride ? idx : G::dim * G::dstride - 1);
+        const float d = dt[idx];
+        v4[t & 3] += (t >= t0 && t < t1) ? d : 0.0f;
+      }
+      const float v = (v4[0] + v4[1]) + (v4[2] + v4[3]);
+      if (det) {
+        dst[((size_t)(g * hc + hl) * K + j) * (size_t)nranges + r] = v;
+      } else {
+        taps[hl * K + j] = v;
+      }
+    }
+    wave_lds_sync();
+  }
+  if (!det) {
+    __syncthreads();
+    float* out = dst + (size_t)g * hc * K;
+    for (int e = threadIdx.x; e < hc * K; e += nthreads) atomicAdd(out + e, taps[e]);
+  }
+}
+
 }  // namespace pt

@@ -28,5 +28,9 @@ extern const DkFn kDkTableV[kNumLB][kNumKB];
 extern const DkFn kDkTableS[kNumLB][kNumKB];
 // matrix-core DK by row bucket 16, 32, 48
 extern const DkMfmaFn kDkMfmaTable[3];
+using DkCgFn = void (*)(const float*, const float*, float*, int, int, int, int,
+                        int, uint32_t, int);
+// channel-group matrix-core DK by row bucket 16, 32, 48
+extern const DkCgFn kDkCgTable[3];
 
 }  // namespace pt

@@ -1,4 +1,4 @@
-// Instantiates the matrix-core DK kernels.
+// Instantiates the matrix-core DK kernels (per-channel and channel-group).
 #include "dwconv1d_kernels.hpp"
 #include "dwconv1d_tables.hpp"
 
@@ -6,4 +6,7 @@ namespace pt {
 const DkMfmaFn kDkMfmaTable[3] = {&dwconv_dk_mfma_kernel<16>,
                                   &dwconv_dk_mfma_kernel<32>,
                                   &dwconv_dk_mfma_kernel<48>};
+const DkCgFn kDkCgTable[3] = {&dwconv_dk_cg_kernel<16>,
+                              &dwconv_dk_cg_kernel<32>,
+                              &dwconv_dk_cg_kernel<48>};
 }  // namespace pt

@@ -125,25 +125,41 @@ def test_workspace_bytes(lib):
         assert out.value % (H * K * 4) == 0  # [H, K, num_btiles] floats
         return out.value // (H * K * 4)
 
-    # Batch tiles of (threads / 64) waves x rows-per-wave samples cover the
-    # batch with at most one partial tile. Rows per wave come from the shape
-    # (not the device) and are whole load groups of the matrix-core kernel:
-    # 48 / 24 / 16 samples for rows of <= 16 / <= 32 / <= 48 floats, up to
-    # 128 samples rounded up to a whole group.
-    for (B, H, L, K) in [(16384, 128, 48, 48), (16384, 64, 16, 3), (1000, 96, 37, 48),
-                         (32768, 256, 48, 4), (20, 4, 8, 3), (4096, 128, 24, 8)]:
+    # Two kernels can serve a call (the channel-group one needs 16-byte
+    # aligned rows), so the workspace holds the larger partial count:
+    #  * per-channel batch tiles of (threads / 64) waves x rows-per-wave
+    #    samples; rows per wave are whole load groups (48 / 24 / 16 samples
+    #    for rows of <= 16 / <= 32 / <= 48 floats), up to 128 samples;
+    #  * channel-group interleaved sample ranges (L % 4 == 0, <= 8 waves, H a
+    #    multiple of 2 * waves): the power of two in [8, 256] nearest to
+    #    2.5 MiB / (16 H L bytes), at most one per 4-sample step.
+    # Both depend on the shape and block size only, never on the device.
+    def per_channel(B, H, L, wpb):
         grp = 48 // (-(-L // 16))
-        top = 128
-        for threads in (64, 256, 768):
+        rpw = -(-(B * H) // 16384)
+        rpw = min(max(-(-rpw // grp) * grp, grp), -(-128 // grp) * grp)
+        rpw = min(rpw, -(-(-(-B // wpb)) // grp) * grp)
+        return -(-B // (wpb * rpw))
+
+    def channel_group(B, H, L, wpb):
+        if L % 4 or wpb > 8 or H % (2 * wpb):
+            return 0
+        want = 2.5 * 2**20 / (16 * H * L)
+        n = 8
+        while n < 256 and n * 2 <= want * 2**0.5:
+            n *= 2
+        return max(1, min(n, -(-B // 4)))
+
+    for (B, H, L, K) in [(16384, 128, 48, 48), (16384, 64, 16, 3), (1000, 96, 37, 48),
+                         (32768, 256, 48, 4), (20, 4, 8, 3), (4096, 128, 24, 8), (3, 16, 48, 5)]:
+        for threads in (64, 128, 192, 256, 512, 768):
             wpb = threads // 64
             n = nbt(B, H, L, K, threads)
-            assert n >= 1
-            assert any(r * wpb * n >= B and r * wpb * (n - 1) < B
-                       for r in range(grp, top + grp, grp)), (B, H, L, threads, n)
-    assert nbt(16384, 128, 48, 48, 256) == 32   # 128 samples per wave
-    assert nbt(16384, 64, 16, 3, 64) == 171     # 64 samples -> 96, two groups of 48
-    assert nbt(16384, 64, 16, 3, 256) == 43     # four waves x 96 samples per tile
-    assert nbt(1000, 96, 37, 48, 64) == 63      # one group of 16 samples per wave
+            assert n == max(per_channel(B, H, L, wpb), channel_group(B, H, L, wpb)), (B, H, L, threads)
+    assert nbt(16384, 128, 48, 48, 256) == 32   # 32 ranges (98 KiB steps), 32 tiles
+    assert nbt(16384, 64, 16, 3, 256) == 128    # 16 KiB steps: 128 interleaved ranges
+    assert nbt(16384, 128, 48, 48, 192) == 43   # per-channel: 3 waves x 128 samples
+    assert nbt(1000, 96, 37, 48, 64) == 63      # L % 4 != 0: per-channel only
     st = lib.pt_dwconv1d_dk_det_workspace_bytes(0, 4, 8, 3, 256, ctypes.byref(out))
     assert st == _lib.PT_OK and out.value == 0
     lds = ctypes.c_int(0)
