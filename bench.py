@@ -131,6 +131,19 @@ def mean(v):
     return sum(v) / len(v) if v else float("nan")
 
 
+def dk_kernel_name(H: int, L: int, threads: int) -> str:
+    """The DK kernel the library picks for 16-byte aligned inputs: the
+    channel-group matrix-core kernel when rows are whole float4 (L % 4 == 0)
+    and H is a multiple of 2 x waves per workgroup (at most 8 waves), else
+    the per-channel matrix-core kernel (or the VALU kernel on request)."""
+    if os.environ.get("PATHTILE_DK_ALGO") == "valu":
+        return "dwconv_dk_kernel"
+    wpb = threads // 64
+    if L % 4 == 0 and wpb <= 8 and H % (2 * wpb) == 0:
+        return "dwconv_dk_cg_kernel"
+    return "dwconv_dk_mfma_kernel"
+
+
 def read_traffic(kernel_tag: str) -> dict | None:
     """HBM bytes per launch of `kernel_tag` from the committed rocprofv3 PMC
     summary (profiles/pmc_traffic_<kernel_tag>.md, lines
@@ -349,8 +362,7 @@ def main(argv=None) -> int:
         "correctness_gate": {k: float(f"{v:.3e}") for k, v in gate.items()},
         "roofline": {
             "kernel": {"fwd": "dwconv_rows_kernel<FWD>", "bwd_input": "dwconv_rows_kernel<DX>",
-                       "bwd_weight": ("dwconv_dk_kernel" if os.environ.get("PATHTILE_DK_ALGO") == "valu"
-                                      else "dwconv_dk_mfma_kernel")}[dominant],
+                       "bwd_weight": dk_kernel_name(H, L, cfg["dk_threads_per_block"])}[dominant],
             "bound": "hbm",
             "achieved": ach,
             "peak": PEAK_HBM_GBPS,

@@ -129,6 +129,51 @@ def test_dk_atomic_and_deterministic(rt, shape, algo, monkeypatch):
             assert np.all(ga[:, j] == 0.0) and np.all(gd1[:, j] == 0.0)
 
 
+def _misaligned(t):
+    """Same values, 4-byte but not 16-byte aligned storage."""
+    flat = torch.zeros(t.numel() + 1, device="cuda:0")
+    flat[1:] = t.reshape(-1).to("cuda:0")
+    v = flat[1:].view(t.shape)
+    assert v.data_ptr() % 16 != 0
+    return v
+
+
+@pytest.mark.parametrize("shape", [
+    (1001, 64, 48, 3),    # ragged last 4-sample step, K = 3 (coalesced atomics)
+    (5, 32, 40, 24),      # fewer steps than interleaved ranges, L < bucket
+    (2048, 128, 20, 9),   # L in the 32 bucket, odd K
+    (4099, 16, 16, 48),   # K > L: zero-overlap taps
+])
+@pytest.mark.parametrize("threads", [64, 128, 256, 512])
+def test_dk_channel_group_matches_per_channel(shape, threads):
+    """16-byte aligned rows with L % 4 == 0 and H a multiple of 2 x waves take
+    the channel-group kernel; the same values in misaligned storage take the
+    per-channel kernel. Both agree with FP64, and the deterministic variant is
+    bitwise reproducible on each path with the workspace the API sizes."""
+    from pathtile_amd import runtime
+
+    B, H, L, K = shape
+    if H % (2 * (threads // 64)):
+        pytest.skip("H not a multiple of the channel group")
+    x, w, dy = _inputs(B, H, L, K, seed=3000 + B + L + K)
+    xd, dyd = _dev(x, dy)
+    xm, dym = _misaligned(x), _misaligned(dy)
+    ref = oracle.dk_f64(dy, x, K)
+    r = runtime.HipWarpRuntime(bwdk_block=threads)
+    for a, b in ((dyd, xd), (dym, xm)):
+        ga = _dk_atomic(r, a, b, K).cpu().numpy()
+        g1 = _dk_det(r, a, b, K).cpu().numpy()
+        g2 = _dk_det(r, a, b, K).cpu().numpy()
+        assert oracle.normalized_max_abs(ga, ref) < DK_TOL
+        assert oracle.normalized_max_abs(g1, ref) < DK_TOL
+        assert np.array_equal(g1, g2)
+        for j in range(K):
+            lo, hi = oracle.valid_tap_range(L, K, j)
+            if hi <= lo:
+                assert np.all(ga[:, j] == 0.0) and np.all(g1[:, j] == 0.0)
+    r.close()
+
+
 def test_golden_c1_fixture(rt):
     from pathlib import Path
 
