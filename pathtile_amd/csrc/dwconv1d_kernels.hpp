@@ -17,10 +17,13 @@
 //     The tile passes through a per-wave LDS transpose (row stride LMAX + 4
 //     floats, bank-conflict free for ds_read/ds_write_b128); each lane keeps
 //     the taps of its own channel (r % H) in VGPRs across a persistent grid;
-//   * DK (dwconv_dk_mfma_kernel, default): a WAVE owns a run of samples b of
-//     one channel h and contracts them on the matrix cores
-//     (v_mfma_f32_16x16x4_f32): D[t][s] = sum_b dy[b][t] * x[b][s]; the taps
-//     are the diagonal sums dk[j] = sum_t D[t][t + j - p];
+//   * DK contracts the batch on the matrix cores (v_mfma_f32_16x16x4_f32):
+//     D_h[t][s] = sum_b dy[b,h,t] * x[b,h,s], and the taps are the diagonal
+//     sums dk[h,j] = sum_t D_h[t][t + j - p]. dwconv_dk_cg_kernel (default
+//     for 16-byte aligned rows, L % 4 == 0) streams contiguous channel-group
+//     segments [b, g*HC .. g*HC+HC, :] with each wave owning two channels;
+//     dwconv_dk_mfma_kernel (any shape) gives a wave a run of samples of one
+//     channel;
 //   * DK (dwconv_dk_kernel, PATHTILE_DK_ALGO=valu): a WAVE owns 64 samples of
 //     one channel; a 16-column strided LDS transpose (TileIO) feeds each lane
 //     its row pair and the lane accumulates every tap on the VALU;
