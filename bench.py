@@ -131,6 +131,23 @@ def mean(v):
     return sum(v) / len(v) if v else float("nan")
 
 
+def rows_kernel_name(H: int, L: int, K: int, dx: bool) -> str:
+    """The FWD/DX kernel the library picks for 16-byte aligned rows: the
+    channel-group matrix-core kernel where the layout allows it (L % 4 == 0,
+    H % 8 == 0) and a row needs >= 10.5 (LMAX / L)^2 useful FMAs per output
+    (LMAX = 16 ceil(L / 16)), else the VALU rows kernel (or either on
+    request through PATHTILE_ROWS_ALGO)."""
+    tag = "DX" if dx else "FWD"
+    algo = os.environ.get("PATHTILE_ROWS_ALGO")
+    p = K // 2
+    useful = sum(max(0, min(L, L - (j - p)) - max(0, p - j)) for j in range(K))
+    lmax = 16 * ((L + 15) // 16)
+    mfma = algo == "mfma" or (algo != "valu" and 2 * useful * L >= 21 * lmax * lmax)
+    if mfma and L % 4 == 0 and H % 8 == 0:
+        return f"dwconv_rows_cg_kernel<{tag}>"
+    return f"dwconv_rows_kernel<{tag}>"
+
+
 def dk_kernel_name(H: int, L: int, threads: int) -> str:
     """The DK kernel the library picks for 16-byte aligned inputs: the
     channel-group matrix-core kernel when rows are whole float4 (L % 4 == 0)
@@ -279,8 +296,7 @@ def main(argv=None) -> int:
         "bwd_weight_zero": lambda: rt.launch_bwd_weight(dy, x, gk, K, zero_first=True),
         "bwd_weight_det": lambda: rt.launch_bwd_weight_deterministic(dy, x, gk, K),
     }
-    loop_ms = {}
-    for ph, fn in loops.items():
+    def time_loop(fn):
         for _ in range(max(1, args.warmup // 4)):
             fn()
         ev0 = torch.cuda.Event(enable_timing=True)
@@ -290,7 +306,21 @@ def main(argv=None) -> int:
             fn()
         ev1.record(stream)
         ev1.synchronize()
-        loop_ms[ph] = ev0.elapsed_time(ev1) / args.steps
+        return ev0.elapsed_time(ev1) / args.steps
+
+    loop_ms = {ph: time_loop(fn) for ph, fn in loops.items()}
+
+    # The VALU rows kernel (the reference's lane-per-row structure, bit-exact
+    # with its fmaf chain) timed beside the default FWD/DX kernel, same loops.
+    prev = os.environ.get("PATHTILE_ROWS_ALGO")
+    os.environ["PATHTILE_ROWS_ALGO"] = "valu"
+    valu_gate = correctness_gate(rt, x, w, dy)
+    valu_ms = {"fwd": time_loop(loops["fwd"]), "bwd_input": time_loop(loops["bwd_input"])}
+    valu_kernels = {"fwd": rows_kernel_name(H, L, K, False), "bwd_input": rows_kernel_name(H, L, K, True)}
+    if prev is None:
+        del os.environ["PATHTILE_ROWS_ALGO"]
+    else:
+        os.environ["PATHTILE_ROWS_ALGO"] = prev
 
     # The reference's per-launch protocol (kernels/warp_tiled_ampere.py:
     # 1059-1070; benchmark/benchmark_pathtile_candidate_sweep.py:274-317):
@@ -323,6 +353,11 @@ def main(argv=None) -> int:
                      "per_launch_event_ms": round(mean(v), 5),
                      "per_launch_event_min_ms": round(min(v), 5)}
     agg = paths["fwd"]["ms"] + paths["bwd_input"]["ms"] + paths["bwd_weight"]["ms"]
+    kernels = {"fwd": rows_kernel_name(H, L, K, False), "bwd_input": rows_kernel_name(H, L, K, True),
+               "bwd_weight": dk_kernel_name(H, L, cfg["dk_threads_per_block"])}
+    for ph in paths:
+        paths[ph]["kernel"] = kernels[{"bwd_weight_zero": "bwd_weight",
+                                       "bwd_weight_det": "bwd_weight"}.get(ph, ph)]
     dominant = max(("fwd", "bwd_input", "bwd_weight"), key=lambda k: paths[k]["ms"])
     tag = {"fwd": "fwd", "bwd_input": "dx", "bwd_weight": "dk"}[dominant]
     ach = paths[dominant]["gbps"]
@@ -360,9 +395,15 @@ def main(argv=None) -> int:
         "algorithmic_bytes_per_path": nbytes,
         "paths": paths,
         "correctness_gate": {k: float(f"{v:.3e}") for k, v in gate.items()},
+        "rows_valu": {
+            ph: {"ms": round(ms, 5), "pct_peak": round(100 * runtime.algorithmic_bandwidth_gbps(nbytes, ms)
+                                                     / PEAK_HBM_GBPS, 2),
+                 "kernel": valu_kernels[ph]}
+            for ph, ms in valu_ms.items()
+        } | {"correctness_gate": {k: float(f"{v:.3e}") for k, v in valu_gate.items()},
+             "note": "PATHTILE_ROWS_ALGO=valu: the bit-exact VALU FWD/DX kernel, same loops"},
         "roofline": {
-            "kernel": {"fwd": "dwconv_rows_kernel<FWD>", "bwd_input": "dwconv_rows_kernel<DX>",
-                       "bwd_weight": dk_kernel_name(H, L, cfg["dk_threads_per_block"])}[dominant],
+            "kernel": kernels[dominant],
             "bound": "hbm",
             "achieved": ach,
             "peak": PEAK_HBM_GBPS,

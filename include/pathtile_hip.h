@@ -50,7 +50,9 @@ extern "C" {
 #define PT_KERNEL_DX 1
 #define PT_KERNEL_DK 2
 #define PT_KERNEL_DK_REDUCE 3
-#define PT_KERNEL_DK_CG 4      /* channel-group DK (L % 4 == 0, H % (4 * waves) == 0) */
+#define PT_KERNEL_DK_CG 4      /* channel-group DK (L % 4 == 0, H % (2 * waves) == 0) */
+#define PT_KERNEL_FWD_CG 5     /* channel-group matrix-core FWD (L % 4 == 0, H % 8 == 0) */
+#define PT_KERNEL_DX_CG 6      /* channel-group matrix-core DX  (L % 4 == 0, H % 8 == 0) */
 
 /* Version of this ABI (PT_ABI_VERSION). */
 int pt_abi_version(void);
@@ -64,6 +66,18 @@ const char* pt_status_string(int status);
  * AmpereWarpRuntime.launch_fwd (kernels/warp_tiled_ampere.py:723-747).
  * waves_per_block: 64-lane wavefronts per workgroup, one of 1,2,4,8,16 (the
  * MI355X counterpart of WARPS_PER_BLOCK, kernels/warp_tiled_ampere.py:643-644).
+ *
+ * Two kernels serve FWD and DX. The lane-per-row VALU kernel reproduces the
+ * reference's fmaf chain bit for bit and honours waves_per_block. Where a
+ * row needs at least 10.5 (LMAX / L)^2 useful FMAs per output on average
+ * (LMAX = 16 ceil(L / 16)) and the layout allows it (L % 4 == 0, H % 8 == 0,
+ * x and y 16-byte aligned), the
+ * channel-group matrix-core kernel runs instead: eight waves per workgroup
+ * whatever waves_per_block says, sums in the matrix cores' order (within
+ * FP32 rounding of the reference: about 3e-7 max-abs-scaled against FP64).
+ * The environment variable PATHTILE_ROWS_ALGO=valu selects the VALU kernel
+ * everywhere, =mfma the matrix-core kernel wherever the layout allows; it is
+ * read on every call.
  */
 int pt_dwconv1d_fwd_f32(const float* x, const float* w, float* y, int B, int H,
                         int L, int K, int waves_per_block, void* stream);
@@ -71,7 +85,8 @@ int pt_dwconv1d_fwd_f32(const float* x, const float* w, float* y, int B, int H,
 /*
  * Input gradient dx = conv^T(dy, w).
  * Replaces dwconv1d_warptile_bwd_input in AmpereWarpRuntime.launch_bwd_input
- * (kernels/warp_tiled_ampere.py:749-770).
+ * (kernels/warp_tiled_ampere.py:749-770). Kernel choice as for the forward
+ * pass (dy and dx 16-byte aligned for the matrix-core kernel).
  */
 int pt_dwconv1d_dx_f32(const float* dy, const float* w, float* dx, int B,
                        int H, int L, int K, int waves_per_block, void* stream);

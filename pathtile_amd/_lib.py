@@ -29,6 +29,9 @@ PT_KERNEL_FWD = 0
 PT_KERNEL_DX = 1
 PT_KERNEL_DK = 2
 PT_KERNEL_DK_REDUCE = 3
+PT_KERNEL_DK_CG = 4
+PT_KERNEL_FWD_CG = 5
+PT_KERNEL_DX_CG = 6
 
 # Every symbol include/pathtile_hip.h declares, with (restype, argtypes).
 _vp = ctypes.c_void_p

@@ -29,6 +29,7 @@ SOURCES = [
     "inst_dk_v.hip",
     "inst_dk_s.hip",
     "inst_dk_mfma.hip",
+    "inst_rows_mfma.hip",
 ]
 INCLUDE = ROOT / "include"
 BUILD_DIR = PKG / "_build"

@@ -333,6 +333,60 @@ static int rows_waves_per_cu(int L, int K) {
   return 10 * useful_fma_per_row(L, K) >= 7LL * L * L ? 8 : 4;
 }
 
+// --- FWD / DX algorithm ----------------------------------------------------
+// The channel-group matrix-core kernel costs the same whatever K is (it
+// multiplies by the whole LMAX x LMAX band matrix of the row bucket); the VALU
+// rows kernel's cost grows with the FMA chain. Measured on MI355X over
+// L = 16..48, K = 3..48 and B = 2048..65536, the matrix cores win once a row
+// needs at least 10.5 (LMAX / L)^2 useful FMAs per output on average (LMAX =
+// the row bucket 16, 32 or 48: rows that fill their bucket partly pay for
+// the matrix work they waste); below that the VALU kernel (bit-exact with the
+// reference's fmaf chain) is as fast or faster.
+// PATHTILE_ROWS_ALGO=valu forces the VALU kernel everywhere; =mfma forces the
+// matrix cores wherever the layout allows them.
+enum RowsAlgo { kRowsValu = 0, kRowsMfma = 1 };
+
+// The matrix-core kernel stages whole float4 rows of kRowsCgWaves channels.
+static bool rows_cg_ok(int H, int L, const void* in, const void* out) {
+  return L % 4 == 0 && H % kRowsCgWaves == 0 && aligned(in, 16) &&
+         aligned(out, 16) &&
+         rows_cg_lds_bytes(L) <= (size_t)max_lds_per_block();
+}
+
+static RowsAlgo rows_algo(int L, int K) {
+  const char* env = getenv("PATHTILE_ROWS_ALGO");
+  if (env && strcmp(env, "valu") == 0) return kRowsValu;
+  if (env && strcmp(env, "mfma") == 0) return kRowsMfma;
+  const long long lmax = 16LL * (mfma_index(L) + 1);
+  // useful / L >= 10.5 (lmax / L)^2, in integers
+  return 2 * useful_fma_per_row(L, K) * L >= 21 * lmax * lmax ? kRowsMfma
+                                                               : kRowsValu;
+}
+
+// Launch of the channel-group kernel: one workgroup per (channel group,
+// sample range), the ranges interleaved in 16-sample steps. As many ranges as
+// fill the CUs with min(2, resident) workgroups each (two measured best where
+// the LDS allows them, L <= 32; at L = 48 one fits).
+static int rows_cg_path(bool dx, const float* in, const float* w, float* out,
+                        int B, int H, int L, int K, void* stream) {
+  RowsCgFn fn = kRowsCgTable[dx ? 1 : 0][mfma_index(L)];
+  const size_t lds = rows_cg_lds_bytes(L);
+  const int threads = kRowsCgWaves * kWave;
+  int per_cu = blocks_per_cu((const void*)fn, threads, lds);
+  if (per_cu > 2) per_cu = 2;
+  const long long ngroups = (long long)H / kRowsCgWaves;
+  const long long tsteps = ((long long)B + kRowsCgStep - 1) / kRowsCgStep;
+  long long nr = ((long long)num_cus() * per_cu + ngroups / 2) / ngroups;
+  if (nr > tsteps) nr = tsteps;
+  if (nr < 1) nr = 1;
+  const long long nb = ngroups * nr;
+  if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
+  int nranges = (int)nr;
+  uint32_t nblocks = (uint32_t)nb;
+  void* args[] = {&in, &w, &out, &B, &H, &L, &K, &nranges, &nblocks};
+  return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream, args);
+}
+
 static long long gcd_ll(long long a, long long b) {
   while (b) {
     const long long t = a % b;
@@ -358,6 +412,8 @@ static int rows_path(bool dx, const float* in, const float* w, float* out,
   const bool vec = (L % 4 == 0) && aligned(in, 16) && aligned(out, 16);
   if (wpb * kWave > rows_max_threads(8 * (lbucket_index(L) + 1), vec))
     return PT_ERR_CONFIG;
+  if (rows_algo(L, K) == kRowsMfma && rows_cg_ok(H, L, in, out))
+    return rows_cg_path(dx, in, w, out, B, H, L, K, stream);
   const int li = lbucket_index(L), ki = kbucket_index(K);
   RowsFn fn = dx ? (vec ? kDxTableV : kDxTableS)[li][ki]
                  : (vec ? kFwdTableV : kFwdTableS)[li][ki];
@@ -428,6 +484,8 @@ static const void* kernel_for(int kernel_id, int L, int K) {
                                       : (const void*)kDkTableV[li][ki];
     case PT_KERNEL_DK_REDUCE: return (const void*)&dk_reduce_kernel;
     case PT_KERNEL_DK_CG: return (const void*)kDkCgTable[mfma_index(L)];
+    case PT_KERNEL_FWD_CG: return (const void*)kRowsCgTable[0][mfma_index(L)];
+    case PT_KERNEL_DX_CG: return (const void*)kRowsCgTable[1][mfma_index(L)];
     default: return nullptr;
   }
 }
@@ -580,6 +638,12 @@ int pt_dynamic_lds_bytes(int kernel_id, int L, int K, int block_config,
         return PT_ERR_CONFIG;
       *lds_bytes = (int)pt::cg_lds_bytes(16 * (pt::mfma_index(L) + 1),
                                          block_config / pt::kWave, L);
+      return PT_OK;
+    case PT_KERNEL_FWD_CG:
+    case PT_KERNEL_DX_CG:
+      // always kRowsCgWaves waves per workgroup, whatever the caller's config
+      if (!pt::valid_wpb(block_config)) return PT_ERR_CONFIG;
+      *lds_bytes = (int)pt::rows_cg_lds_bytes(L);
       return PT_OK;
     default:
       return PT_ERR_CONFIG;

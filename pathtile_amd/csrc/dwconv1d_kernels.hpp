@@ -782,6 +782,176 @@ __global__ __launch_bounds__(1024) void dwconv_dk_mfma_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// FWD / DX on channel-group tiles (matrix cores), for long FMA chains.
+//   FWD: y [b,h,t] = sum_s x [b,h,s] * w[h, s - t + p]
+//   DX : dx[b,h,t] = sum_s dy[b,h,s] * w[h, t - s + p]
+// i.e. per channel a product of the [samples x L] rows with the banded
+// Toeplitz matrix of the taps. Workgroup (g, r) owns channel group g (one
+// channel per wave, kRowsCgWaves waves) and the interleaved 16-sample steps
+// r, r + nranges, ...; per step it stages the group's contiguous segments
+// [b, g*HC .. g*HC+HC, :] through LDS (two input and two output stages, one
+// barrier per step) and each wave runs v_mfma_f32_16x16x4_f32 with M = 16
+// samples, N = 16 output columns, K = 4 input columns. K slot kk of MFMA step
+// u is input column u + (LMAX/4) * kk, so a lane reads its A operands as
+// LMAX/4 consecutive floats and its B operands (the taps) are loaded once.
+// The sums run in the matrix cores' order, not the reference's fmaf chain:
+// results agree with it to FP32 rounding (about 3e-7 max-abs-scaled).
+// ---------------------------------------------------------------------------
+constexpr int kRowsCgWaves = 8;    // one channel per wave
+constexpr int kRowsCgStep = 16;    // samples per step (MFMA M)
+
+__host__ __device__ constexpr size_t rows_cg_lds_bytes(int L) {
+  // two input + two output stages of 16 samples x (HC * L + 4) floats
+  return (size_t)4 * kRowsCgStep * (kRowsCgWaves * L + 4) * sizeof(float);
+}
+
+template <int LMAX, bool DX, int kDepth>  // kDepth: steps in flight in registers
+__global__ __launch_bounds__(kRowsCgWaves * kWave) void dwconv_rows_cg_kernel(
+    const float* __restrict__ in, const float* __restrict__ w,
+    float* __restrict__ out, int B, int H, int L, int K, int nranges,
+    uint32_t nblocks) {
+  constexpr int NT = LMAX / 16;  // 16-wide output tiles
+  constexpr int NU = LMAX / 4;   // MFMA steps over the input columns
+  constexpr int HC = kRowsCgWaves;
+  constexpr int kNpt = (HC * LMAX * kRowsCgStep / 4 + HC * kWave - 1) / (HC * kWave);
+  extern __shared__ float lds[];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int ngroups = H / HC;
+  const uint32_t blk = xcd_remap(blockIdx.x, nblocks);
+  const int g = (int)(blk % (uint32_t)ngroups);
+  const int r = (int)(blk / (uint32_t)ngroups);
+  const int tsteps = (B + kRowsCgStep - 1) / kRowsCgStep;
+  const int nsteps = r < tsteps ? (tsteps - 1 - r) / nranges + 1 : 0;
+
+  const int seg = HC * L, seg4 = seg >> 2;
+  const int sk = seg + 4;                 // LDS stride between samples
+  const int sz = kRowsCgStep * sk;        // one stage
+  const int per = kRowsCgStep * seg4;     // float4 per stage
+  const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
+  const uint32_t grp_bytes = (uint32_t)g * (uint32_t)seg * 4u;
+  float* inl = lds;                       // input stages 0, 1
+  float* outl = lds + 2 * sz;             // output stages 0, 1
+
+  // Loop-invariant part of each staged element (as in the DK kernel).
+  int ek[kNpt];
+  uint32_t eoff[kNpt], elds[kNpt];
+#pragma unroll
+  for (int i = 0; i < kNpt; ++i) {
+    const int e = i * (HC * kWave) + (int)threadIdx.x;
+    const int k = e < per ? e / seg4 : kRowsCgStep;
+    const int q = e - (e / seg4) * seg4;
+    ek[i] = k;
+    eoff[i] = (uint32_t)k * row_bytes + grp_bytes + 16u * (uint32_t)q;
+    elds[i] = (uint32_t)(k * sk + 4 * q);
+  }
+  float4 stg[kDepth][kNpt];
+  auto load_step = [&](int s, float4 (&st)[kNpt]) {
+    const int bs = (r + s * nranges) * kRowsCgStep;
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(in + (size_t)bs * (size_t)H * (size_t)L);
+    const int klim = min(kRowsCgStep, B - bs);
+#pragma unroll
+    for (int i = 0; i < kNpt; ++i)
+      st[i] = buf_load4<kCpolNT>(rs, ek[i] < klim ? eoff[i] : kOob, 0);
+  };
+  auto store_stage = [&](int buf, const float4 (&st)[kNpt]) {
+#pragma unroll
+    for (int i = 0; i < kNpt; ++i)
+      if (ek[i] < kRowsCgStep)
+        *reinterpret_cast<float4*>(inl + buf * sz + elds[i]) = st[i];
+  };
+  auto flush_out = [&](int s) {
+    const float* o = outl + (s & 1) * sz;
+    const int bs = (r + s * nranges) * kRowsCgStep;
+    const __amdgpu_buffer_rsrc_t ro =
+        make_rsrc(out + (size_t)bs * (size_t)H * (size_t)L);
+    const int klim = min(kRowsCgStep, B - bs);
+#pragma unroll
+    for (int i = 0; i < kNpt; ++i) {
+      const float4 v = *reinterpret_cast<const float4*>(o + (ek[i] < kRowsCgStep ? elds[i] : 0u));
+      buf_store4<kCpolNT>(v, ro, ek[i] < klim ? eoff[i] : kOob);
+    }
+  };
+
+  // B operands: step u, tile tt, lane l -> input column s = u + NU*(l/16),
+  // output column t = 16 tt + l % 16; zero outside the band and the row.
+  const int kk = lane >> 4, jj = lane & 15;
+  const int p = K >> 1;
+  const int h = g * HC + wave;
+  float bt[NU][NT];
+#pragma unroll
+  for (int u = 0; u < NU; ++u)
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      const int sc = u + NU * kk, tc = 16 * tt + jj;
+      const int j = DX ? (tc - sc + p) : (sc - tc + p);
+      const bool ok = j >= 0 && j < K && sc < L && tc < L;
+      bt[u][tt] = ok ? w[(size_t)h * K + j] : 0.0f;
+    }
+
+  const int rq = 4 * kk;
+  const int cb = wave * L;
+  auto mfma_step = [&](int s) {
+    const float* src = inl + (s & 1) * sz + jj * sk + cb + NU * kk;  // sample jj
+    float* o = outl + (s & 1) * sz;
+    float a[NU];
+#pragma unroll
+    for (int q = 0; q < NU / 4; ++q) {
+      const float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
+      a[4 * q + 0] = v.x;
+      a[4 * q + 1] = v.y;
+      a[4 * q + 2] = v.z;
+      a[4 * q + 3] = v.w;
+    }
+    if (L != LMAX) {  // columns >= L belong to the next channel: zero them
+#pragma unroll
+      for (int u = 0; u < NU; ++u) a[u] = u + NU * kk < L ? a[u] : 0.0f;
+    }
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+        d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], bt[u][tt], d, 0, 0, 0);
+      const int t = 16 * tt + jj;
+      if (t < L) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) o[(rq + rr) * sk + cb + t] = d[rr];
+      }
+    }
+  };
+
+  if (nsteps > 0) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d)
+      if (d < nsteps) load_step(d, stg[d]);
+    store_stage(0, stg[0]);
+    if (kDepth < nsteps) load_step(kDepth, stg[0]);
+    __syncthreads();
+    for (int s0 = 0; s0 < nsteps; s0 += kDepth) {
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) {
+        const int s = s0 + d;
+        if (s < nsteps) {
+          // Output stage s & 1 was last read by flush_out(s - 2), which
+          // every thread finished before the barrier of step s - 1.
+          mfma_step(s);
+          if (s + 1 < nsteps) {
+            store_stage((s + 1) & 1, stg[(d + 1) % kDepth]);
+            if (s + 1 + kDepth < nsteps)
+              load_step(s + 1 + kDepth, stg[(d + 1) % kDepth]);
+          }
+          __syncthreads();
+          flush_out(s);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // DK on channel-group tiles (matrix cores). For a sample b the rows of
 // channels [g*HC, g*HC + HC) are one contiguous segment of HC * L floats, so
 // a workgroup that owns channel group g streams whole segments instead of

@@ -32,5 +32,9 @@ using DkCgFn = void (*)(const float*, const float*, float*, int, int, int, int,
                         int, uint32_t, int);
 // channel-group matrix-core DK by row bucket 16, 32, 48
 extern const DkCgFn kDkCgTable[3];
+using RowsCgFn = void (*)(const float*, const float*, float*, int, int, int,
+                          int, int, uint32_t);
+// channel-group matrix-core FWD / DX: [0 = FWD, 1 = DX][row bucket 16, 32, 48]
+extern const RowsCgFn kRowsCgTable[2][3];
 
 }  // namespace pt

@@ -1,0 +1,11 @@
+// Instantiates the channel-group matrix-core FWD / DX kernels.
+#include "dwconv1d_kernels.hpp"
+#include "dwconv1d_tables.hpp"
+
+namespace pt {
+const RowsCgFn kRowsCgTable[2][3] = {
+    {&dwconv_rows_cg_kernel<16, false, 2>, &dwconv_rows_cg_kernel<32, false, 2>,
+     &dwconv_rows_cg_kernel<48, false, 2>},
+    {&dwconv_rows_cg_kernel<16, true, 2>, &dwconv_rows_cg_kernel<32, true, 2>,
+     &dwconv_rows_cg_kernel<48, true, 2>}};
+}  // namespace pt

@@ -13,10 +13,12 @@ Three reports, each written for one workload:
             of the bytes a copy loads, ``WRITE_SIZE`` reads them exactly.
 ``valu``    VALU instruction counts and the VALU-busy fraction from
             ``SQ_INSTS_VALU`` / ``SQ_ACTIVE_INST_VALU`` / ``SQ_BUSY_CYCLES`` /
-            ``GRBM_GUI_ACTIVE``.
+            ``GRBM_GUI_ACTIVE``, and the MFMA-busy fraction from
+            ``SQ_VALU_MFMA_BUSY_CYCLES`` when collected.
 
-Only the dispatches with the largest grid of each kernel are kept, so the
-small correctness-gate launches that run before the timed loops are left out.
+Only the dispatches with the largest grid of each kernel, and none below a
+quarter of its median duration or counter value, are kept, so the small
+correctness-gate launches that run before the timed loops are left out.
 
 Usage::
 
@@ -54,12 +56,23 @@ def short_name(name: str) -> str:
     return name
 
 
-def _largest_dispatches(rows, key_grid):
-    """Keep, per kernel name, only the rows whose grid equals its maximum."""
+def _largest_dispatches(rows, key_grid, key_value=None):
+    """Keep, per kernel name, only the rows whose grid equals its maximum and,
+    with `key_value`, whose value is at least a quarter of that kernel's
+    median: kernels that size their grid by the GPU rather than the batch
+    (persistent and sample-range grids) launch the same grid for the small
+    correctness-gate batch, which the value filter then drops."""
     best = {}
     for r in rows:
         best[r["name"]] = max(best.get(r["name"], 0), r[key_grid])
-    return [r for r in rows if r[key_grid] == best[r["name"]]]
+    rows = [r for r in rows if r[key_grid] == best[r["name"]]]
+    if key_value is None:
+        return rows
+    med = {}
+    for name in best:
+        v = [r[key_value] for r in rows if r["name"] == name]
+        med[name] = statistics.median(v) if v else 0
+    return [r for r in rows if r[key_value] >= 0.25 * med[r["name"]]]
 
 
 def kernel_rows(db: str):
@@ -85,7 +98,7 @@ def counter_rows(db: str, counter: str):
 
 def trace_report(db: str, command: str, match: str = "pt::") -> str:
     rows = [r for r in kernel_rows(db) if match in r["name"] or r["name"] == COPY_KERNEL]
-    rows = _largest_dispatches(rows, "grid")
+    rows = _largest_dispatches(rows, "grid", "duration")
     by = {}
     for r in rows:
         by.setdefault(r["name"], []).append(r)
@@ -99,14 +112,15 @@ def trace_report(db: str, command: str, match: str = "pt::") -> str:
                    f"{r0['vgpr_count']} | {r0['accum_vgpr_count']} | {r0['sgpr_count']} | "
                    f"{r0['lds_size']} | {r0['scratch_size']} |")
     head = ["Command:", "", "```", command, "```", "",
-            "Dispatches with each kernel's largest grid only (the timed loops; "
-            "the small correctness-gate launches are dropped).", ""]
+            "Dispatches with each kernel's largest grid only, and none shorter than a "
+            "quarter of that kernel's median (the timed loops; the small "
+            "correctness-gate launches are dropped).", ""]
     return "\n".join(head + out) + "\n"
 
 
 def _mean_counter(db: str, counter: str, match: str):
     rows = _largest_dispatches(
-        [r for r in counter_rows(db, counter) if match in r["name"]], "grid")
+        [r for r in counter_rows(db, counter) if match in r["name"]], "grid", "value")
     if not rows:
         raise SystemExit(f"no {counter} rows for kernels matching {match!r} in {db}")
     vals = [r["value"] for r in rows]
@@ -159,11 +173,11 @@ def traffic_report(fetch_db: str, write_db: str, kernel: str, tag: str,
 def valu_report(db: str, command: str, useful_fma: dict[str, int], clock_mhz: float,
                 match: str = "pt::") -> str:
     counters = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_ACTIVE_INST_VALU", "SQ_BUSY_CYCLES",
-                "GRBM_GUI_ACTIVE", "SQ_WAVE_CYCLES")
+                "GRBM_GUI_ACTIVE", "SQ_WAVE_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES")
     per = {}
     for c in counters:
         rows = _largest_dispatches(
-            [r for r in counter_rows(db, c) if match in r["name"]], "grid")
+            [r for r in counter_rows(db, c) if match in r["name"]], "grid", "value")
         for r in rows:
             per.setdefault(r["name"], {}).setdefault(c, []).append(r["value"])
     out = ["Command:", "", "```", command, "```", "",
@@ -171,8 +185,10 @@ def valu_report(db: str, command: str, useful_fma: dict[str, int], clock_mhz: fl
            f"GRBM_GUI_ACTIVE / {NUM_XCD} XCDs). FP32 fraction = useful FP32 FLOPs / "
            f"(duration x 78.6 TFLOP/s non-packed vector FP32 peak; packed FP32 is off in this "
            f"build), duration = GRBM_GUI_ACTIVE / {NUM_XCD} / {clock_mhz:.0f} MHz.", "",
-           "| kernel | dispatches | waves | VALU insts | VALU insts / wave | VALU-busy | useful FMA | FP32 fraction |",
-           "|---|---|---|---|---|---|---|---|"]
+           f"MFMA-busy = SQ_VALU_MFMA_BUSY_CYCLES / ({NUM_SIMDS} SIMDs x GRBM_GUI_ACTIVE / "
+           f"{NUM_XCD} XCDs) (n/a when that counter was not collected).", "",
+           "| kernel | dispatches | waves | VALU insts | VALU insts / wave | VALU-busy | MFMA-busy | useful FMA | FP32 fraction |",
+           "|---|---|---|---|---|---|---|---|---|"]
     for name, cs in per.items():
         m = {c: statistics.mean(v) for c, v in cs.items()}
         n = len(cs.get("SQ_INSTS_VALU", []))
@@ -185,8 +201,10 @@ def valu_report(db: str, command: str, useful_fma: dict[str, int], clock_mhz: fl
             fma_s = str(fma)
         else:
             frac, fma_s = "n/a", "n/a"
+        mfma = (f"{m['SQ_VALU_MFMA_BUSY_CYCLES'] / (NUM_SIMDS * gui):.3f}"
+                if "SQ_VALU_MFMA_BUSY_CYCLES" in m else "n/a")
         out.append(f"| `{short_name(name)}` | {n} | {m['SQ_WAVES']:.0f} | {m['SQ_INSTS_VALU']:.0f} | "
-                   f"{m['SQ_INSTS_VALU'] / max(m['SQ_WAVES'], 1):.0f} | {busy:.3f} | {fma_s} | {frac} |")
+                   f"{m['SQ_INSTS_VALU'] / max(m['SQ_WAVES'], 1):.0f} | {busy:.3f} | {mfma} | {fma_s} | {frac} |")
     return "\n".join(out) + "\n"
 
 

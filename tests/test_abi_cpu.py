@@ -166,6 +166,12 @@ def test_workspace_bytes(lib):
     assert lib.pt_dynamic_lds_bytes(_lib.PT_KERNEL_FWD, 48, 48, 8, ctypes.byref(lds)) == 0
     assert lds.value == 8 * 64 * (48 + 4) * 4  # 64-row tile, padded stride
     assert lib.pt_dynamic_lds_bytes(_lib.PT_KERNEL_FWD, 48, 48, 3, ctypes.byref(lds)) == _lib.PT_ERR_CONFIG
+    # matrix-core FWD/DX: 8 channels x 16 samples, two input + two output stages
+    for kid in (_lib.PT_KERNEL_FWD_CG, _lib.PT_KERNEL_DX_CG):
+        for L in (4, 16, 32, 48):
+            assert lib.pt_dynamic_lds_bytes(kid, L, 48, 1, ctypes.byref(lds)) == 0
+            assert lds.value == 4 * 16 * (8 * L + 4) * 4
+        assert lib.pt_dynamic_lds_bytes(kid, 48, 48, 3, ctypes.byref(lds)) == _lib.PT_ERR_CONFIG
 
 
 def test_library_is_not_linked_to_the_oracle():

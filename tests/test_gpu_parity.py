@@ -1,9 +1,13 @@
 """GPU parity of the HIP kernels against the CPU oracle (marked ``gpu``).
 
 Bars (stated per test):
-* FWD / dX: bit-exact against the oracle's restatement of the reference's
-  FP32 fmaf chain (oracle.fwd_f32_refchain / dx_f32_refchain) and within
-  1e-5 max-abs-scaled of FP64;
+* FWD / dX, VALU kernel (PATHTILE_ROWS_ALGO=valu, and every shape the
+  matrix-core kernel does not serve): bit-exact against the oracle's
+  restatement of the reference's FP32 fmaf chain (oracle.fwd_f32_refchain /
+  dx_f32_refchain) and within 1e-5 max-abs-scaled of FP64;
+* FWD / dX, channel-group matrix-core kernel (the default for long FMA
+  chains with L % 4 == 0, H % 8 == 0 and 16-byte aligned rows): within 1e-5
+  max-abs-scaled of FP64 (the matrix cores sum in their own order);
 * dK (atomic and deterministic): within 1e-4 max-abs-scaled of FP64
   (atomic order is not fixed); the deterministic variant is also bitwise
   reproducible run to run; taps that meet no element are exactly 0.
@@ -90,19 +94,66 @@ SHAPES = [
 ]
 
 
+def _mfma_serves(H, L, K, algo):
+    """Whether the channel-group matrix-core FWD/DX kernel serves a 16-byte
+    aligned call: the layout must allow it (L % 4 == 0, H % 8 == 0) and,
+    unless forced, the row must need >= 10.5 (LMAX / L)^2 useful FMAs per
+    output (LMAX = 16 ceil(L / 16))."""
+    if algo == "valu" or L % 4 or H % 8:
+        return False
+    lmax = 16 * ((L + 15) // 16)
+    return algo == "mfma" or 2 * oracle.useful_fma_per_row(L, K) * L >= 21 * lmax * lmax
+
+
+@pytest.mark.parametrize("algo", ["auto", "valu", "mfma"])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "B{}H{}L{}K{}".format(*s))
-def test_fwd_dx_bit_exact_and_fp64(rt, shape):
+def test_fwd_dx_bit_exact_and_fp64(rt, shape, algo, monkeypatch):
+    """Both FWD/DX kernels; the library reads PATHTILE_ROWS_ALGO on every
+    call. The VALU kernel is bit-exact with the reference's fmaf chain."""
+    if algo != "auto":
+        monkeypatch.setenv("PATHTILE_ROWS_ALGO", algo)
     B, H, L, K = shape
     x, w, dy = _inputs(B, H, L, K, seed=1000 + B + H + L + K)
     xd, wd, dyd = _dev(x, w, dy)
     y = _fwd(rt, xd, wd).cpu().numpy()
     dx = _dx(rt, dyd, wd).cpu().numpy()
-    y_ref = oracle.fwd_f32_refchain(x, w)
-    dx_ref = oracle.dx_f32_refchain(dy, w)
-    assert np.array_equal(y, y_ref), oracle.normalized_max_abs(y, y_ref)
-    assert np.array_equal(dx, dx_ref), oracle.normalized_max_abs(dx, dx_ref)
+    assert np.isfinite(y).all() and np.isfinite(dx).all()
+    if not _mfma_serves(H, L, K, algo):
+        y_ref = oracle.fwd_f32_refchain(x, w)
+        dx_ref = oracle.dx_f32_refchain(dy, w)
+        assert np.array_equal(y, y_ref), oracle.normalized_max_abs(y, y_ref)
+        assert np.array_equal(dx, dx_ref), oracle.normalized_max_abs(dx, dx_ref)
     assert oracle.normalized_max_abs(y, oracle.fwd_f64(x, w)) < FWD_TOL
     assert oracle.normalized_max_abs(dx, oracle.dx_f64(dy, w)) < FWD_TOL
+
+
+@pytest.mark.parametrize("shape", [
+    (1, 8, 48, 48),       # one sample: a single ragged 16-sample step
+    (15, 16, 44, 48),     # L < row bucket (48): columns of the next channel masked
+    (33, 8, 36, 32),      # L in the 48 bucket, ragged last step
+    (100, 24, 20, 17),    # L in the 32 bucket, odd K
+    (77, 8, 12, 40),      # K > L
+    (50, 16, 4, 9),       # L = 4: three quarters of each MFMA input masked
+    (513, 8, 8, 3),       # short filter, forced onto the matrix cores
+    (4096, 8, 48, 48),    # one channel group, many interleaved ranges
+    (40, 4800, 16, 16),   # 600 channel groups, more than two per CU: one range each
+])
+def test_fwd_dx_matrix_core_kernel(rt, shape, monkeypatch):
+    """The channel-group matrix-core kernel (forced) against FP64 on the
+    layouts it serves, with infinities in the next channel's rows: its
+    masked columns must not leak into this channel's outputs."""
+    monkeypatch.setenv("PATHTILE_ROWS_ALGO", "mfma")
+    B, H, L, K = shape
+    x, w, dy = _inputs(B, H, L, K, seed=4000 + B + H + L + K)
+    x[:, 1::2, :] = float("inf")
+    dy[:, 1::2, :] = float("inf")
+    xd, wd, dyd = _dev(x, w, dy)
+    y = _fwd(rt, xd, wd).cpu().numpy()[:, 0::2]
+    dx = _dx(rt, dyd, wd).cpu().numpy()[:, 0::2]
+    xe, we, dye = x[:, 0::2].contiguous(), w[0::2].contiguous(), dy[:, 0::2].contiguous()
+    assert np.isfinite(y).all() and np.isfinite(dx).all()
+    assert oracle.normalized_max_abs(y, oracle.fwd_f64(xe, we)) < FWD_TOL
+    assert oracle.normalized_max_abs(dx, oracle.dx_f64(dye, we)) < FWD_TOL
 
 
 @pytest.mark.parametrize("algo", ["auto", "valu", "mfma"])
@@ -203,18 +254,31 @@ def test_golden_edge_fixtures(rt):
         assert oracle.normalized_max_abs(_dk_det(rt, dyd, xd, K).cpu().numpy(), d[f"{n}/dk64"]) < DK_TOL
 
 
+@pytest.mark.parametrize("algo", ["valu", "auto"])
 @pytest.mark.parametrize("wpb,L", [(1, 48), (2, 48), (4, 48), (8, 48), (16, 32), (8, 37)])
-def test_every_waves_per_block_gives_the_same_bits(wpb, L):
+def test_every_waves_per_block_gives_the_same_bits(wpb, L, algo, monkeypatch):
+    """VALU: every waves_per_block reproduces the reference's fmaf chain.
+    Default: the matrix-core kernel (L % 4 == 0, H % 8 == 0, K = 48) ignores
+    waves_per_block, so every value gives the bits of waves_per_block = 1."""
     from pathtile_amd import runtime
 
+    if algo != "auto":
+        monkeypatch.setenv("PATHTILE_ROWS_ALGO", algo)
     B, H, K = 200, 24, 48
     x, w, dy = _inputs(B, H, L, K, seed=7)
     xd, wd, dyd = _dev(x, w, dy)
     r = runtime.HipWarpRuntime(waves_per_block=wpb)
     y = _fwd(r, xd, wd).cpu().numpy()
     dx = _dx(r, dyd, wd).cpu().numpy()
-    assert np.array_equal(y, oracle.fwd_f32_refchain(x, w))
-    assert np.array_equal(dx, oracle.dx_f32_refchain(dy, w))
+    if _mfma_serves(H, L, K, algo):
+        r1 = runtime.HipWarpRuntime(waves_per_block=1)
+        assert np.array_equal(y, _fwd(r1, xd, wd).cpu().numpy())
+        assert np.array_equal(dx, _dx(r1, dyd, wd).cpu().numpy())
+        assert oracle.normalized_max_abs(y, oracle.fwd_f64(x, w)) < FWD_TOL
+        assert oracle.normalized_max_abs(dx, oracle.dx_f64(dy, w)) < FWD_TOL
+    else:
+        assert np.array_equal(y, oracle.fwd_f32_refchain(x, w))
+        assert np.array_equal(dx, oracle.dx_f32_refchain(dy, w))
 
 
 @pytest.mark.parametrize("threads", [64, 128, 192, 256, 320, 384, 512, 768])
@@ -259,9 +323,10 @@ def test_atomic_dk_accumulates_into_gk(rt):
     assert oracle.normalized_max_abs(gk.cpu().numpy(), ref) < DK_TOL
 
 
-def test_primary_shape_sampled_rows_and_full_dk(rt):
-    """B=16384 H=128 L=48 K=48: FWD/dX bit-exact on 256 sampled batch rows
-    (all channels), dK against FP64 over the full batch."""
+def test_primary_shape_sampled_rows_and_full_dk(rt, monkeypatch):
+    """B=16384 H=128 L=48 K=48: FWD/dX (matrix-core default) within 1e-5 of
+    FP64 on 256 sampled batch rows (all channels), the VALU kernel bit-exact
+    on the same rows, dK against FP64 over the full batch."""
     B, H, L, K = 16384, 128, 48, 48
     x, w, dy = _inputs(B, H, L, K, seed=42)
     xd, wd, dyd = _dev(x, w, dy)
@@ -269,8 +334,14 @@ def test_primary_shape_sampled_rows_and_full_dk(rt):
     dx = _dx(rt, dyd, wd)
     idx = torch.from_numpy(np.random.default_rng(0).choice(B, 256, replace=False))
     ys, dxs = y[idx.cuda()].cpu().numpy(), dx[idx.cuda()].cpu().numpy()
-    assert np.array_equal(ys, oracle.fwd_f32_refchain(x[idx], w))
-    assert np.array_equal(dxs, oracle.dx_f32_refchain(dy[idx], w))
+    assert oracle.normalized_max_abs(ys, oracle.fwd_f64(x[idx], w)) < FWD_TOL
+    assert oracle.normalized_max_abs(dxs, oracle.dx_f64(dy[idx], w)) < FWD_TOL
+    monkeypatch.setenv("PATHTILE_ROWS_ALGO", "valu")
+    yv, dxv = _fwd(rt, xd, wd), _dx(rt, dyd, wd)
+    monkeypatch.delenv("PATHTILE_ROWS_ALGO")
+    assert np.array_equal(yv[idx.cuda()].cpu().numpy(), oracle.fwd_f32_refchain(x[idx], w))
+    assert np.array_equal(dxv[idx.cuda()].cpu().numpy(), oracle.dx_f32_refchain(dy[idx], w))
+    del yv, dxv
     ref = oracle.dk_f64(dy, x, K)
     assert oracle.normalized_max_abs(_dk_atomic(rt, dyd, xd, K).cpu().numpy(), ref) < DK_TOL
     g1 = _dk_det(rt, dyd, xd, K).cpu().numpy()
@@ -283,8 +354,9 @@ def test_primary_shape_sampled_rows_and_full_dk(rt):
 
 
 def test_misaligned_and_noncontiguous_inputs(rt):
-    """A storage offset that breaks 16-byte alignment takes the dword path;
-    results stay bit-exact."""
+    """A storage offset that breaks 16-byte alignment takes the VALU kernel's
+    dword path (the matrix-core kernel needs aligned rows); results stay
+    bit-exact."""
     B, H, L, K = 64, 6, 48, 48
     x, w, dy = _inputs(B, H, L, K, seed=10)
     flat = torch.zeros(x.numel() + 1, device="cuda:0")
@@ -300,7 +372,7 @@ def test_autograd_depthconvampere_and_shared(rt):
     from pathtile_amd.kernels import warp_tiled as wt
 
     runtime.install_runtime(rt)
-    B, H, L, K = 96, 10, 48, 48
+    B, H, L, K = 96, 10, 48, 48  # H % 8 != 0: the bit-exact VALU kernel
     x, w, dy = _inputs(B, H, L, K, seed=11)
     _, gx_ref, gk_ref = oracle.torch_grads(x.double(), w.double(), dy.double())
     for fn in (runtime.depthwise_conv_ampere, wt.depthwise_conv_shared):
