@@ -600,9 +600,12 @@ class DepthConvAmpere(torch.autograd.Function):
             raise ValueError("Unexpected gradient shape")
         gx = torch.empty_like(x_c)
         runtime.launch_bwd_input(gy_c, k_c, gx)
-        # As in the reference, the zero-fill sits outside the dK kernel event.
-        gk = torch.zeros_like(k_c)
-        runtime.launch_bwd_weight(gy_c, x_c, gk, K)
+        # The reference zero-fills gk and adds into it with atomics
+        # (:890-893). The two-pass dK overwrites gk instead: no memset, a
+        # fixed summation order (reproducible gradients), and on MI355X the
+        # same time as zero-fill + atomics.
+        gk = torch.empty_like(k_c)
+        runtime.launch_bwd_weight_deterministic(gy_c, x_c, gk, K)
         return gx, gk
 
 

@@ -380,9 +380,12 @@ def test_autograd_depthconvampere_and_shared(rt):
         wd = w.cuda().requires_grad_(True)
         y = fn(xd, wd)
         assert np.array_equal(y.detach().cpu().numpy(), oracle.fwd_f32_refchain(x, w))
-        gx, gk = torch.autograd.grad(y, (xd, wd), dy.cuda())
+        gx, gk = torch.autograd.grad(y, (xd, wd), dy.cuda(), retain_graph=True)
         assert oracle.normalized_max_abs(gx.cpu().numpy(), gx_ref.numpy()) < FWD_TOL
         assert oracle.normalized_max_abs(gk.cpu().numpy(), gk_ref.numpy()) < DK_TOL
+        # both backward passes take the two-pass dK: reproducible bits
+        _, gk2 = torch.autograd.grad(y, (xd, wd), dy.cuda())
+        assert torch.equal(gk, gk2)
     wt.reset_timing_collectors()
     xd = x.cuda().requires_grad_(True)
     y = wt.DepthwiseConvShared.apply(xd, w.cuda().requires_grad_(True))
