@@ -56,6 +56,9 @@ def parse_args(argv=None):
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-runs", type=int, default=5)
+    p.add_argument("--s4convd-steps", type=int, default=0, metavar="N",
+                   help="also time N S4ConvD training steps (the reference's Model() at "
+                        "B16384 L48, SGD lr 1e-3 momentum 0.9) on each backend")
     p.add_argument("--copy-probe", type=int, default=0, metavar="N",
                    help="after timing, run N plain device copies of x into y "
                         "(known bytes: 2 * B*H*L*4 per copy) to calibrate "
@@ -237,6 +240,56 @@ def cpu_baseline(x, w, dy, runs: int) -> dict:
     }
 
 
+def s4convd_training_steps(steps: int, warmup: int, dev) -> dict:
+    """Time S4ConvD training steps (forward, backward, SGD) of the reference's
+    default Model() on a synthetic batch shaped like its training batches
+    (B=16384 windows of L=48 steps, 4 features; kernels/warp_tiled_ampere.py:
+    1193-1215, 1345-1354, 1442-1446), on the "warp" backend (HIP path, skip
+    term fused) and the "pytorch" backend (PyTorch's GPU convolution)."""
+    import torch
+
+    from pathtile_amd import runtime, s4convd
+    from pathtile_amd.kernels import warp_tiled_ampere as wta
+
+    runtime.get_or_create_runtime()  # the frozen policy's launch config
+    out = {}
+    prev = wta.TRAIN_CONV_BACKEND
+    try:
+        for name in ("warp", "pytorch"):
+            wta.TRAIN_CONV_BACKEND = name
+            torch.manual_seed(0)
+            model = s4convd.Model().to(dev)
+            opt = torch.optim.SGD(model.parameters(), lr=1e-3, momentum=0.9)
+            g = torch.Generator().manual_seed(1)
+            x = torch.randn(16384, 48, 4, generator=g).to(dev)
+            target = torch.rand(16384, 1, generator=g).to(dev)
+
+            def step():
+                opt.zero_grad(set_to_none=True)
+                loss = s4convd.rmsle(model(x), target)
+                loss.backward()
+                opt.step()
+                return loss
+
+            for _ in range(warmup):
+                step()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                loss = step()
+            torch.cuda.synchronize()
+            out[name] = {"ms_per_step": round((time.perf_counter() - t0) * 1e3 / steps, 4),
+                         "final_loss": float(loss.detach())}
+            del model, opt, x, target
+            torch.cuda.empty_cache()
+    finally:
+        wta.TRAIN_CONV_BACKEND = prev
+    return {"workload": "S4ConvD Model() (4 blocks, H128, state 64), B16384 L48 synthetic, "
+                        "SGD lr 1e-3 momentum 0.9, dropout 0.01",
+            "steps": steps, "warmup": warmup, **out,
+            "speedup_vs_pytorch": round(out["pytorch"]["ms_per_step"] / out["warp"]["ms_per_step"], 3)}
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
@@ -413,6 +466,9 @@ def main(argv=None) -> int:
             "algorithmic_bytes": nbytes,
         },
     }
+    if args.s4convd_steps:
+        log("S4ConvD training steps ...")
+        line["s4convd"] = s4convd_training_steps(args.s4convd_steps, max(3, args.warmup // 4), dev)
     if args.copy_probe:
         for _ in range(args.copy_probe):
             y.copy_(x)
