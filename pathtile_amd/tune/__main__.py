@@ -7,6 +7,10 @@
     python -m pathtile_amd.tune report [--out DIR]
         CPU: recompute the policy from the tuning CSVs, verify it matches the
         frozen one and predates every held-out trial, rewrite the report.
+    python -m pathtile_amd.tune baselines [--out DIR] [--budget 6]
+        CPU: score the selector baselines (majority winner, global static,
+        a coverage-selected shape budget) beside the frozen policy on the
+        same CSVs; writes DIR/baselines.json.
 """
 
 from __future__ import annotations
@@ -18,7 +22,7 @@ import subprocess
 import sys
 from pathlib import Path
 
-from . import select
+from . import baselines, select
 from .shapes import SEED, draw_shapes
 
 PKG = Path(__file__).resolve().parent
@@ -98,7 +102,9 @@ def build_report(out: Path, policy: dict) -> dict:
 
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(prog="python -m pathtile_amd.tune")
-    p.add_argument("command", choices=["all", "report"])
+    p.add_argument("command", choices=["all", "report", "baselines"])
+    p.add_argument("--budget", type=int, default=6,
+                   help="tuning shapes of the coverage-budget baseline")
     p.add_argument("--out", type=Path, default=DEFAULT_OUT)
     p.add_argument("--trials", type=int, default=3)
     p.add_argument("--warmup", type=int, default=50)
@@ -146,6 +152,15 @@ def main(argv=None) -> int:
         return 0
 
     policy = json.loads((out / "frozen_policy.json").read_text())
+    if args.command == "baselines":
+        train = select.mean_of_trials(sum((_read_csv(q) for q in sorted(out.glob("train_trial*.csv"))), []))
+        hold = select.mean_of_trials(sum((_read_csv(q) for q in sorted(out.glob("holdout_trial*.csv"))), []))
+        result = baselines.evaluate(train, hold, policy["selected"], args.budget)
+        (out / "baselines.json").write_text(json.dumps(result, indent=2))
+        for name, r in result["policies"].items():
+            print(f"{name:32s} {r['policy']}  held-out mean regret {r['holdout']['mean_regret_pct']:.3f}%  "
+                  f"tuning {r['train']['mean_regret_pct']:.3f}%")
+        return 0
     report = build_report(out, policy)
     print(json.dumps(report, indent=2))
     return 0

@@ -91,3 +91,106 @@ def test_normalize_roundoff_and_geomean():
     assert select.geometric_mean([1.0, 4.0]) == pytest.approx(2.0)
     with pytest.raises(ValueError):
         select.geometric_mean([1.0, 0.0])
+
+
+# ---------------------------------------------------------------------------
+# Selector baselines and the coverage budget (pathtile_amd/tune/baselines.py)
+# ---------------------------------------------------------------------------
+from pathtile_amd.tune import baselines  # noqa: E402
+
+
+def _full(table):
+    """rows from {phase: {cid: {value: ms}}}"""
+    rows = []
+    for ph, per in table.items():
+        for cid, cand in per.items():
+            for v, ms in cand.items():
+                rows.append(_row(cid, ph, v, ms))
+    return rows
+
+
+def test_majority_winner_counts_shape_wins():
+    """fwd: 2 wins s1, s2 and 4 wins s3 -> 2, although 4 has the smaller sum;
+    dx: one win each for 1 and 8 -> the smaller value; dk: a tie within a
+    shape goes to the smaller value (128 wins s1 and s2)."""
+    t = {
+        "fwd": {"s1": {2: 1.0, 4: 1.1}, "s2": {2: 1.0, 4: 1.2}, "s3": {2: 9.0, 4: 1.0}},
+        "bwd_input": {"s1": {1: 1.0, 8: 2.0}, "s2": {1: 2.0, 8: 1.0}, "s3": {1: 1.0, 8: 1.0}},
+        "bwd_weight": {"s1": {128: 1.0, 256: 1.0}, "s2": {128: 1.0, 256: 1.0}, "s3": {128: 2.0, 256: 1.0}},
+    }
+    rows = _full(t)
+    pol = baselines.majority_winner_policy(rows)
+    assert pol == {"fwd_waves_per_block": 2, "dx_waves_per_block": 1, "dk_threads_per_block": 128}
+    assert select.select_policy(rows)["fwd_waves_per_block"] == 4
+
+
+def test_global_static_raw_sum_is_the_per_path_choice_and_geomean_can_differ():
+    """Summed latency separates over the paths, so its best combination is
+    select_policy's; the geometric-mean regret weighs shapes equally and can
+    prefer another value (here fwd 2: 10% worse on the big shape s1, a third
+    faster on the small shape s2)."""
+    t = {
+        "fwd": {"s1": {2: 11.0, 4: 10.0}, "s2": {2: 0.1, 4: 0.15}},
+        "bwd_input": {"s1": {1: 0.01, 2: 0.02}, "s2": {1: 0.01, 2: 0.02}},
+        "bwd_weight": {"s1": {64: 0.01}, "s2": {64: 0.01}},
+    }
+    rows = _full(t)
+    table = baselines.global_static_table(rows)
+    assert len(table) == 2 * 2 * 1
+    raw = baselines.best_by(table, "raw_total_ms")
+    assert raw == select.select_policy(rows)
+    assert raw["fwd_waves_per_block"] == 4
+    assert baselines.best_by(table, "geomean_regret_pct")["fwd_waves_per_block"] == 2
+    r = next(x for x in table if x["fwd_waves_per_block"] == 4 and x["dx_waves_per_block"] == 1)
+    # s1 is at its oracle (10.02); s2 takes 0.17 against 0.12
+    assert r["max_regret_pct"] == pytest.approx((0.17 / 0.12 - 1) * 100)
+    assert r["mean_regret_pct"] == pytest.approx((0.17 / 0.12 - 1) * 50)
+    assert r["geomean_regret_pct"] == pytest.approx(((0.17 / 0.12) ** 0.5 - 1) * 100)
+
+
+def test_coverage_queries_on_a_line():
+    """Shapes that differ only in B = 2, 4, 8, 16, 32: the most work first
+    (B = 32), then the farthest (B = 2), then the middle (B = 8), then of the
+    two equidistant gaps the lower index (B = 4)."""
+    dims = [(b, 64, 16, 8) for b in (2, 4, 8, 16, 32)]
+    assert baselines.coverage_queries(dims, 4) == [4, 0, 2, 1]
+    assert baselines.coverage_queries(dims, 5) == [4, 0, 2, 1, 3]
+    with pytest.raises(ValueError):
+        baselines.coverage_queries(dims, 1)
+
+
+def test_coverage_queries_standardise_each_dimension():
+    """Without standardisation B (range 2^4) would dominate L (range 2^1.6);
+    standardised, each spans the same distance, so after the largest-work
+    shape the farthest pick is the corner opposite in both."""
+    dims = [(32768, 64, 48, 8), (2048, 64, 48, 8), (32768, 64, 16, 8), (2048, 64, 16, 8)]
+    assert baselines.useful_products(*dims[0]) == max(baselines.useful_products(*d) for d in dims)
+    assert baselines.coverage_queries(dims, 2) == [0, 3]
+
+
+def test_useful_products_matches_the_path_count():
+    from pathtile_amd import runtime
+
+    for B, H, L, K in ((3, 5, 48, 48), (2, 7, 16, 3), (1, 1, 1, 1), (4, 2, 9, 40)):
+        assert 2 * baselines.useful_products(B, H, L, K) == runtime.useful_flops(B, H, L, K)
+
+
+def test_baselines_on_the_committed_tuner_results():
+    """On the committed MI355X trial CSVs: the summed-latency baseline is the
+    frozen policy, every budget's coverage policy is a valid candidate
+    combination, and the full budget gives the frozen policy."""
+    import json
+    from pathlib import Path
+
+    from pathtile_amd.tune.__main__ import _read_csv
+
+    res = Path(__file__).resolve().parents[1] / "pathtile_amd" / "tune" / "results"
+    train = select.mean_of_trials(sum((_read_csv(p) for p in sorted(res.glob("train_trial*.csv"))), []))
+    hold = select.mean_of_trials(sum((_read_csv(p) for p in sorted(res.glob("holdout_trial*.csv"))), []))
+    frozen = json.loads((res / "frozen_policy.json").read_text())["selected"]
+    out = baselines.evaluate(train, hold, frozen, 6)
+    assert out["policies"]["global_static_raw_sum"]["policy"] == frozen
+    assert len(out["coverage_shapes"]) == 6
+    assert out["coverage_budget_sweep"][-1]["policy"] == frozen
+    for name, r in out["policies"].items():
+        assert r["holdout"]["shapes"] == 10 and r["train"]["shapes"] == 20, name
