@@ -56,6 +56,9 @@ def parse_args(argv=None):
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-runs", type=int, default=5)
+    p.add_argument("--gpu-library-steps", type=int, default=0, metavar="N",
+                   help="also time N calls per path of PyTorch's GPU convolution (MIOpen) "
+                        "on the same tensors")
     p.add_argument("--s4convd-steps", type=int, default=0, metavar="N",
                    help="also time N S4ConvD training steps (the reference's Model() at "
                         "B16384 L48, SGD lr 1e-3 momentum 0.9) on each backend")
@@ -238,6 +241,41 @@ def cpu_baseline(x, w, dy, runs: int) -> dict:
         "paths_ms": {k: round(v, 3) for k, v in out.items()},
         "wall_s": round(time.perf_counter() - t_all, 1),
     }
+
+
+def gpu_library_baseline(x, w, dy, steps: int) -> dict:
+    """PyTorch's own GPU path for the same op on the same tensors (grouped
+    F.conv1d, MIOpen on ROCm), with the reference's PyTorch boundaries: FWD =
+    the convolution, dX = autograd.grad(y, x), dK = autograd.grad(y, w), the
+    graph built outside the events; one event pair per call, mean over
+    `steps` calls after one warm-up call."""
+    import torch
+
+    from pathtile_amd.runtime import reference_depthwise_conv as conv
+
+    out = {}
+    for phase in ("fwd", "dx", "dk"):
+        ts = []
+        for r in range(steps + 1):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            if phase == "fwd":
+                e0.record()
+                conv(x, w)
+                e1.record()
+            else:
+                xr = x.detach().requires_grad_(phase == "dx")
+                wr = w.detach().requires_grad_(phase == "dk")
+                y = conv(xr, wr)
+                e0.record()
+                torch.autograd.grad(y, xr if phase == "dx" else wr, dy)
+                e1.record()
+            e1.synchronize()
+            if r > 0:
+                ts.append(e0.elapsed_time(e1))
+        out[phase] = round(mean(ts), 4)
+    return {"what": "torch.nn.functional.conv1d(groups=H) on the GPU (MIOpen), same tensors",
+            "paths_ms": out, "total_ms": round(sum(out.values()), 4), "calls_per_path": steps}
 
 
 def s4convd_training_steps(steps: int, warmup: int, dev) -> dict:
@@ -466,6 +504,9 @@ def main(argv=None) -> int:
             "algorithmic_bytes": nbytes,
         },
     }
+    if args.gpu_library_steps:
+        log("GPU library baseline ...")
+        line["gpu_library_baseline"] = gpu_library_baseline(x, w, dy, args.gpu_library_steps)
     if args.s4convd_steps:
         log("S4ConvD training steps ...")
         line["s4convd"] = s4convd_training_steps(args.s4convd_steps, max(3, args.warmup // 4), dev)
