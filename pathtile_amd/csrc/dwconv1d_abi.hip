@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
+#include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -153,6 +154,7 @@ constexpr double kDkMallBytes = 256.0 * 1024 * 1024;  // MI355X Infinity Cache
 struct DkGeom {
   DkAlgo algo;
   bool cg;            // channel-group kernel
+  bool nt;            // channel-group kernel with non-temporal loads
   int wpb;
   int rows_per_wave;  // VALU: 64-sample chunks per wave; MFMA: samples;
                       // channel-group: samples per workgroup
@@ -167,16 +169,48 @@ static bool dk_cg_ok(int H, int L, int threads) {
   return L % 4 == 0 && wpb <= 8 && H % (kCgChannelsPerWave * wpb) == 0;
 }
 
-// Interleaved sample ranges of the channel-group DK: the power of two
-// (8 .. 256) nearest to 2.5 MiB / (bytes of one 4-sample step of one
-// tensor), so a workgroup's successive steps lie about 2.5 MiB apart; that
-// stride measured best on MI355X from H = 64 to 256 and L = 16 to 48. It
-// depends on the shape only (not on the block size or the device).
+// Tensors of at least the 256 MiB MALL stream differently from smaller ones
+// in the channel-group DK, so two settings depend on that size:
+//  * loads: non-temporal from 256 MiB up (4-10% faster there, e.g. 128 vs
+//    132 us at P), plain below (non-temporal loads cost small L = 16 / 32
+//    shapes 11-20% in the tuner's per-launch protocol);
+//  * interleaved sample ranges (a workgroup's successive steps lie nr steps
+//    apart): from 256 MiB up, of the counts 2^k and 3 * 2^(k-1) in [8, 256]
+//    the one nearest (by ratio; ties to the smaller) to 3 MiB / (bytes of one
+//    4-sample step of one tensor). 3 MiB measured best at every row length;
+//    at L = 16 and 32 it is 15-17% faster than the power of two nearest
+//    2.5 MiB, and at L = 40, whose 3 MiB counts (38, 77) are neither form,
+//    the neighbouring power of two is 4-8% faster than 38 or 77. Below
+//    256 MiB: the power of two (8 .. 256) nearest to 2.5 MiB per step, which
+//    keeps more steps per workgroup.
+// Measured on MI355X over the 30 tuner shapes, P and S with the tuner's own
+// protocol, both libraries on one box. Both depend on the shape only (not on
+// the block size or the device).
+static bool cg_large(int B, int H, int L) {
+  return 4.0 * (double)B * (double)H * (double)L >= kDkMallBytes;
+}
+
 static long long cg_ranges(int B, int H, int L) {
   const double step_bytes = 16.0 * (double)H * (double)L;
-  const double want = 2.5 * 1024 * 1024 / step_bytes;
   long long nr = 8;
-  while (nr < 256 && (double)(nr * 2) <= want * 1.41421356) nr *= 2;
+  if (cg_large(B, H, L)) {
+    const double want = 3.0 * 1024 * 1024 / step_bytes;
+    double best = 1e300;
+    for (long long p = 8; p <= 256; p *= 2) {
+      const long long cands[2] = {p, p + p / 2};
+      for (long long c : cands) {
+        if (c > 256) continue;
+        const double d = fabs(log((double)c / want));
+        if (d < best - 1e-12) {
+          best = d;
+          nr = c;
+        }
+      }
+    }
+  } else {
+    const double want = 2.5 * 1024 * 1024 / step_bytes;
+    while (nr < 256 && (double)(nr * 2) <= want * 1.41421356) nr *= 2;
+  }
   const long long tsteps = ((long long)B + kCgStep - 1) / kCgStep;
   if (nr > tsteps) nr = tsteps;
   return nr < 1 ? 1 : nr;
@@ -189,6 +223,7 @@ static DkGeom dk_geometry(int B, int H, int L, int K, int threads, bool vec16) {
   const long long wpb = g.wpb;
   const long long rows = (long long)B * H;
   g.cg = g.algo == kDkMfma && vec16 && dk_cg_ok(H, L, threads);
+  g.nt = g.cg && cg_large(B, H, L);
   if (g.cg) {
     const long long ngroups = (long long)H / (kCgChannelsPerWave * wpb);
     const long long nr = cg_ranges(B, H, L);
@@ -445,7 +480,7 @@ static int dk_path(bool det, const float* gy, const float* x, float* dst,
   uint32_t nblocks = (uint32_t)g.nblocks;
   int rpw = g.rows_per_wave, nbt = g.nbt, d = det ? 1 : 0;
   if (g.cg) {
-    DkCgFn fn = kDkCgTable[mfma_index(L)];
+    DkCgFn fn = (g.nt ? kDkCgTableNT : kDkCgTable)[mfma_index(L)];
     const size_t lds = cg_lds_bytes(16 * (mfma_index(L) + 1), g.wpb, L);
     void* args[] = {&gy, &x, &dst, &B, &H, &L, &K, &nbt, &nblocks, &d};
     return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream,

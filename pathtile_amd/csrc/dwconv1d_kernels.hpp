@@ -997,7 +997,7 @@ __host__ __device__ constexpr size_t cg_lds_bytes(int lmax, int wpb, int L) {
   return (stages > dtile ? stages : dtile) * sizeof(float);
 }
 
-template <int LMAX>
+template <int LMAX, int LOAD_CPOL = kCpolNone>
 __global__ __launch_bounds__(512) void dwconv_dk_cg_kernel(
     const float* __restrict__ gy, const float* __restrict__ x,
     float* __restrict__ dst, int B, int H, int L, int K, int nranges,
@@ -1056,8 +1056,8 @@ __global__ __launch_bounds__(512) void dwconv_dk_cg_kernel(
 #pragma unroll
     for (int i = 0; i < kNpt; ++i) {
       const uint32_t o = ek[i] < klim ? eoff[i] : kOob;
-      st[0][i] = buf_load4(rg, o, 0);
-      st[1][i] = buf_load4(rx, o, 0);
+      st[0][i] = buf_load4<LOAD_CPOL>(rg, o, 0);
+      st[1][i] = buf_load4<LOAD_CPOL>(rx, o, 0);
     }
   };
   auto store_stage = [&](int buf, const float4 (&st)[2][kNpt]) {

@@ -30,8 +30,10 @@ extern const DkFn kDkTableS[kNumLB][kNumKB];
 extern const DkMfmaFn kDkMfmaTable[3];
 using DkCgFn = void (*)(const float*, const float*, float*, int, int, int, int,
                         int, uint32_t, int);
-// channel-group matrix-core DK by row bucket 16, 32, 48
+// channel-group matrix-core DK by row bucket 16, 32, 48; NT: non-temporal
+// loads (tensors of at least 256 MiB)
 extern const DkCgFn kDkCgTable[3];
+extern const DkCgFn kDkCgTableNT[3];
 using RowsCgFn = void (*)(const float*, const float*, float*, int, int, int,
                           int, int, uint32_t);
 // channel-group matrix-core FWD / DX: [0 = FWD, 1 = DX][row bucket 16, 32, 48]

@@ -9,4 +9,7 @@ const DkMfmaFn kDkMfmaTable[3] = {&dwconv_dk_mfma_kernel<16>,
 const DkCgFn kDkCgTable[3] = {&dwconv_dk_cg_kernel<16>,
                               &dwconv_dk_cg_kernel<32>,
                               &dwconv_dk_cg_kernel<48>};
+const DkCgFn kDkCgTableNT[3] = {&dwconv_dk_cg_kernel<16, kCpolNT>,
+                                &dwconv_dk_cg_kernel<32, kCpolNT>,
+                                &dwconv_dk_cg_kernel<48, kCpolNT>};
 }  // namespace pt

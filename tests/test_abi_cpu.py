@@ -8,6 +8,7 @@ return before any HIP call (invalid shapes/configs/NULL pointers).
 from __future__ import annotations
 
 import ctypes
+import math
 import re
 import subprocess
 from pathlib import Path
@@ -131,8 +132,10 @@ def test_workspace_bytes(lib):
     #    samples; rows per wave are whole load groups (48 / 24 / 16 samples
     #    for rows of <= 16 / <= 32 / <= 48 floats), up to 128 samples;
     #  * channel-group interleaved sample ranges (L % 4 == 0, <= 8 waves, H a
-    #    multiple of 2 * waves): the power of two in [8, 256] nearest to
-    #    2.5 MiB / (16 H L bytes), at most one per 4-sample step.
+    #    multiple of 2 * waves), at most one per 4-sample step: for tensors of
+    #    at least 256 MiB, of 2^k and 3 * 2^(k-1) in [8, 256] the one nearest
+    #    by ratio to 3 MiB / (16 H L bytes) (ties to the smaller); below that,
+    #    the power of two in [8, 256] nearest to 2.5 MiB / (16 H L bytes).
     # Both depend on the shape and block size only, never on the device.
     def per_channel(B, H, L, wpb):
         grp = 48 // (-(-L // 16))
@@ -144,10 +147,15 @@ def test_workspace_bytes(lib):
     def channel_group(B, H, L, wpb):
         if L % 4 or wpb > 8 or H % (2 * wpb):
             return 0
-        want = 2.5 * 2**20 / (16 * H * L)
-        n = 8
-        while n < 256 and n * 2 <= want * 2**0.5:
-            n *= 2
+        if 4 * B * H * L >= 256 * 2**20:
+            want = 3 * 2**20 / (16 * H * L)
+            cands = sorted({c for k in range(3, 9) for c in (2**k, 3 * 2**(k - 1)) if 8 <= c <= 256})
+            n = min(cands, key=lambda c: (abs(math.log(c / want)), c))
+        else:
+            want = 2.5 * 2**20 / (16 * H * L)
+            n = 8
+            while n < 256 and n * 2 <= want * 2**0.5:
+                n *= 2
         return max(1, min(n, -(-B // 4)))
 
     for (B, H, L, K) in [(16384, 128, 48, 48), (16384, 64, 16, 3), (1000, 96, 37, 48),
@@ -156,8 +164,11 @@ def test_workspace_bytes(lib):
             wpb = threads // 64
             n = nbt(B, H, L, K, threads)
             assert n == max(per_channel(B, H, L, wpb), channel_group(B, H, L, wpb)), (B, H, L, threads)
-    assert nbt(16384, 128, 48, 48, 256) == 32   # 32 ranges (98 KiB steps), 32 tiles
-    assert nbt(16384, 64, 16, 3, 256) == 128    # 16 KiB steps: 128 interleaved ranges
+    assert nbt(16384, 128, 48, 48, 256) == 32   # 32 ranges (96 KiB steps), 32 tiles
+    assert nbt(16384, 64, 16, 3, 256) == 128    # 64 MiB tensors, 16 KiB steps: 128
+    assert nbt(16384, 128, 40, 48, 256) == 32   # 80 KiB steps: 38.4 -> 32 (not 48)
+    assert nbt(16384, 128, 32, 8, 256) == 48    # 256 MiB tensors, 64 KiB steps: 48 = 3 * 2^4
+    assert nbt(8192, 128, 32, 8, 256) == 32     # 128 MiB tensors: 2.5 MiB rule, 32
     assert nbt(16384, 128, 48, 48, 192) == 43   # per-channel: 3 waves x 128 samples
     assert nbt(1000, 96, 37, 48, 64) == 63      # L % 4 != 0: per-channel only
     st = lib.pt_dwconv1d_dk_det_workspace_bytes(0, 4, 8, 3, 256, ctypes.byref(out))
