@@ -424,3 +424,40 @@ def test_empty_batch(rt):
     gk.fill_(7.0)
     rt.launch_bwd_weight_deterministic(x, x, gk, 5)
     assert torch.all(gk == 0)
+
+
+def test_maximum_size_sampled_rows_and_adjoint_identities(rt):
+    """B*H*L just under 2^31 (the library's limit; 8.6 GB per tensor):
+    FWD/dX within 1e-5 of FP64 on sampled batch rows, dK within 1e-4 of FP64
+    on two full channels, and over the whole tensors the size-independent
+    identities <FWD(x; w), dY> = <x, DX(dY; w)> = <dK(dY, x), w> in FP64."""
+    B, H, L, K = 43690, 1024, 48, 48
+    assert B * H * L < 2**31
+    print(f"[case] max size B={B} H={H} L={L} K={K}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(77)
+    x = torch.randn(B, H, L, device="cuda", generator=g)
+    dy = torch.randn(B, H, L, device="cuda", generator=g)
+    w = torch.randn(H, K, device="cuda", generator=g) / K ** 0.5
+    y = torch.empty_like(x)
+    rt.launch_fwd(x, w, y)
+    idx = torch.tensor([0, 1, 12345, 30001, B - 2, B - 1], device="cuda")
+    xs, ys, dys = x[idx].cpu(), y[idx].cpu().numpy(), dy[idx].cpu()
+    wc = w.cpu()
+    assert oracle.normalized_max_abs(ys, oracle.fwd_f64(xs, wc)) < FWD_TOL
+    left = float((y.double() * dy.double()).sum())
+    ynorm = float(y.double().norm())
+    del y
+    dx = torch.empty_like(x)
+    rt.launch_bwd_input(dy, w, dx)
+    assert oracle.normalized_max_abs(dx[idx].cpu().numpy(), oracle.dx_f64(dys, wc)) < FWD_TOL
+    right = float((x.double() * dx.double()).sum())
+    del dx
+    gk = torch.empty(H, K, device="cuda")
+    rt.launch_bwd_weight_deterministic(dy, x, gk, K)
+    dk_w = float((gk.double() * w.double()).sum())
+    scale = ynorm * float(dy.double().norm())
+    assert abs(left - right) <= 1e-6 * scale
+    assert abs(left - dk_w) <= 1e-6 * scale
+    for h in (3, H - 1):
+        ref = oracle.dk_f64(dy[:, h:h + 1].cpu(), x[:, h:h + 1].cpu(), K)
+        assert oracle.normalized_max_abs(gk[h:h + 1].cpu().numpy(), ref) < DK_TOL
