@@ -522,14 +522,21 @@ class HipWarpRuntime:
 
     def resource_report(self, L: int = DEFAULT_L, K: int = DEFAULT_K):
         """Registers, LDS, scratch and estimated occupancy of the kernels that
-        serve (L, K) (the reference's resource_report, :814-833)."""
+        serve (L, K) (the reference's resource_report, :814-833). FWD and dX
+        list both kernels: the VALU rows kernel at this runtime's waves per
+        block, and the channel-group matrix-core kernel (8 waves), which
+        serves long FMA chains on 16-byte aligned rows with L % 4 == 0 and
+        H % 8 == 0."""
         import pandas as pd
 
         rows = []
+        cg_block = 8 * WAVE_SIZE
         for name, kid, block, cfg in (
             ("fwd", _lib.PT_KERNEL_FWD, self.fwd_block, self.waves_per_block),
+            ("fwd_matrix_cores", _lib.PT_KERNEL_FWD_CG, cg_block, self.waves_per_block),
             ("bwd_input", _lib.PT_KERNEL_DX, self.dx_waves_per_block * WAVE_SIZE,
              self.dx_waves_per_block),
+            ("bwd_input_matrix_cores", _lib.PT_KERNEL_DX_CG, cg_block, self.dx_waves_per_block),
             ("bwd_weight", _lib.PT_KERNEL_DK, self.bwdk_block, self.bwdk_block),
         ):
             a = self.kernel_attributes(kid, L, K)

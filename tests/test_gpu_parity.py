@@ -461,3 +461,15 @@ def test_maximum_size_sampled_rows_and_adjoint_identities(rt):
     for h in (3, H - 1):
         ref = oracle.dk_f64(dy[:, h:h + 1].cpu(), x[:, h:h + 1].cpu(), K)
         assert oracle.normalized_max_abs(gk[h:h + 1].cpu().numpy(), ref) < DK_TOL
+
+
+def test_resource_report_lists_every_kernel(rt):
+    """The reference's resource_report (kernels/warp_tiled_ampere.py:814-833):
+    one row per kernel that can serve (L, K), with registers, LDS and an
+    occupancy estimate; no kernel spills to scratch."""
+    df = rt.resource_report(48, 48)
+    assert list(df["kernel"]) == ["fwd", "fwd_matrix_cores", "bwd_input",
+                                  "bwd_input_matrix_cores", "bwd_weight"]
+    assert (df["scratch_bytes"] == 0).all()
+    for L, K in ((16, 3), (37, 48), (8, 8)):
+        assert len(rt.resource_report(L, K)) == 5
