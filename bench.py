@@ -401,6 +401,28 @@ def main(argv=None) -> int:
 
     loop_ms = {ph: time_loop(fn) for ph, fn in loops.items()}
 
+    # BF16 I/O (no reference counterpart): the same workload with x, dY and
+    # the FWD/dX outputs in bfloat16, taps and dK in FP32, same loops. Its
+    # algorithmic bytes are (2 B H L * 2 + H K * 4) per path.
+    xb, dyb = x.to(torch.bfloat16), dy.to(torch.bfloat16)
+    yb, dxb = torch.empty_like(xb), torch.empty_like(dyb)
+    bf16_loops = {
+        "fwd": lambda: rt.launch_fwd_bf16(xb, w, yb),
+        "bwd_input": lambda: rt.launch_bwd_input_bf16(dyb, w, dxb),
+        "bwd_weight": lambda: rt.launch_bwd_weight_bf16(dyb, xb, gk, K),
+        "bwd_weight_det": lambda: rt.launch_bwd_weight_deterministic_bf16(dyb, xb, gk, K),
+    }
+    bf16_ms = {ph: time_loop(fn) for ph, fn in bf16_loops.items()}
+    # gate: BF16 FWD against the FP32 path on the same (BF16-valued) input
+    rows_b = min(512, B)
+    y32 = torch.empty(rows_b, H, L, device=dev)
+    rt.launch_fwd(xb[:rows_b].float().contiguous(), w, y32)
+    torch.cuda.synchronize()
+    bf16_gate = float((yb[:rows_b].float() - y32).abs().max() / y32.abs().max().clamp_min(1e-30))
+    if not bf16_gate < 2.0 ** -8:
+        raise SystemExit(f"BF16 gate failed: {bf16_gate}")
+    del xb, dyb, yb, dxb, y32
+
     # The VALU rows kernel (the reference's lane-per-row structure, bit-exact
     # with its fmaf chain) timed beside the default FWD/DX kernel, same loops.
     prev = os.environ.get("PATHTILE_ROWS_ALGO")
@@ -486,6 +508,19 @@ def main(argv=None) -> int:
         "algorithmic_bytes_per_path": nbytes,
         "paths": paths,
         "correctness_gate": {k: float(f"{v:.3e}") for k, v in gate.items()},
+        "bf16_io": {
+            "paths": {
+                ph: {"ms": round(ms, 5),
+                     "gbps": round((2 * B * H * L * 2 + H * K * 4) / (ms / 1e3) / 1e9, 1),
+                     "pct_peak": round(100 * (2 * B * H * L * 2 + H * K * 4) / (ms / 1e3) / 1e9
+                                       / PEAK_HBM_GBPS, 2)}
+                for ph, ms in bf16_ms.items()
+            },
+            "fwd_dx_dk_ms": round(bf16_ms["fwd"] + bf16_ms["bwd_input"] + bf16_ms["bwd_weight"], 5),
+            "gate_vs_fp32_path": float(f"{bf16_gate:.3e}"),
+            "note": "x, dY, y, dX bfloat16; taps and dK FP32; FP32 accumulation; "
+                    "algorithmic bytes (2 B H L * 2 + H K * 4) per path",
+        },
         "rows_valu": {
             ph: {"ms": round(ms, 5), "pct_peak": round(100 * runtime.algorithmic_bandwidth_gbps(nbytes, ms)
                                                      / PEAK_HBM_GBPS, 2),

@@ -127,6 +127,33 @@ int pt_dwconv1d_dk_det_f32(const float* dy, const float* x, float* dk,
                            void* stream);
 
 /*
+ * BF16 I/O variants (no counterpart in the reference, which is FP32 only).
+ * x, y, dy, dx are bfloat16 tensors passed as their 16-bit patterns; w and dk
+ * stay FP32. The kernels widen BF16 to FP32 exactly, accumulate in FP32 on
+ * the matrix cores (the channel-group kernels above), and round FP32 outputs
+ * to BF16 to nearest-even. They halve the bytes the paths move. Only the
+ * channel-group layout is served: L % 4 == 0 and, for FWD/DX, H % 8 == 0,
+ * for DK, threads_per_block <= 512 with H % (2 * threads_per_block / 64) == 0
+ * (PT_ERR_CONFIG otherwise); BF16 tensors must be 16-byte aligned
+ * (PT_ERR_ALIGN). DK semantics match the FP32 entry points (atomic with
+ * optional zero_first; deterministic two-pass with its own workspace size).
+ */
+int pt_dwconv1d_fwd_bf16(const void* x, const float* w, void* y, int B, int H,
+                         int L, int K, void* stream);
+int pt_dwconv1d_dx_bf16(const void* dy, const float* w, void* dx, int B, int H,
+                        int L, int K, void* stream);
+int pt_dwconv1d_dk_atomic_bf16(const void* dy, const void* x, float* dk, int B,
+                               int H, int L, int K, int threads_per_block,
+                               int zero_first, void* stream);
+int pt_dwconv1d_dk_det_bf16_workspace_bytes(int B, int H, int L, int K,
+                                            int threads_per_block,
+                                            size_t* bytes);
+int pt_dwconv1d_dk_det_bf16(const void* dy, const void* x, float* dk,
+                            void* workspace, size_t workspace_bytes, int B,
+                            int H, int L, int K, int threads_per_block,
+                            void* stream);
+
+/*
  * Compiled resources of the kernel that serves (L, K) for `kernel_id`
  * (PT_KERNEL_*), as hipFuncGetAttributes reports them on the current device:
  * registers per lane, static LDS bytes, scratch (private) bytes per lane and

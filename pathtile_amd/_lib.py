@@ -48,6 +48,13 @@ SIGNATURES = {
     "pt_dwconv1d_dk_det_f32": (
         _i, [_vp, _vp, _vp, _vp, ctypes.c_size_t, _i, _i, _i, _i, _i, _vp]
     ),
+    "pt_dwconv1d_fwd_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "pt_dwconv1d_dx_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "pt_dwconv1d_dk_atomic_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "pt_dwconv1d_dk_det_bf16_workspace_bytes": (_i, [_i, _i, _i, _i, _i, _szp]),
+    "pt_dwconv1d_dk_det_bf16": (
+        _i, [_vp, _vp, _vp, _vp, ctypes.c_size_t, _i, _i, _i, _i, _i, _vp]
+    ),
     "pt_kernel_attributes": (_i, [_i, _i, _i, _ip, _ip, _ip, _ip]),
     "pt_dynamic_lds_bytes": (_i, [_i, _i, _i, _i, _ip]),
 }

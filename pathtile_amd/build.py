@@ -30,6 +30,7 @@ SOURCES = [
     "inst_dk_s.hip",
     "inst_dk_mfma.hip",
     "inst_rows_mfma.hip",
+    "inst_bf16.hip",
 ]
 INCLUDE = ROOT / "include"
 BUILD_DIR = PKG / "_build"

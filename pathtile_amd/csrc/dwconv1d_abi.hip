@@ -186,14 +186,14 @@ static bool dk_cg_ok(int H, int L, int threads) {
 // Measured on MI355X over the 30 tuner shapes, P and S with the tuner's own
 // protocol, both libraries on one box. Both depend on the shape only (not on
 // the block size or the device).
-static bool cg_large(int B, int H, int L) {
-  return 4.0 * (double)B * (double)H * (double)L >= kDkMallBytes;
+static bool cg_large(int B, int H, int L, int esize = 4) {
+  return (double)esize * (double)B * (double)H * (double)L >= kDkMallBytes;
 }
 
-static long long cg_ranges(int B, int H, int L) {
-  const double step_bytes = 16.0 * (double)H * (double)L;
+static long long cg_ranges(int B, int H, int L, int esize = 4) {
+  const double step_bytes = (double)kCgStep * esize * (double)H * (double)L;
   long long nr = 8;
-  if (cg_large(B, H, L)) {
+  if (cg_large(B, H, L, esize)) {
     const double want = 3.0 * 1024 * 1024 / step_bytes;
     double best = 1e300;
     for (long long p = 8; p <= 256; p *= 2) {
@@ -216,17 +216,20 @@ static long long cg_ranges(int B, int H, int L) {
   return nr < 1 ? 1 : nr;
 }
 
-static DkGeom dk_geometry(int B, int H, int L, int K, int threads, bool vec16) {
+// esize: bytes per element of dy and x (4 FP32, 2 BF16; BF16 runs the
+// channel-group kernel only).
+static DkGeom dk_geometry(int B, int H, int L, int K, int threads, bool vec16,
+                          int esize = 4) {
   DkGeom g;
   g.algo = dk_algo(L, K);
   g.wpb = threads / kWave;
   const long long wpb = g.wpb;
   const long long rows = (long long)B * H;
   g.cg = g.algo == kDkMfma && vec16 && dk_cg_ok(H, L, threads);
-  g.nt = g.cg && cg_large(B, H, L);
+  g.nt = g.cg && cg_large(B, H, L, esize);
   if (g.cg) {
     const long long ngroups = (long long)H / (kCgChannelsPerWave * wpb);
-    const long long nr = cg_ranges(B, H, L);
+    const long long nr = cg_ranges(B, H, L, esize);
     g.rows_per_wave = 0;
     g.nbt = (int)nr;
     g.nblocks = ngroups * nr;
@@ -402,14 +405,17 @@ static RowsAlgo rows_algo(int L, int K) {
 // sample range), the ranges interleaved in 16-sample steps. As many ranges as
 // fill the CUs with min(2, resident) workgroups each (two measured best where
 // the LDS allows them, L <= 32; at L = 48 one fits).
-static int rows_cg_path(bool dx, const float* in, const float* w, float* out,
-                        int B, int H, int L, int K, void* stream) {
-  RowsCgFn fn = kRowsCgTable[dx ? 1 : 0][mfma_index(L)];
-  const size_t lds = rows_cg_lds_bytes(L);
-  const int threads = kRowsCgWaves * kWave;
+// hc: channels (= waves) per workgroup; max_per_cu: workgroups per CU the
+// range count is sized for (at most what fits).
+template <typename T, typename Fn>
+static int rows_cg_launch(Fn fn, const T* in, const float* w, T* out, int B,
+                          int H, int L, int K, void* stream,
+                          int hc = kRowsCgWaves, int max_per_cu = 2) {
+  const size_t lds = rows_cg_lds_bytes(L, hc);
+  const int threads = hc * kWave;
   int per_cu = blocks_per_cu((const void*)fn, threads, lds);
-  if (per_cu > 2) per_cu = 2;
-  const long long ngroups = (long long)H / kRowsCgWaves;
+  if (per_cu > max_per_cu) per_cu = max_per_cu;
+  const long long ngroups = (long long)H / hc;
   const long long tsteps = ((long long)B + kRowsCgStep - 1) / kRowsCgStep;
   long long nr = ((long long)num_cus() * per_cu + ngroups / 2) / ngroups;
   if (nr > tsteps) nr = tsteps;
@@ -420,6 +426,12 @@ static int rows_cg_path(bool dx, const float* in, const float* w, float* out,
   uint32_t nblocks = (uint32_t)nb;
   void* args[] = {&in, &w, &out, &B, &H, &L, &K, &nranges, &nblocks};
   return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream, args);
+}
+
+static int rows_cg_path(bool dx, const float* in, const float* w, float* out,
+                        int B, int H, int L, int K, void* stream) {
+  return rows_cg_launch(kRowsCgTable[dx ? 1 : 0][mfma_index(L)], in, w, out, B,
+                        H, L, K, stream);
 }
 
 static long long gcd_ll(long long a, long long b) {
@@ -506,6 +518,52 @@ static int dk_path(bool det, const float* gy, const float* x, float* dst,
   void* args[] = {&gy, &x, &dst, &B, &H, &L, &K, &rpw, &nbt, &nblocks, &d};
   return launch((const void*)fn, nblocks, (uint32_t)threads,
                 (size_t)g.wpb * kStageBytes, stream, args);
+}
+
+// --- BF16 I/O --------------------------------------------------------------
+// x, y, dy, dx are bfloat16 (uint16_t bit patterns), w and dk FP32; the
+// kernels widen BF16 to FP32 exactly, accumulate in FP32 on the matrix cores
+// and narrow FP32 outputs to BF16 with round-to-nearest-even. Only the
+// channel-group kernels take BF16: rows of whole 16-byte LDS vectors
+// (L % 4 == 0), 16-byte aligned tensors, H % 8 == 0 (FWD / DX) or
+// H % (2 * waves) == 0 with at most 8 waves (DK).
+static int bf16_rows_path(bool dx, const void* in, const float* w, void* out,
+                          int B, int H, int L, int K, void* stream) {
+  int st = check_shape(B, H, L, K);
+  if (st != PT_OK) return st;
+  if (L % 4 != 0 || H % kRowsCgWaves != 0) return PT_ERR_CONFIG;
+  if (rows_cg_lds_bytes(L) > (size_t)max_lds_per_block()) return PT_ERR_CONFIG;
+  if (B == 0 || H == 0) return PT_OK;
+  if (!in || !w || !out) return PT_ERR_NULL;
+  if (!aligned(in, 16) || !aligned(out, 16) || !aligned(w, 4)) return PT_ERR_ALIGN;
+  // Row bucket 48: 4-channel groups, three per CU (the matrix cores' step
+  // pipeline, not HBM, bounds the BF16 kernel; 12 waves per CU hide it best,
+  // 10% faster than 8-channel groups at B16384 H128 L48 on MI355X).
+  const bool l48 = mfma_index(L) == 2;
+  return rows_cg_launch(kRowsCgTableBf16[dx ? 1 : 0][mfma_index(L)],
+                        (const uint16_t*)in, w, (uint16_t*)out, B, H, L, K,
+                        stream, l48 ? kRowsCgBf16WavesL48 : kRowsCgWaves,
+                        l48 ? 3 : 2);
+}
+
+static int bf16_dk_check(int B, int H, int L, int K, int threads) {
+  int st = check_shape(B, H, L, K);
+  if (st != PT_OK) return st;
+  if (!valid_dk_threads(threads) || !dk_cg_ok(H, L, threads)) return PT_ERR_CONFIG;
+  return PT_OK;
+}
+
+static int bf16_dk_launch(bool det, const void* gy, const void* x, float* dst,
+                          int B, int H, int L, int K, int threads,
+                          const DkGeom& g, void* stream) {
+  DkCgBf16Fn fn = (g.nt ? kDkCgTableBf16NT : kDkCgTableBf16)[mfma_index(L)];
+  const size_t lds = cg_lds_bytes(16 * (mfma_index(L) + 1), g.wpb, L);
+  const uint16_t* gyp = (const uint16_t*)gy;
+  const uint16_t* xp = (const uint16_t*)x;
+  uint32_t nblocks = (uint32_t)g.nblocks;
+  int nbt = g.nbt, d = det ? 1 : 0;
+  void* args[] = {&gyp, &xp, &dst, &B, &H, &L, &K, &nbt, &nblocks, &d};
+  return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream, args);
 }
 
 static const void* kernel_for(int kernel_id, int L, int K) {
@@ -683,6 +741,84 @@ int pt_dynamic_lds_bytes(int kernel_id, int L, int K, int block_config,
     default:
       return PT_ERR_CONFIG;
   }
+}
+
+int pt_dwconv1d_fwd_bf16(const void* x, const float* w, void* y, int B, int H,
+                         int L, int K, void* stream) {
+  return pt::bf16_rows_path(false, x, w, y, B, H, L, K, stream);
+}
+
+int pt_dwconv1d_dx_bf16(const void* dy, const float* w, void* dx, int B, int H,
+                        int L, int K, void* stream) {
+  return pt::bf16_rows_path(true, dy, w, dx, B, H, L, K, stream);
+}
+
+int pt_dwconv1d_dk_atomic_bf16(const void* dy, const void* x, float* dk, int B,
+                               int H, int L, int K, int threads_per_block,
+                               int zero_first, void* stream) {
+  int st = pt::bf16_dk_check(B, H, L, K, threads_per_block);
+  if (st != PT_OK) return st;
+  if (H == 0) return PT_OK;
+  if (!dk) return PT_ERR_NULL;
+  if (!pt::aligned(dk, 4)) return PT_ERR_ALIGN;
+  if (zero_first) {
+    st = pt::zero_fill(dk, H * K, stream);
+    if (st != PT_OK) return st;
+  }
+  if (B == 0) return PT_OK;
+  if (!dy || !x) return PT_ERR_NULL;
+  if (!pt::aligned(dy, 16) || !pt::aligned(x, 16)) return PT_ERR_ALIGN;
+  const pt::DkGeom g = pt::dk_geometry(B, H, L, K, threads_per_block, true, 2);
+  if (!g.cg) return PT_ERR_CONFIG;  // e.g. PATHTILE_DK_ALGO=valu
+  if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
+  return pt::bf16_dk_launch(false, dy, x, dk, B, H, L, K, threads_per_block, g,
+                            stream);
+}
+
+int pt_dwconv1d_dk_det_bf16_workspace_bytes(int B, int H, int L, int K,
+                                            int threads_per_block,
+                                            size_t* bytes) {
+  if (!bytes) return PT_ERR_NULL;
+  int st = pt::bf16_dk_check(B, H, L, K, threads_per_block);
+  if (st != PT_OK) return st;
+  if (B == 0 || H == 0) {
+    *bytes = 0;
+    return PT_OK;
+  }
+  const long long nr = pt::cg_ranges(B, H, L, 2);
+  *bytes = (size_t)H * (size_t)K * (size_t)nr * sizeof(float);
+  return PT_OK;
+}
+
+int pt_dwconv1d_dk_det_bf16(const void* dy, const void* x, float* dk,
+                            void* workspace, size_t workspace_bytes, int B,
+                            int H, int L, int K, int threads_per_block,
+                            void* stream) {
+  int st = pt::bf16_dk_check(B, H, L, K, threads_per_block);
+  if (st != PT_OK) return st;
+  if (H == 0) return PT_OK;
+  if (!dk) return PT_ERR_NULL;
+  if (!pt::aligned(dk, 4)) return PT_ERR_ALIGN;
+  if (B == 0) return pt::zero_fill(dk, H * K, stream);
+  if (!dy || !x) return PT_ERR_NULL;
+  if (!pt::aligned(dy, 16) || !pt::aligned(x, 16)) return PT_ERR_ALIGN;
+  const pt::DkGeom g = pt::dk_geometry(B, H, L, K, threads_per_block, true, 2);
+  if (!g.cg) return PT_ERR_CONFIG;
+  if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
+  const size_t need = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
+  if (!workspace || workspace_bytes < need) return PT_ERR_WORKSPACE;
+  if (!pt::aligned(workspace, 4)) return PT_ERR_ALIGN;
+  float* partials = (float*)workspace;
+  st = pt::bf16_dk_launch(true, dy, x, partials, B, H, L, K, threads_per_block,
+                          g, stream);
+  if (st != PT_OK) return st;
+  int ncoef = H * K;
+  int nbt = g.nbt;
+  const float* cp = partials;
+  void* args[] = {&cp, &dk, &ncoef, &nbt};
+  const uint32_t grid = (uint32_t)((ncoef + 3) / 4);
+  return pt::launch((const void*)&pt::dk_reduce_kernel, grid, 256, 0, stream,
+                    args);
 }
 
 }  // extern "C"

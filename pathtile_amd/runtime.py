@@ -504,6 +504,113 @@ class HipWarpRuntime:
 
         (collector or KERNEL_EVENTS).launch("bwd_weight_det", launch, {"B": B, "H": H, "L": L, "K": K})
 
+    # ------------------------------------------------------------- BF16 I/O
+    # No counterpart in the reference (FP32 only): bfloat16 activations and
+    # gradients, FP32 taps and dK, FP32 accumulation on the matrix cores.
+    @staticmethod
+    def _check_bf16(t: torch.Tensor, k: torch.Tensor, name: str) -> tuple[int, int, int, int]:
+        if not t.is_cuda or not k.is_cuda:
+            raise ValueError(f"{name} and k must be CUDA tensors")
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bfloat16")
+        if k.dtype != torch.float32:
+            raise ValueError("k must be float32")
+        if t.ndim != 3 or k.ndim != 2:
+            raise ValueError(f"Expected {name}[B,H,L] and k[H,K]")
+        B, H, L = map(int, t.shape)
+        Hk, K = map(int, k.shape)
+        if H != Hk:
+            raise ValueError(f"Channel mismatch: {name} H={H}, k H={Hk}")
+        if L > MAX_L or K > MAX_K:
+            raise ValueError(f"Specialized kernels require L<={MAX_L}, K<={MAX_K}")
+        return B, H, L, K
+
+    def launch_fwd_bf16(self, x: torch.Tensor, k: torch.Tensor, y: torch.Tensor,
+                        collector: KernelEventCollector | None = None) -> None:
+        self._check_open()
+        B, H, L, K = self._check_bf16(x, k, "x")
+        if y.dtype != torch.bfloat16 or y.shape != x.shape:
+            raise ValueError("y must be a bfloat16 tensor shaped like x")
+        self._require_contiguous(x, k, y)
+
+        def launch() -> None:
+            with torch.cuda.device(x.device):
+                st = self._lib.pt_dwconv1d_fwd_bf16(_ptr(x), _ptr(k), _ptr(y), B, H, L, K,
+                                                    _stream_handle(x.device))
+            _lib.check(st, "pt_dwconv1d_fwd_bf16")
+
+        (collector or KERNEL_EVENTS).launch("fwd_bf16", launch, {"B": B, "H": H, "L": L, "K": K})
+
+    def launch_bwd_input_bf16(self, gy: torch.Tensor, k: torch.Tensor, gx: torch.Tensor,
+                              collector: KernelEventCollector | None = None) -> None:
+        self._check_open()
+        B, H, L, K = self._check_bf16(gy, k, "gy")
+        if gx.dtype != torch.bfloat16 or gx.shape != gy.shape:
+            raise ValueError("gx must be a bfloat16 tensor shaped like gy")
+        self._require_contiguous(gy, k, gx)
+
+        def launch() -> None:
+            with torch.cuda.device(gy.device):
+                st = self._lib.pt_dwconv1d_dx_bf16(_ptr(gy), _ptr(k), _ptr(gx), B, H, L, K,
+                                                   _stream_handle(gy.device))
+            _lib.check(st, "pt_dwconv1d_dx_bf16")
+
+        (collector or KERNEL_EVENTS).launch("bwd_input_bf16", launch, {"B": B, "H": H, "L": L, "K": K})
+
+    def _check_bf16_dk(self, gy, x, gk, K) -> tuple[int, int, int]:
+        if not gy.is_cuda or not x.is_cuda or not gk.is_cuda:
+            raise ValueError("gy, x, and gk must be CUDA tensors")
+        if gy.dtype != torch.bfloat16 or x.dtype != torch.bfloat16 or gk.dtype != torch.float32:
+            raise ValueError("gy and x must be bfloat16, gk float32")
+        if gy.shape != x.shape or x.ndim != 3:
+            raise ValueError("gy and x must have the same [B,H,L] shape")
+        B, H, L = map(int, x.shape)
+        if tuple(gk.shape) != (H, K):
+            raise ValueError(f"gk must have shape {(H, K)}")
+        if L > MAX_L or K > MAX_K:
+            raise ValueError(f"Specialized kernels require L<={MAX_L}, K<={MAX_K}")
+        self._require_contiguous(gy, x, gk)
+        return B, H, L
+
+    def launch_bwd_weight_bf16(self, gy: torch.Tensor, x: torch.Tensor, gk: torch.Tensor, K: int,
+                               collector: KernelEventCollector | None = None,
+                               zero_first: bool = False) -> None:
+        """Atomic BF16 dK: accumulates into the FP32 gk (zero_first clears it)."""
+        self._check_open()
+        K = int(K)
+        B, H, L = self._check_bf16_dk(gy, x, gk, K)
+
+        def launch() -> None:
+            with torch.cuda.device(x.device):
+                st = self._lib.pt_dwconv1d_dk_atomic_bf16(
+                    _ptr(gy), _ptr(x), _ptr(gk), B, H, L, K, self.bwdk_block,
+                    1 if zero_first else 0, _stream_handle(x.device))
+            _lib.check(st, "pt_dwconv1d_dk_atomic_bf16")
+
+        (collector or KERNEL_EVENTS).launch("bwd_weight_bf16", launch, {"B": B, "H": H, "L": L, "K": K})
+
+    def launch_bwd_weight_deterministic_bf16(self, gy: torch.Tensor, x: torch.Tensor,
+                                             gk: torch.Tensor, K: int,
+                                             collector: KernelEventCollector | None = None) -> None:
+        """Two-pass BF16 dK: overwrites the FP32 gk, bitwise reproducible."""
+        self._check_open()
+        K = int(K)
+        B, H, L = self._check_bf16_dk(gy, x, gk, K)
+        out = ctypes.c_size_t(0)
+        st = self._lib.pt_dwconv1d_dk_det_bf16_workspace_bytes(B, H, L, K, self.bwdk_block,
+                                                               ctypes.byref(out))
+        _lib.check(st, "pt_dwconv1d_dk_det_bf16_workspace_bytes")
+        ws = self._get_workspace(int(out.value), x.device)
+
+        def launch() -> None:
+            with torch.cuda.device(x.device):
+                st = self._lib.pt_dwconv1d_dk_det_bf16(
+                    _ptr(gy), _ptr(x), _ptr(gk), _ptr(ws), ws.numel(),
+                    B, H, L, K, self.bwdk_block, _stream_handle(x.device))
+            _lib.check(st, "pt_dwconv1d_dk_det_bf16")
+
+        (collector or KERNEL_EVENTS).launch("bwd_weight_det_bf16", launch, {"B": B, "H": H, "L": L, "K": K})
+
     # ------------------------------------------------------------- reporting
     def kernel_attributes(self, kernel_id: int, L: int, K: int) -> dict[str, int]:
         regs, lds, scratch, maxt = (ctypes.c_int(0) for _ in range(4))
@@ -620,6 +727,44 @@ def depthwise_conv_ampere(x: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
     return DepthConvAmpere.apply(x, k)
 
 
+class DepthConvBf16(torch.autograd.Function):
+    """BF16-I/O counterpart of DepthConvAmpere (no reference counterpart):
+    x, y and the activation gradients are bfloat16, k and its gradient FP32
+    (the two-pass deterministic dK)."""
+
+    @staticmethod
+    def forward(ctx: Any, x: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
+        runtime = get_runtime()
+        x_c = x.contiguous()
+        k_c = k.contiguous()
+        B, H, L, K = runtime._check_bf16(x_c, k_c, "x")
+        y = torch.empty_like(x_c)
+        runtime.launch_fwd_bf16(x_c, k_c, y)
+        ctx.save_for_backward(x_c, k_c)
+        ctx.params = (B, H, L, K)
+        return y
+
+    @staticmethod
+    def backward(ctx: Any, gy: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        runtime = get_runtime()
+        x_c, k_c = ctx.saved_tensors
+        B, H, L, K = ctx.params
+        gy_c = gy.to(torch.bfloat16).contiguous()
+        gx = gk = None
+        if ctx.needs_input_grad[0]:
+            gx = torch.empty_like(x_c)
+            runtime.launch_bwd_input_bf16(gy_c, k_c, gx)
+        if ctx.needs_input_grad[1]:
+            gk = torch.empty_like(k_c)
+            runtime.launch_bwd_weight_deterministic_bf16(gy_c, x_c, gk, K)
+        return gx, gk
+
+
+def depthwise_conv_bf16(x: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
+    """y = conv(x, k) for bfloat16 x and FP32 k (L % 4 == 0, H % 8 == 0)."""
+    return DepthConvBf16.apply(x, k)
+
+
 def reference_depthwise_conv(x: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
     """PyTorch form of the same op (kernels/warp_tiled_ampere.py:901-903); the
     S4ConvD "pytorch" backend, not a fallback of the HIP path."""
@@ -651,5 +796,6 @@ __all__ = [
     "HipWarpRuntime", "AmpereWarpRuntime",
     "install_runtime", "get_runtime", "get_or_create_runtime",
     "DepthConvAmpere", "depthwise_conv_ampere", "reference_depthwise_conv",
+    "DepthConvBf16", "depthwise_conv_bf16",
     "configure_torch",
 ]

@@ -115,6 +115,39 @@ def test_argument_validation_before_launch(lib):
     del P
 
 
+def test_bf16_argument_validation_before_launch(lib):
+    """BF16 entry points: shape, then layout (PT_ERR_CONFIG: L % 4, H % 8 for
+    FWD/DX, the channel-group block rule for DK), then empty tensors, NULL,
+    and 16-byte alignment, all before any device work."""
+    from pathtile_amd import _lib
+
+    buf = (ctypes.c_ubyte * 4096)()
+    base = ctypes.addressof(buf)
+    al = base + (-base) % 16
+    pa, pb, pc = (ctypes.c_void_p(al + o) for o in (0, 1024, 2048))
+    mis = ctypes.c_void_p(al + 8)
+    S = None
+    for fn in (lib.pt_dwconv1d_fwd_bf16, lib.pt_dwconv1d_dx_bf16):
+        assert fn(pa, pb, pc, 2, 8, 49, 5, S) == _lib.PT_ERR_SHAPE
+        assert fn(pa, pb, pc, 2, 8, 18, 5, S) == _lib.PT_ERR_CONFIG   # L % 4
+        assert fn(pa, pb, pc, 2, 12, 16, 5, S) == _lib.PT_ERR_CONFIG  # H % 8
+        assert fn(pa, pb, pc, 0, 8, 16, 5, S) == _lib.PT_OK           # empty
+        assert fn(None, pb, pc, 2, 8, 16, 5, S) == _lib.PT_ERR_NULL
+        assert fn(mis, pb, pc, 2, 8, 16, 5, S) == _lib.PT_ERR_ALIGN
+    dk = lib.pt_dwconv1d_dk_atomic_bf16
+    assert dk(pa, pb, pc, 2, 8, 18, 5, 128, 0, S) == _lib.PT_ERR_CONFIG   # L % 4
+    assert dk(pa, pb, pc, 2, 6, 16, 5, 256, 0, S) == _lib.PT_ERR_CONFIG   # H % (2 * 4)
+    assert dk(pa, pb, pc, 2, 24, 16, 5, 768, 0, S) == _lib.PT_ERR_CONFIG  # > 8 waves
+    assert dk(pa, pb, None, 2, 8, 16, 5, 128, 0, S) == _lib.PT_ERR_NULL
+    assert dk(mis, pb, pc, 2, 8, 16, 5, 128, 0, S) == _lib.PT_ERR_ALIGN
+    out = ctypes.c_size_t(0)
+    st = lib.pt_dwconv1d_dk_det_bf16_workspace_bytes(16384, 128, 48, 48, 128, ctypes.byref(out))
+    # BF16 tensors of 192 MiB (below the 256 MiB MALL rule), steps of
+    # 4 x 128 x 48 x 2 bytes = 48 KiB: the power of two nearest 2.5 MiB, 64
+    assert st == _lib.PT_OK and out.value == 128 * 48 * 64 * 4
+    assert lib.pt_dwconv1d_dk_det_bf16(pa, pb, pc, None, 0, 2, 8, 16, 5, 128, S) == _lib.PT_ERR_WORKSPACE
+
+
 def test_workspace_bytes(lib):
     from pathtile_amd import _lib
 
