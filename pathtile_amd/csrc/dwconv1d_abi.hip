@@ -405,13 +405,13 @@ static RowsAlgo rows_algo(int L, int K) {
 // sample range), the ranges interleaved in 16-sample steps. As many ranges as
 // fill the CUs with min(2, resident) workgroups each (two measured best where
 // the LDS allows them, L <= 32; at L = 48 one fits).
-// hc: channels (= waves) per workgroup; max_per_cu: workgroups per CU the
-// range count is sized for (at most what fits).
+// hc: channels (= waves) per workgroup; lds: dynamic LDS per workgroup;
+// max_per_cu: workgroups per CU the range count is sized for (at most what
+// fits).
 template <typename T, typename Fn>
 static int rows_cg_launch(Fn fn, const T* in, const float* w, T* out, int B,
-                          int H, int L, int K, void* stream,
-                          int hc = kRowsCgWaves, int max_per_cu = 2) {
-  const size_t lds = rows_cg_lds_bytes(L, hc);
+                          int H, int L, int K, void* stream, int hc,
+                          size_t lds, int max_per_cu) {
   const int threads = hc * kWave;
   int per_cu = blocks_per_cu((const void*)fn, threads, lds);
   if (per_cu > max_per_cu) per_cu = max_per_cu;
@@ -431,7 +431,7 @@ static int rows_cg_launch(Fn fn, const T* in, const float* w, T* out, int B,
 static int rows_cg_path(bool dx, const float* in, const float* w, float* out,
                         int B, int H, int L, int K, void* stream) {
   return rows_cg_launch(kRowsCgTable[dx ? 1 : 0][mfma_index(L)], in, w, out, B,
-                        H, L, K, stream);
+                        H, L, K, stream, kRowsCgWaves, rows_cg_lds_bytes(L), 2);
 }
 
 static long long gcd_ll(long long a, long long b) {
@@ -521,29 +521,27 @@ static int dk_path(bool det, const float* gy, const float* x, float* dst,
 }
 
 // --- BF16 I/O --------------------------------------------------------------
-// x, y, dy, dx are bfloat16 (uint16_t bit patterns), w and dk FP32; the
-// kernels widen BF16 to FP32 exactly, accumulate in FP32 on the matrix cores
-// and narrow FP32 outputs to BF16 with round-to-nearest-even. Only the
-// channel-group kernels take BF16: rows of whole 16-byte LDS vectors
-// (L % 4 == 0), 16-byte aligned tensors, H % 8 == 0 (FWD / DX) or
-// H % (2 * waves) == 0 with at most 8 waves (DK).
+// x, y, dy, dx are bfloat16 (uint16_t bit patterns), w and dk FP32. FWD / DX
+// run on the BF16 matrix cores (FP32 taps as a hi + lo BF16 pair), DK on the
+// channel-group kernel with BF16 widened to FP32 in LDS; both accumulate in
+// FP32, and BF16 outputs are rounded to nearest-even. Layout: 4-value
+// aligned row offsets (L % 4 == 0), 16-byte aligned tensors, H % 8 == 0
+// (FWD / DX) or H % (2 * waves) == 0 with at most 8 waves (DK).
 static int bf16_rows_path(bool dx, const void* in, const float* w, void* out,
                           int B, int H, int L, int K, void* stream) {
   int st = check_shape(B, H, L, K);
   if (st != PT_OK) return st;
   if (L % 4 != 0 || H % kRowsCgWaves != 0) return PT_ERR_CONFIG;
-  if (rows_cg_lds_bytes(L) > (size_t)max_lds_per_block()) return PT_ERR_CONFIG;
+  const size_t lds = rows_bf16mma_lds_bytes(L, kRowsCgWaves);
+  if (lds > (size_t)max_lds_per_block()) return PT_ERR_CONFIG;
   if (B == 0 || H == 0) return PT_OK;
   if (!in || !w || !out) return PT_ERR_NULL;
   if (!aligned(in, 16) || !aligned(out, 16) || !aligned(w, 4)) return PT_ERR_ALIGN;
-  // Row bucket 48: 4-channel groups, three per CU (the matrix cores' step
-  // pipeline, not HBM, bounds the BF16 kernel; 12 waves per CU hide it best,
-  // 10% faster than 8-channel groups at B16384 H128 L48 on MI355X).
-  const bool l48 = mfma_index(L) == 2;
+  // up to three workgroups per CU where the LDS allows (two at L = 48):
+  // measured best on MI355X at L = 16, 32 and 48
   return rows_cg_launch(kRowsCgTableBf16[dx ? 1 : 0][mfma_index(L)],
                         (const uint16_t*)in, w, (uint16_t*)out, B, H, L, K,
-                        stream, l48 ? kRowsCgBf16WavesL48 : kRowsCgWaves,
-                        l48 ? 3 : 2);
+                        stream, kRowsCgWaves, lds, 3);
 }
 
 static int bf16_dk_check(int B, int H, int L, int K, int threads) {

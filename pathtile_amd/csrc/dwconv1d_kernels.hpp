@@ -798,7 +798,6 @@ __global__ __launch_bounds__(1024) void dwconv_dk_mfma_kernel(
 // results agree with it to FP32 rounding (about 3e-7 max-abs-scaled).
 // ---------------------------------------------------------------------------
 constexpr int kRowsCgWaves = 8;    // one channel per wave
-constexpr int kRowsCgBf16WavesL48 = 4;  // BF16, row bucket 48: smaller groups
 constexpr int kRowsCgStep = 16;    // samples per step (MFMA M)
 
 // 16-byte chunks of the staged segments: 4 FP32 or 8 BF16 elements (BF16 is
@@ -1006,6 +1005,179 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
         if (s < nsteps) {
           // Output stage s & 1 was last read by flush_out(s - 2), which
           // every thread finished before the barrier of step s - 1.
+          mfma_step(s);
+          if (s + 1 < nsteps) {
+            store_stage((s + 1) & 1, stg[(d + 1) % kDepth]);
+            if (s + 1 + kDepth < nsteps)
+              load_step(s + 1 + kDepth, stg[(d + 1) % kDepth]);
+          }
+          __syncthreads();
+          flush_out(s);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// FWD / DX with BF16 I/O on the BF16 matrix cores. The channel-group tiling
+// and pipeline of dwconv_rows_cg_kernel, with three differences:
+//  * the input stages hold the BF16 values as they arrive (2 bytes each), and
+//    a lane reads its A operands straight from them as 4-element BF16
+//    vectors (no widening);
+//  * v_mfma_f32_16x16x16_bf16 (M = 16 samples, N = 16 output columns,
+//    K = 16 input columns) replaces four FP32 16x16x4 instructions; K slot
+//    4 kg + i of MFMA u is input column (LMAX/4) kg + 4 u + i, so a lane's A
+//    operands for all u are LMAX/4 consecutive values;
+//  * the FP32 taps enter as two BF16 operands, hi = bf16(w) and
+//    lo = bf16(w - hi), two MFMAs per chunk: the products x * hi + x * lo are
+//    exact in FP32 and hi + lo differs from w by at most 2^-16 |w|, far
+//    below the BF16 rounding of the outputs.
+// Outputs go through FP32 output stages in LDS and narrow to BF16
+// (round-to-nearest-even) on the way out, as in the templated kernel.
+// ---------------------------------------------------------------------------
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__host__ __device__ constexpr size_t rows_bf16mma_lds_bytes(int L, int hc) {
+  // two BF16 input stages of 16 samples x (hc * L + 8) values, two FP32
+  // output stages of 16 samples x (hc * L + 4) values
+  return (size_t)2 * kRowsCgStep * (hc * L + 8) * 2 +
+         (size_t)2 * kRowsCgStep * (hc * L + 4) * sizeof(float);
+}
+
+template <int LMAX, bool DX, int HC>
+__global__ __launch_bounds__(HC * kWave) void dwconv_rows_bf16mma_kernel(
+    const uint16_t* __restrict__ in, const float* __restrict__ w,
+    uint16_t* __restrict__ out, int B, int H, int L, int K, int nranges,
+    uint32_t nblocks) {
+  constexpr int NT = LMAX / 16;    // 16-wide output tiles
+  constexpr int NUB = LMAX / 4;    // input columns per K group of a lane
+  constexpr int NG = NUB / 4;      // MFMAs (16 input columns) per tile
+  constexpr int kDepth = 2;        // steps in flight in registers
+  constexpr int kNpt = (HC * LMAX * kRowsCgStep / 8 + HC * kWave - 1) / (HC * kWave);
+  extern __shared__ float lds[];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int ngroups = H / HC;
+  const uint32_t blk = xcd_remap(blockIdx.x, nblocks);
+  const int g = (int)(blk % (uint32_t)ngroups);
+  const int r = (int)(blk / (uint32_t)ngroups);
+  const int tsteps = (B + kRowsCgStep - 1) / kRowsCgStep;
+  const int nsteps = r < tsteps ? (tsteps - 1 - r) / nranges + 1 : 0;
+
+  const int seg = HC * L, segc = seg / 8;   // BF16 values, 16-byte chunks
+  const int ski = seg + 8;                  // input-stage stride (values)
+  const int sko = seg + 4;                  // output-stage stride (floats)
+  const int per = kRowsCgStep * segc;       // chunks per stage
+  const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 2u;
+  const uint32_t grp_bytes = (uint32_t)g * (uint32_t)seg * 2u;
+  uint16_t* inl = reinterpret_cast<uint16_t*>(lds);             // 2 stages
+  float* outl = lds + (2 * kRowsCgStep * ski) / 2;               // 2 stages
+  const int szi = kRowsCgStep * ski, szo = kRowsCgStep * sko;
+
+  int ek[kNpt];
+  uint32_t eoff[kNpt], elds[kNpt], oelds[kNpt];
+#pragma unroll
+  for (int i = 0; i < kNpt; ++i) {
+    const int e = i * (HC * kWave) + (int)threadIdx.x;
+    const int k = e < per ? e / segc : kRowsCgStep;
+    const int q = e - (e / segc) * segc;
+    ek[i] = k;
+    eoff[i] = (uint32_t)k * row_bytes + grp_bytes + 16u * (uint32_t)q;
+    elds[i] = (uint32_t)(k * ski + 8 * q);   // in BF16 values
+    oelds[i] = (uint32_t)(k * sko + 8 * q);  // in floats
+  }
+  u32x4 stg[kDepth][kNpt];
+  auto load_step = [&](int s, u32x4 (&st)[kNpt]) {
+    const int bs = (r + s * nranges) * kRowsCgStep;
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc_t(in + (size_t)bs * (size_t)H * (size_t)L);
+    const int klim = min(kRowsCgStep, B - bs);
+#pragma unroll
+    for (int i = 0; i < kNpt; ++i)
+      st[i] = buf_load_chunk<kCpolNT>(rs, ek[i] < klim ? eoff[i] : kOob);
+  };
+  auto store_stage = [&](int buf, const u32x4 (&st)[kNpt]) {
+#pragma unroll
+    for (int i = 0; i < kNpt; ++i)
+      if (ek[i] < kRowsCgStep)
+        *reinterpret_cast<u32x4*>(inl + buf * szi + elds[i]) = st[i];
+  };
+  auto flush_out = [&](int s) {
+    const float* o = outl + (s & 1) * szo;
+    const int bs = (r + s * nranges) * kRowsCgStep;
+    const __amdgpu_buffer_rsrc_t ro =
+        make_rsrc_t(out + (size_t)bs * (size_t)H * (size_t)L);
+    const int klim = min(kRowsCgStep, B - bs);
+#pragma unroll
+    for (int i = 0; i < kNpt; ++i) {
+      const u32x4 v = lds_to_chunk<uint16_t>(o + (ek[i] < kRowsCgStep ? oelds[i] : 0u));
+      buf_store_chunk<kCpolNT>(v, ro, ek[i] < klim ? eoff[i] : kOob);
+    }
+  };
+
+  // B operands: MFMA u, tile tt, lane (n = l % 16, kg = l / 16), element i:
+  // input column s = NUB kg + 4 u + i, output column t = 16 tt + n.
+  const int kg = lane >> 4, jj = lane & 15;
+  const int p = K >> 1;
+  const int h = g * HC + wave;
+  s16x4 bh[NG][NT], bl[NG][NT];
+#pragma unroll
+  for (int u = 0; u < NG; ++u)
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int sc = NUB * kg + 4 * u + i, tc = 16 * tt + jj;
+        const int j = DX ? (tc - sc + p) : (sc - tc + p);
+        const bool ok = j >= 0 && j < K && sc < L && tc < L;
+        const float wv = ok ? w[(size_t)h * K + j] : 0.0f;
+        const uint32_t hi = bf16_bits_rne(wv);
+        const uint32_t lo = bf16_bits_rne(wv - __uint_as_float(hi << 16));
+        bh[u][tt][i] = (short)hi;
+        bl[u][tt][i] = (short)lo;
+      }
+
+  const int rq = 4 * kg;
+  const int cb = wave * L;
+  auto mfma_step = [&](int s) {
+    const uint16_t* src = inl + (s & 1) * szi + jj * ski + cb + NUB * kg;  // sample jj
+    float* o = outl + (s & 1) * szo;
+    s16x4 a[NG];
+#pragma unroll
+    for (int u = 0; u < NG; ++u) {
+      a[u] = *reinterpret_cast<const s16x4*>(src + 4 * u);
+      if (L != LMAX && NUB * kg + 4 * u >= L) a[u] = s16x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < NG; ++u) {
+        d = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a[u], bh[u][tt], d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a[u], bl[u][tt], d, 0, 0, 0);
+      }
+      const int t = 16 * tt + jj;
+      if (t < L) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) o[(rq + rr) * sko + cb + t] = d[rr];
+      }
+    }
+  };
+
+  if (nsteps > 0) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d)
+      if (d < nsteps) load_step(d, stg[d]);
+    store_stage(0, stg[0]);
+    if (kDepth < nsteps) load_step(kDepth, stg[0]);
+    __syncthreads();
+    for (int s0 = 0; s0 < nsteps; s0 += kDepth) {
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) {
+        const int s = s0 + d;
+        if (s < nsteps) {
           mfma_step(s);
           if (s + 1 < nsteps) {
             store_stage((s + 1) & 1, stg[(d + 1) % kDepth]);
