@@ -129,9 +129,10 @@ int pt_dwconv1d_dk_det_f32(const float* dy, const float* x, float* dk,
 /*
  * BF16 I/O variants (no counterpart in the reference, which is FP32 only).
  * x, y, dy, dx are bfloat16 tensors passed as their 16-bit patterns; w and dk
- * stay FP32. The kernels widen BF16 to FP32 exactly, accumulate in FP32 on
- * the matrix cores (the channel-group kernels above), and round FP32 outputs
- * to BF16 to nearest-even. They halve the bytes the paths move. Only the
+ * stay FP32. The kernels multiply on the BF16 matrix cores with FP32
+ * accumulation (FWD/DX split each FP32 tap into a hi + lo BF16 pair; DK
+ * products of two BF16 values are exact in FP32) and round FP32 outputs to
+ * BF16 to nearest-even. They halve the bytes the paths move. Only the
  * channel-group layout is served: L % 4 == 0 and, for FWD/DX, H % 8 == 0,
  * for DK, threads_per_block <= 512 with H % (2 * threads_per_block / 64) == 0
  * (PT_ERR_CONFIG otherwise); BF16 tensors must be 16-byte aligned

@@ -186,27 +186,34 @@ static bool dk_cg_ok(int H, int L, int threads) {
 // Measured on MI355X over the 30 tuner shapes, P and S with the tuner's own
 // protocol, both libraries on one box. Both depend on the shape only (not on
 // the block size or the device).
-static bool cg_large(int B, int H, int L, int esize = 4) {
-  return (double)esize * (double)B * (double)H * (double)L >= kDkMallBytes;
+static bool cg_large(int B, int H, int L) {
+  return 4.0 * (double)B * (double)H * (double)L >= kDkMallBytes;
 }
 
-static long long cg_ranges(int B, int H, int L, int esize = 4) {
-  const double step_bytes = (double)kCgStep * esize * (double)H * (double)L;
+// Of the counts 2^k and 3 * 2^(k-1) in [8, 256], the one nearest (by ratio;
+// ties to the smaller) to `want`.
+static long long nearest_range_count(double want) {
   long long nr = 8;
-  if (cg_large(B, H, L, esize)) {
-    const double want = 3.0 * 1024 * 1024 / step_bytes;
-    double best = 1e300;
-    for (long long p = 8; p <= 256; p *= 2) {
-      const long long cands[2] = {p, p + p / 2};
-      for (long long c : cands) {
-        if (c > 256) continue;
-        const double d = fabs(log((double)c / want));
-        if (d < best - 1e-12) {
-          best = d;
-          nr = c;
-        }
+  double best = 1e300;
+  for (long long p = 8; p <= 256; p *= 2) {
+    const long long cands[2] = {p, p + p / 2};
+    for (long long c : cands) {
+      if (c > 256) continue;
+      const double d = fabs(log((double)c / want));
+      if (d < best - 1e-12) {
+        best = d;
+        nr = c;
       }
     }
+  }
+  return nr;
+}
+
+static long long cg_ranges(int B, int H, int L) {
+  const double step_bytes = (double)kCgStep * 4.0 * (double)H * (double)L;
+  long long nr = 8;
+  if (cg_large(B, H, L)) {
+    nr = nearest_range_count(3.0 * 1024 * 1024 / step_bytes);
   } else {
     const double want = 2.5 * 1024 * 1024 / step_bytes;
     while (nr < 256 && (double)(nr * 2) <= want * 1.41421356) nr *= 2;
@@ -216,8 +223,29 @@ static long long cg_ranges(int B, int H, int L, int esize = 4) {
   return nr < 1 ? 1 : nr;
 }
 
-// esize: bytes per element of dy and x (4 FP32, 2 BF16; BF16 runs the
-// channel-group kernel only).
+// BF16 DK on the BF16 matrix cores (16-sample steps):
+//  * sample ranges: the 3 MiB count above for the 16-sample step, at every
+//    tensor size (over the tuner's 30 shapes plus P, S and E2 in BF16 it was
+//    1.4% faster in total than the 2.5 MiB power of two and 5% faster than
+//    2 MiB);
+//  * loads: non-temporal from 64 MiB per tensor up (4-9% faster there, e.g.
+//    65 vs 69 us at P in BF16 and 234 vs 251 us at S), plain below (up to
+//    20% faster on 32 MiB tensors).
+// Measured on MI355X with interleaved rounds and a duplicate control.
+constexpr double kBmNtBytes = 64.0 * 1024 * 1024;
+
+static bool bm_nt(int B, int H, int L) {
+  return 2.0 * (double)B * (double)H * (double)L >= kBmNtBytes;
+}
+
+static long long bm_ranges(int B, int H, int L) {
+  const double step_bytes = (double)kBmStep * 2.0 * (double)H * (double)L;
+  long long nr = nearest_range_count(3.0 * 1024 * 1024 / step_bytes);
+  const long long tsteps = ((long long)B + kBmStep - 1) / kBmStep;
+  if (nr > tsteps) nr = tsteps;
+  return nr < 1 ? 1 : nr;
+}
+
 static DkGeom dk_geometry(int B, int H, int L, int K, int threads, bool vec16,
                           int esize = 4) {
   DkGeom g;
@@ -226,10 +254,10 @@ static DkGeom dk_geometry(int B, int H, int L, int K, int threads, bool vec16,
   const long long wpb = g.wpb;
   const long long rows = (long long)B * H;
   g.cg = g.algo == kDkMfma && vec16 && dk_cg_ok(H, L, threads);
-  g.nt = g.cg && cg_large(B, H, L, esize);
+  g.nt = g.cg && cg_large(B, H, L);
   if (g.cg) {
     const long long ngroups = (long long)H / (kCgChannelsPerWave * wpb);
-    const long long nr = cg_ranges(B, H, L, esize);
+    const long long nr = cg_ranges(B, H, L);
     g.rows_per_wave = 0;
     g.nbt = (int)nr;
     g.nblocks = ngroups * nr;
@@ -551,11 +579,25 @@ static int bf16_dk_check(int B, int H, int L, int K, int threads) {
   return PT_OK;
 }
 
+// Geometry of the BF16 DK (one kernel: the shape checks of bf16_dk_check
+// admit exactly the layouts it serves).
+static DkGeom bm_geometry(int B, int H, int L, int threads) {
+  DkGeom g;
+  g.algo = kDkMfma;
+  g.cg = true;
+  g.nt = bm_nt(B, H, L);
+  g.wpb = threads / kWave;
+  g.rows_per_wave = 0;
+  g.nbt = (int)bm_ranges(B, H, L);
+  g.nblocks = (long long)H / (kCgChannelsPerWave * g.wpb) * g.nbt;
+  return g;
+}
+
 static int bf16_dk_launch(bool det, const void* gy, const void* x, float* dst,
                           int B, int H, int L, int K, int threads,
                           const DkGeom& g, void* stream) {
-  DkCgBf16Fn fn = (g.nt ? kDkCgTableBf16NT : kDkCgTableBf16)[mfma_index(L)];
-  const size_t lds = cg_lds_bytes(16 * (mfma_index(L) + 1), g.wpb, L);
+  DkBf16Fn fn = (g.nt ? kDkBf16mmaTableNT : kDkBf16mmaTable)[mfma_index(L)];
+  const size_t lds = dk_bf16mma_lds_bytes(16 * (mfma_index(L) + 1), g.wpb);
   const uint16_t* gyp = (const uint16_t*)gy;
   const uint16_t* xp = (const uint16_t*)x;
   uint32_t nblocks = (uint32_t)g.nblocks;
@@ -766,8 +808,7 @@ int pt_dwconv1d_dk_atomic_bf16(const void* dy, const void* x, float* dk, int B,
   if (B == 0) return PT_OK;
   if (!dy || !x) return PT_ERR_NULL;
   if (!pt::aligned(dy, 16) || !pt::aligned(x, 16)) return PT_ERR_ALIGN;
-  const pt::DkGeom g = pt::dk_geometry(B, H, L, K, threads_per_block, true, 2);
-  if (!g.cg) return PT_ERR_CONFIG;  // e.g. PATHTILE_DK_ALGO=valu
+  const pt::DkGeom g = pt::bm_geometry(B, H, L, threads_per_block);
   if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
   return pt::bf16_dk_launch(false, dy, x, dk, B, H, L, K, threads_per_block, g,
                             stream);
@@ -783,7 +824,7 @@ int pt_dwconv1d_dk_det_bf16_workspace_bytes(int B, int H, int L, int K,
     *bytes = 0;
     return PT_OK;
   }
-  const long long nr = pt::cg_ranges(B, H, L, 2);
+  const long long nr = pt::bm_ranges(B, H, L);
   *bytes = (size_t)H * (size_t)K * (size_t)nr * sizeof(float);
   return PT_OK;
 }
@@ -800,8 +841,7 @@ int pt_dwconv1d_dk_det_bf16(const void* dy, const void* x, float* dk,
   if (B == 0) return pt::zero_fill(dk, H * K, stream);
   if (!dy || !x) return PT_ERR_NULL;
   if (!pt::aligned(dy, 16) || !pt::aligned(x, 16)) return PT_ERR_ALIGN;
-  const pt::DkGeom g = pt::dk_geometry(B, H, L, K, threads_per_block, true, 2);
-  if (!g.cg) return PT_ERR_CONFIG;
+  const pt::DkGeom g = pt::bm_geometry(B, H, L, threads_per_block);
   if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
   const size_t need = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
   if (!workspace || workspace_bytes < need) return PT_ERR_WORKSPACE;

@@ -1238,6 +1238,72 @@ __host__ __device__ constexpr size_t cg_lds_bytes(int lmax, int wpb, int L) {
   return (stages > dtile ? stages : dtile) * sizeof(float);
 }
 
+// Epilogue shared by the channel-group DK kernels. Per wave: D_c through
+// the wave's own LDS tile (the stages are free after the kernel's last
+// barrier), then lane j < K sums D_c[t][t + j - p] over t in [t0, t1) in
+// four fixed-order partial sums, all reads issued at once (the t loop is
+// unrolled over the bucket, out-of-range terms masked). The workgroup's
+// channels are consecutive, so its hc x K tap sums are one contiguous block
+// of dk: they are collected in LDS and added with one coalesced atomic per
+// element (a few cache lines per workgroup, not one line operation per wave
+// and channel, which contended badly at small K). det: write the sums as
+// partials [h][j][nranges] instead.
+template <int LMAX>
+__device__ __forceinline__ void dk_cg_epilogue(
+    const f32x4 (&acc)[kCgChannelsPerWave][LMAX / 16][LMAX / 16], float* lds,
+    float* __restrict__ dst, int wave, int wpb, int g, int r, int hc, int L,
+    int K, int nranges, int det) {
+  using G = CgGeo<LMAX>;
+  constexpr int NT = G::nt;
+  constexpr int CPW = kCgChannelsPerWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int nthreads = blockDim.x;
+  float* dt = lds + wave * (G::dim * G::dstride);
+  float* taps = lds + wpb * (G::dim * G::dstride);  // [hc][K]
+  const int rq = 4 * (lane >> 4);
+  const int cl = lane & 15;
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+#pragma unroll
+    for (int a = 0; a < NT; ++a)
+#pragma unroll
+      for (int b = 0; b < NT; ++b)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          dt[(16 * a + rq + rr) * G::dstride + 16 * b + cl] = acc[c][a][b][rr];
+    wave_lds_sync();
+    const int hl = wave * CPW + c;  // channel within the group
+    if (lane < K) {
+      const int j = lane;
+      const int m = j - (K >> 1);
+      const int t0 = max(0, -m);
+      const int t1 = min(L, L - m);
+      float v4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int t = 0; t < G::dim; ++t) {
+        // D_c[t][t + m] = dt[m + t * (dstride + 1)]; masked terms read a
+        // clamped in-tile address (a tap may have no valid t at all).
+        int idx = m + t * (G::dstride + 1);
+        idx = idx < 0 ? 0 : (idx < G::dim * G::dstride ? idx : G::dim * G::dstride - 1);
+        const float d = dt[idx];
+        v4[t & 3] += (t >= t0 && t < t1) ? d : 0.0f;
+      }
+      const float v = (v4[0] + v4[1]) + (v4[2] + v4[3]);
+      if (det) {
+        dst[((size_t)(g * hc + hl) * K + j) * (size_t)nranges + r] = v;
+      } else {
+        taps[hl * K + j] = v;
+      }
+    }
+    wave_lds_sync();
+  }
+  if (!det) {
+    __syncthreads();
+    float* out = dst + (size_t)g * hc * K;
+    for (int e = threadIdx.x; e < hc * K; e += nthreads) atomicAdd(out + e, taps[e]);
+  }
+}
+
 // T: element type of gy and x (float, or uint16_t holding bfloat16); dk and
 // its partials are FP32 either way.
 template <int LMAX, int LOAD_CPOL = kCpolNone, typename T = float>
@@ -1376,59 +1442,200 @@ __global__ __launch_bounds__(512) void dwconv_dk_cg_kernel(
     }
   }
 
-  // Per-wave epilogue: D_c through the wave's own LDS tile (the stages are
-  // free after the last barrier), then lane j < K sums D_c[t][t + j - p]
-  // over t in [t0, t1) in four fixed-order partial sums, all reads issued
-  // at once (the t loop is unrolled over the bucket, out-of-range terms
-  // masked). The workgroup's channels are consecutive, so its hc x K tap
-  // sums are one contiguous block of dk: they are collected in LDS and added
-  // with one coalesced atomic per element (a few cache lines per workgroup,
-  // not one line operation per wave and channel, which contended badly at
-  // small K).
-  float* dt = lds + wave * (G::dim * G::dstride);
-  float* taps = lds + wpb * (G::dim * G::dstride);  // [hc][K]
-  const int rq = 4 * (lane >> 4);
-  const int cl = lane & 15;
+  dk_cg_epilogue<LMAX>(acc, lds, dst, wave, wpb, g, r, hc, L, K, nranges, det);
+}
+
+// ---------------------------------------------------------------------------
+// Channel-group DK for BF16 tensors on the BF16 matrix cores.
+//
+// The channel-group DK above with three changes that keep its per-step
+// pipeline off the critical path when the tensors are half as large:
+//  * a step is 16 samples, the K of v_mfma_f32_16x16x16bf16_1k (4x fewer
+//    barriers and LDS round trips per sample than 4-sample FP32 steps);
+//  * the LDS stages keep the raw BF16 values (16-byte chunk copies, no
+//    widening);
+//  * each D_c tile is 16x16 BF16 products summed over 16 samples per
+//    instruction. A product of two BF16 values is exact in FP32, so the
+//    accumulation is the only rounding, as with widened operands.
+// LDS is one region per wave, [stage][tensor][sample][kBmRow(LMAX)]: the
+// wave's two channels (2 L values, a multiple of 8, so no 16-byte chunk
+// straddles two waves) of each of the 16 samples. Every offset inside a
+// region is a compile-time constant, so the operand gathers use one lane
+// address per (channel, column tile) and immediate offsets.
+// The MFMA's K index k = 4 * (lane / 16) + v (v = 0..3; lane l holds
+// A[l % 16][k] and B[k][l % 16]) is mapped to sample kq + 4 v of the step
+// (kq = lane / 16): any bijection gives the same sum over the step, and this
+// one puts the four 16-lane groups of a wave one row apart; a row length of
+// 16 (mod 32) values puts them in disjoint LDS banks.
+// ---------------------------------------------------------------------------
+constexpr int kBmStep = 16;  // samples per stage (the BF16 MFMA K)
+
+// Values per sample row of a wave's region: at least the wave's two
+// channels of the bucket, 16 (mod 32).
+__host__ __device__ constexpr int kBmRow(int lmax) {
+  return kCgChannelsPerWave * lmax + ((16 - (kCgChannelsPerWave * lmax) % 32) % 32 + 32) % 32;
+}
+
+// Dynamic LDS of the BF16 DK kernel: the wave regions (two stages of both
+// tensors), or, for the epilogue, one D tile per wave plus the tap sums.
+__host__ __device__ constexpr size_t dk_bf16mma_lds_bytes(int lmax, int wpb) {
+  const size_t stages = (size_t)wpb * 2 * 2 * kBmStep * (size_t)kBmRow(lmax) * sizeof(uint16_t);
+  const size_t dtile = ((size_t)wpb * (16 * (lmax / 16)) * (16 * (lmax / 16) + 1) +
+                        (size_t)kCgChannelsPerWave * wpb * kMaxK) *
+                       sizeof(float);
+  return stages > dtile ? stages : dtile;
+}
+
+template <int LMAX, int LOAD_CPOL = kCpolNone>
+__global__ __launch_bounds__(512) void dwconv_dk_bf16mma_kernel(
+    const uint16_t* __restrict__ gy, const uint16_t* __restrict__ x,
+    float* __restrict__ dst, int B, int H, int L, int K, int nranges,
+    uint32_t nblocks, int det) {
+  using G = CgGeo<LMAX>;
+  constexpr int NT = G::nt;
+  constexpr int CPW = kCgChannelsPerWave;
+  constexpr int STEP = kBmStep;
+  constexpr int EPC = ChunkOf<uint16_t>::n;  // 8 values per 16-byte chunk
+  constexpr int ROW = kBmRow(LMAX);
+  constexpr int TSZ = STEP * ROW;            // one tensor's stage in a region
+  constexpr int REGION = 2 * 2 * TSZ;        // one wave's region
+  extern __shared__ float lds[];
+  uint16_t* const l16 = reinterpret_cast<uint16_t*>(lds);
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wpb = blockDim.x / kWave;
+  const int nthreads = blockDim.x;
+  const int hc = CPW * wpb;
+  const int ngroups = H / hc;
+  const uint32_t blk = xcd_remap(blockIdx.x, nblocks);
+  const int g = (int)(blk % (uint32_t)ngroups);
+  const int r = (int)(blk / (uint32_t)ngroups);
+  const int tsteps = (B + STEP - 1) / STEP;
+  const int nsteps = r < tsteps ? (tsteps - 1 - r) / nranges + 1 : 0;
+
+  const int seg = hc * L;                 // values per sample segment
+  const int segc = seg / EPC;             // chunks per segment
+  const int wseg = CPW * L;               // values of one wave per sample
+  const int per = STEP * segc;            // chunks per stage and tensor
+  constexpr int kNpt = (CPW * LMAX * STEP / EPC + kWave - 1) / kWave;
+  const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 2u;  // one sample
+  const uint32_t grp_bytes = (uint32_t)g * (uint32_t)seg * 2u;
+
+  // Loop-invariant part of each staged chunk: its sample within the step,
+  // its byte offset from the step's first sample, its place in LDS (the
+  // region of the wave whose channels it holds).
+  int ek[kNpt];
+  uint32_t eoff[kNpt], elds[kNpt];
 #pragma unroll
-  for (int c = 0; c < CPW; ++c) {
+  for (int i = 0; i < kNpt; ++i) {
+    const int e = i * nthreads + (int)threadIdx.x;
+    const int k = e < per ? e / segc : STEP;  // STEP: no chunk
+    const int q = e - (e / segc) * segc;
+    const int w = (EPC * q) / wseg;
+    ek[i] = k;
+    eoff[i] = (uint32_t)k * row_bytes + grp_bytes + 16u * (uint32_t)q;
+    elds[i] = (uint32_t)(w * REGION + k * ROW + (EPC * q - w * wseg));
+  }
+
+  // One step in flight in registers: a 16-sample step is 4x the bytes of
+  // an FP32 channel-group step, and a second one measured no faster.
+  u32x4 stg[2][kNpt];
+  auto load_step = [&](int s, u32x4 (&st)[2][kNpt]) {
+    const int bs = (r + s * nranges) * STEP;
+    const size_t r0 = (size_t)bs * (size_t)H * (size_t)L;
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc_t(gy + r0);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc_t(x + r0);
+    const int klim = min(STEP, B - bs);
+#pragma unroll
+    for (int i = 0; i < kNpt; ++i) {
+      const uint32_t o = ek[i] < klim ? eoff[i] : kOob;
+      st[0][i] = buf_load_chunk<LOAD_CPOL>(rg, o);
+      st[1][i] = buf_load_chunk<LOAD_CPOL>(rx, o);
+    }
+  };
+  auto store_stage = [&](int buf, const u32x4 (&st)[2][kNpt]) {
+    uint16_t* base = l16 + buf * 2 * TSZ;
+#pragma unroll
+    for (int i = 0; i < kNpt; ++i) {
+      if (ek[i] < STEP) {
+        *reinterpret_cast<u32x4*>(base + elds[i]) = st[0][i];
+        *reinterpret_cast<u32x4*>(base + TSZ + elds[i]) = st[1][i];
+      }
+    }
+  };
+
+  f32x4 acc[CPW][NT][NT];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c)
 #pragma unroll
     for (int a = 0; a < NT; ++a)
 #pragma unroll
-      for (int b = 0; b < NT; ++b)
+      for (int b = 0; b < NT; ++b) acc[c][a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Lane addresses of the operand gathers: sample kq of the step, column
+  // 16 tt + (lane % 16) of channel c clamped to L - 1. Rows and columns at
+  // or past L of D_c are never read by the epilogue, so the clamped values
+  // need no masking.
+  const int kq = lane >> 4;
+  const int col = lane & 15;
+  const uint16_t* lrow = l16 + wave * REGION + kq * ROW;
+  int aoff[CPW][NT];
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          dt[(16 * a + rq + rr) * G::dstride + 16 * b + cl] = acc[c][a][b][rr];
-    wave_lds_sync();
-    const int hl = wave * CPW + c;  // channel within the group
-    if (lane < K) {
-      const int j = lane;
-      const int m = j - (K >> 1);
-      const int t0 = max(0, -m);
-      const int t1 = min(L, L - m);
-      float v4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c = 0; c < CPW; ++c)
 #pragma unroll
-      for (int t = 0; t < G::dim; ++t) {
-        // D_c[t][t + m] = dt[m + t * (dstride + 1)]; masked terms read a
-        // clamped in-tile address (a tap may have no valid t at all).
-        int idx = m + t * (G::dstride + 1);
-        idx = idx < 0 ? 0 : (idx < G::dim * G::dstride ? idx : G::dim * G::dstride - 1);
-        const float d = dt[idx];
-        v4[t & 3] += (t >= t0 && t < t1) ? d : 0.0f;
+    for (int tt = 0; tt < NT; ++tt) {
+      const int cc = 16 * tt + col;
+      aoff[c][tt] = c * L + (cc < L ? cc : L - 1);
+    }
+  auto mfma_step = [&](int buf) {
+    const uint16_t* gdy = lrow + buf * 2 * TSZ;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      s16x4 av[NT], bv[NT];
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) {
+        const uint16_t* p = gdy + aoff[c][tt];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          av[tt][v] = (short)p[4 * v * ROW];
+          bv[tt][v] = (short)p[TSZ + 4 * v * ROW];
+        }
       }
-      const float v = (v4[0] + v4[1]) + (v4[2] + v4[3]);
-      if (det) {
-        dst[((size_t)(g * hc + hl) * K + j) * (size_t)nranges + r] = v;
-      } else {
-        taps[hl * K + j] = v;
+#pragma unroll
+      for (int a = 0; a < NT; ++a)
+#pragma unroll
+        for (int b = 0; b < NT; ++b)
+          acc[c][a][b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av[a], bv[b],
+                                                                   acc[c][a][b], 0, 0, 0);
+    }
+  };
+
+  if (nsteps > 0) {
+    // Local step s is loaded into stg, stored to LDS stage s % 2 while step
+    // s - 1 is consumed from the other stage, and consumed after the next
+    // barrier; the loop is unrolled by 2 so the stage index is static.
+    load_step(0, stg);
+    store_stage(0, stg);
+    if (1 < nsteps) load_step(1, stg);
+    __syncthreads();
+    for (int s0 = 0; s0 < nsteps; s0 += 2) {
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const int s = s0 + d;
+        if (s < nsteps) {
+          mfma_step(d);
+          if (s + 1 < nsteps) {
+            store_stage(d ^ 1, stg);
+            if (s + 2 < nsteps) load_step(s + 2, stg);
+          }
+          __syncthreads();
+        }
       }
     }
-    wave_lds_sync();
   }
-  if (!det) {
-    __syncthreads();
-    float* out = dst + (size_t)g * hc * K;
-    for (int e = threadIdx.x; e < hc * K; e += nthreads) atomicAdd(out + e, taps[e]);
-  }
+
+  dk_cg_epilogue<LMAX>(acc, lds, dst, wave, wpb, g, r, hc, L, K, nranges, det);
 }
 
 }  // namespace pt

@@ -41,10 +41,10 @@ extern const RowsCgFn kRowsCgTable[2][3];
 // BF16 I/O (uint16_t bit patterns; FP32 taps, FP32 accumulation)
 using RowsCgBf16Fn = void (*)(const uint16_t*, const float*, uint16_t*, int,
                               int, int, int, int, uint32_t);
-using DkCgBf16Fn = void (*)(const uint16_t*, const uint16_t*, float*, int, int,
+using DkBf16Fn = void (*)(const uint16_t*, const uint16_t*, float*, int, int,
                             int, int, int, uint32_t, int);
 extern const RowsCgBf16Fn kRowsCgTableBf16[2][3];
-extern const DkCgBf16Fn kDkCgTableBf16[3];
-extern const DkCgBf16Fn kDkCgTableBf16NT[3];
+extern const DkBf16Fn kDkBf16mmaTable[3];
+extern const DkBf16Fn kDkBf16mmaTableNT[3];
 
 }  // namespace pt

@@ -1,5 +1,5 @@
-// Instantiates the BF16-I/O kernels (FWD / DX on the BF16 matrix cores, DK
-// on the channel-group kernel).
+// Instantiates the BF16-I/O kernels (FWD / DX and DK on the BF16 matrix
+// cores).
 #include "dwconv1d_kernels.hpp"
 #include "dwconv1d_tables.hpp"
 
@@ -12,10 +12,11 @@ const RowsCgBf16Fn kRowsCgTableBf16[2][3] = {
     {&dwconv_rows_bf16mma_kernel<16, true, kRowsCgWaves>,
      &dwconv_rows_bf16mma_kernel<32, true, kRowsCgWaves>,
      &dwconv_rows_bf16mma_kernel<48, true, kRowsCgWaves>}};
-const DkCgBf16Fn kDkCgTableBf16[3] = {&dwconv_dk_cg_kernel<16, kCpolNone, uint16_t>,
-                                      &dwconv_dk_cg_kernel<32, kCpolNone, uint16_t>,
-                                      &dwconv_dk_cg_kernel<48, kCpolNone, uint16_t>};
-const DkCgBf16Fn kDkCgTableBf16NT[3] = {&dwconv_dk_cg_kernel<16, kCpolNT, uint16_t>,
-                                        &dwconv_dk_cg_kernel<32, kCpolNT, uint16_t>,
-                                        &dwconv_dk_cg_kernel<48, kCpolNT, uint16_t>};
+// DK on the BF16 matrix cores: plain and non-temporal loads
+const DkBf16Fn kDkBf16mmaTable[3] = {&dwconv_dk_bf16mma_kernel<16, kCpolNone>,
+                                       &dwconv_dk_bf16mma_kernel<32, kCpolNone>,
+                                       &dwconv_dk_bf16mma_kernel<48, kCpolNone>};
+const DkBf16Fn kDkBf16mmaTableNT[3] = {&dwconv_dk_bf16mma_kernel<16, kCpolNT>,
+                                         &dwconv_dk_bf16mma_kernel<32, kCpolNT>,
+                                         &dwconv_dk_bf16mma_kernel<48, kCpolNT>};
 }  // namespace pt

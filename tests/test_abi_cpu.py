@@ -140,12 +140,38 @@ def test_bf16_argument_validation_before_launch(lib):
     assert dk(pa, pb, pc, 2, 24, 16, 5, 768, 0, S) == _lib.PT_ERR_CONFIG  # > 8 waves
     assert dk(pa, pb, None, 2, 8, 16, 5, 128, 0, S) == _lib.PT_ERR_NULL
     assert dk(mis, pb, pc, 2, 8, 16, 5, 128, 0, S) == _lib.PT_ERR_ALIGN
-    out = ctypes.c_size_t(0)
-    st = lib.pt_dwconv1d_dk_det_bf16_workspace_bytes(16384, 128, 48, 48, 128, ctypes.byref(out))
-    # BF16 tensors of 192 MiB (below the 256 MiB MALL rule), steps of
-    # 4 x 128 x 48 x 2 bytes = 48 KiB: the power of two nearest 2.5 MiB, 64
-    assert st == _lib.PT_OK and out.value == 128 * 48 * 64 * 4
     assert lib.pt_dwconv1d_dk_det_bf16(pa, pb, pc, None, 0, 2, 8, 16, 5, 128, S) == _lib.PT_ERR_WORKSPACE
+
+
+def test_bf16_workspace_bytes(lib):
+    """BF16 DK partials: [H, K, ranges] floats, one range per 16-sample step
+    at most; the range count is, of 2^k and 3 * 2^(k-1) in [8, 256], the one
+    nearest by ratio to 3 MiB / (16 * 2 * H * L bytes) (ties to the smaller),
+    at every tensor size; independent of the block size."""
+    from pathtile_amd import _lib
+
+    out = ctypes.c_size_t(0)
+    cands = sorted({c for k in range(3, 9) for c in (2**k, 3 * 2**(k - 1)) if 8 <= c <= 256})
+
+    def ranges(B, H, L):
+        want = 3 * 2**20 / (32 * H * L)
+        n = min(cands, key=lambda c: (abs(math.log(c / want)), c))
+        return max(1, min(n, -(-B // 16)))
+
+    for (B, H, L, K) in [(16384, 128, 48, 48), (32768, 256, 48, 4), (4096, 128, 24, 48),
+                         (2048, 64, 24, 48), (16384, 64, 16, 3), (40, 8, 16, 5), (1, 8, 4, 3)]:
+        for threads in (64, 128, 256, 512):
+            if H % (2 * threads // 64):
+                continue
+            st = lib.pt_dwconv1d_dk_det_bf16_workspace_bytes(B, H, L, K, threads, ctypes.byref(out))
+            assert st == _lib.PT_OK
+            assert out.value == H * K * ranges(B, H, L) * 4, (B, H, L, threads)
+    # P in BF16: 192 KiB steps, 3 MiB / 192 KiB = 16 ranges
+    lib.pt_dwconv1d_dk_det_bf16_workspace_bytes(16384, 128, 48, 48, 128, ctypes.byref(out))
+    assert out.value == 128 * 48 * 16 * 4
+    # B = 40: three 16-sample steps, so three ranges
+    lib.pt_dwconv1d_dk_det_bf16_workspace_bytes(40, 8, 16, 5, 128, ctypes.byref(out))
+    assert out.value == 8 * 5 * 3 * 4
 
 
 def test_workspace_bytes(lib):
