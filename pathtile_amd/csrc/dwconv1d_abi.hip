@@ -555,21 +555,27 @@ static int dk_path(bool det, const float* gy, const float* x, float* dst,
 // FP32, and BF16 outputs are rounded to nearest-even. Layout: 4-value
 // aligned row offsets (L % 4 == 0), 16-byte aligned tensors, H % 8 == 0
 // (FWD / DX) or H % (2 * waves) == 0 with at most 8 waves (DK).
+// BF16 FWD / DX: 16-channel workgroups where H % 16 == 0, else 8-channel
+// ones; one pass of resident workgroups over the GPU (at most 2 per CU of
+// 16 channels, 3 of 8). Measured on MI355X against 4 / 8 / 16 channels and
+// 0.25x - 4x that many sample ranges: within 3% of the best at every shape
+// tried (P, S, L = 16 / 24 / 32 / 40), and 8-16% faster than 8-channel
+// groups at P, S, L = 40 and L = 16.
 static int bf16_rows_path(bool dx, const void* in, const float* w, void* out,
                           int B, int H, int L, int K, void* stream) {
   int st = check_shape(B, H, L, K);
   if (st != PT_OK) return st;
-  if (L % 4 != 0 || H % kRowsCgWaves != 0) return PT_ERR_CONFIG;
-  const size_t lds = rows_bf16mma_lds_bytes(L, kRowsCgWaves);
+  if (L % 4 != 0 || H % 8 != 0) return PT_ERR_CONFIG;
+  const bool wide = H % 16 == 0;
+  const int hc = wide ? 16 : 8;
+  const size_t lds = rows_bf16mma_lds_bytes(L, hc);
   if (lds > (size_t)max_lds_per_block()) return PT_ERR_CONFIG;
   if (B == 0 || H == 0) return PT_OK;
   if (!in || !w || !out) return PT_ERR_NULL;
   if (!aligned(in, 16) || !aligned(out, 16) || !aligned(w, 4)) return PT_ERR_ALIGN;
-  // up to three workgroups per CU where the LDS allows (two at L = 48):
-  // measured best on MI355X at L = 16, 32 and 48
-  return rows_cg_launch(kRowsCgTableBf16[dx ? 1 : 0][mfma_index(L)],
+  return rows_cg_launch(kRowsCgTableBf16[dx ? 1 : 0][wide ? 1 : 0][mfma_index(L)],
                         (const uint16_t*)in, w, (uint16_t*)out, B, H, L, K,
-                        stream, kRowsCgWaves, lds, 3);
+                        stream, hc, lds, wide ? 2 : 3);
 }
 
 static int bf16_dk_check(int B, int H, int L, int K, int threads) {

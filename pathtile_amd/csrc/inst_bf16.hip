@@ -4,14 +4,20 @@
 #include "dwconv1d_tables.hpp"
 
 namespace pt {
-// FWD / DX on the BF16 matrix cores, 8-channel groups
-const RowsCgBf16Fn kRowsCgTableBf16[2][3] = {
-    {&dwconv_rows_bf16mma_kernel<16, false, kRowsCgWaves>,
-     &dwconv_rows_bf16mma_kernel<32, false, kRowsCgWaves>,
-     &dwconv_rows_bf16mma_kernel<48, false, kRowsCgWaves>},
-    {&dwconv_rows_bf16mma_kernel<16, true, kRowsCgWaves>,
-     &dwconv_rows_bf16mma_kernel<32, true, kRowsCgWaves>,
-     &dwconv_rows_bf16mma_kernel<48, true, kRowsCgWaves>}};
+// FWD / DX on the BF16 matrix cores: [dx][16-channel groups][row bucket]
+const RowsCgBf16Fn kRowsCgTableBf16[2][2][3] = {
+    {{&dwconv_rows_bf16mma_kernel<16, false, 8>,
+      &dwconv_rows_bf16mma_kernel<32, false, 8>,
+      &dwconv_rows_bf16mma_kernel<48, false, 8>},
+     {&dwconv_rows_bf16mma_kernel<16, false, 16>,
+      &dwconv_rows_bf16mma_kernel<32, false, 16>,
+      &dwconv_rows_bf16mma_kernel<48, false, 16>}},
+    {{&dwconv_rows_bf16mma_kernel<16, true, 8>,
+      &dwconv_rows_bf16mma_kernel<32, true, 8>,
+      &dwconv_rows_bf16mma_kernel<48, true, 8>},
+     {&dwconv_rows_bf16mma_kernel<16, true, 16>,
+      &dwconv_rows_bf16mma_kernel<32, true, 16>,
+      &dwconv_rows_bf16mma_kernel<48, true, 16>}}};
 // DK on the BF16 matrix cores: plain and non-temporal loads
 const DkBf16Fn kDkBf16mmaTable[3] = {&dwconv_dk_bf16mma_kernel<16, kCpolNone>,
                                        &dwconv_dk_bf16mma_kernel<32, kCpolNone>,
