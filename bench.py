@@ -423,6 +423,32 @@ def main(argv=None) -> int:
         raise SystemExit(f"BF16 gate failed: {bf16_gate}")
     del xb, dyb, yb, dxb, y32
 
+    # Channels-last dK through the Flash-DWC bridge ABI (flash_dk_fp32): x and
+    # dY permuted to [B, 1, L, H] outside the timed region, dw [1, K, H]
+    # accumulated into, same loop; GZ = 1 (B % 16 == 0 and H % 32 == 0 are the
+    # bridge's own rules, so other shapes skip the leg). Gate: the row-major
+    # deterministic dK of the same data.
+    cl_leg = None
+    if B % 16 == 0 and H % 32 == 0:
+        xc = x.permute(0, 2, 1).unsqueeze(1).contiguous()
+        dyc = dy.permute(0, 2, 1).unsqueeze(1).contiguous()
+        dwc = torch.zeros(1, K, H, device=dev)
+        cl_ms = time_loop(lambda: rt.launch_bwd_weight_channels_last(xc, dyc, dwc, 1))
+        rt.launch_bwd_weight_deterministic(dy, x, gk, K)
+        rt.launch_bwd_weight_channels_last(xc, dyc, dwc, 1, zero_first=True)
+        torch.cuda.synchronize()
+        cl_gate = float((dwc[0].T - gk).abs().max() / gk.abs().max().clamp_min(1e-30))
+        if not cl_gate < 1e-5:
+            raise SystemExit(f"channels-last dK gate failed: {cl_gate}")
+        cl_gbps = runtime.algorithmic_bandwidth_gbps(runtime.minimum_algorithmic_bytes(B, H, L, K), cl_ms)
+        cl_leg = {"ms": round(cl_ms, 5), "gbps": round(cl_gbps, 1),
+                  "pct_peak": round(100 * cl_gbps / PEAK_HBM_GBPS, 2),
+                  "kernel": f"dwconv_dk_cl_kernel<{16 * ((L + 15) // 16)}>",
+                  "gate_vs_row_major": float(f"{cl_gate:.3e}"),
+                  "note": "flash_dk_fp32 (x, dY [B,1,L,H]; dw [1,K,H] accumulated), GZ=1; "
+                          "algorithmic bytes as the row-major dK"}
+        del xc, dyc, dwc
+
     # The VALU rows kernel (the reference's lane-per-row structure, bit-exact
     # with its fmaf chain) timed beside the default FWD/DX kernel, same loops.
     prev = os.environ.get("PATHTILE_ROWS_ALGO")
@@ -521,6 +547,7 @@ def main(argv=None) -> int:
             "note": "x, dY, y, dX bfloat16; taps and dK FP32; FP32 accumulation; "
                     "algorithmic bytes (2 B H L * 2 + H K * 4) per path",
         },
+        "channels_last_dk": cl_leg,
         "rows_valu": {
             ph: {"ms": round(ms, 5), "pct_peak": round(100 * runtime.algorithmic_bandwidth_gbps(nbytes, ms)
                                                      / PEAK_HBM_GBPS, 2),

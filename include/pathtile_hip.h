@@ -155,6 +155,22 @@ int pt_dwconv1d_dk_det_bf16(const void* dy, const void* x, float* dk,
                             void* stream);
 
 /*
+ * Channels-last DK with the C ABI of the Flash-DWC dW bridge the reference
+ * binds through ctypes (benchmark/flashdwc_fp32_bridge.cu:6-34; called from
+ * benchmark/check_dk_fp64_comparison.py:16-65). x and dy are [B, 1, L, H]
+ * FP32, dw is [1, K, H]:
+ *   dw[j][h] += sum_b sum_t dy[b][t][h] * x[b][t + j - K/2][h]
+ * (x zero outside [0, L)); the caller zeroes dw first. Returns 0, or -2 for
+ * the arguments the bridge rejects (NULL pointers; B, H, L, K or GZ <= 0;
+ * H % 32 != 0; B % GZ != 0; (B / GZ) % 16 != 0) and for the ones this
+ * library does not serve (L or K above 48; x or dy not 16-byte aligned, dw
+ * not 4-byte aligned), or PT_ERR_HIP. GZ, the bridge's batch split, is
+ * validated as the bridge does and otherwise ignored.
+ */
+int flash_dk_fp32(const float* x, const float* dy, float* dw, int B, int H,
+                  int L, int K, int GZ, void* stream);
+
+/*
  * Compiled resources of the kernel that serves (L, K) for `kernel_id`
  * (PT_KERNEL_*), as hipFuncGetAttributes reports them on the current device:
  * registers per lane, static LDS bytes, scratch (private) bytes per lane and

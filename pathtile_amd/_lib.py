@@ -55,6 +55,7 @@ SIGNATURES = {
     "pt_dwconv1d_dk_det_bf16": (
         _i, [_vp, _vp, _vp, _vp, ctypes.c_size_t, _i, _i, _i, _i, _i, _vp]
     ),
+    "flash_dk_fp32": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "pt_kernel_attributes": (_i, [_i, _i, _i, _ip, _ip, _ip, _ip]),
     "pt_dynamic_lds_bytes": (_i, [_i, _i, _i, _i, _ip]),
 }

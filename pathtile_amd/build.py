@@ -31,6 +31,7 @@ SOURCES = [
     "inst_dk_mfma.hip",
     "inst_rows_mfma.hip",
     "inst_bf16.hip",
+    "inst_dk_cl.hip",
 ]
 INCLUDE = ROOT / "include"
 BUILD_DIR = PKG / "_build"

@@ -612,6 +612,29 @@ static int bf16_dk_launch(bool det, const void* gy, const void* x, float* dst,
   return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream, args);
 }
 
+// Channels-last DK: 32-channel workgroups of 16 waves, one resident pass of
+// them over the GPU (the sample ranges are the resident workgroups per
+// channel group), at most one range per 4-sample step.
+static int dk_cl_launch(const float* x, const float* dy, float* dw, int B,
+                        int H, int L, int K, void* stream) {
+  const DkClFn fn = kDkClTable[mfma_index(L)];
+  const size_t lds = dk_cl_lds_bytes(16 * (mfma_index(L) + 1), L);
+  if (lds > (size_t)max_lds_per_block()) return PT_ERR_CONFIG;
+  const int threads = kClWaves * kWave;
+  const long long ngroups = (long long)H / kClChannels;
+  const long long tsteps = ((long long)B + kCgStep - 1) / kCgStep;
+  const long long slots = (long long)num_cus() * blocks_per_cu((const void*)fn, threads, lds);
+  long long nr = (slots + ngroups - 1) / ngroups;
+  if (nr > tsteps) nr = tsteps;
+  if (nr < 1) nr = 1;
+  const long long nb = ngroups * nr;
+  if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
+  int nranges = (int)nr;
+  uint32_t nblocks = (uint32_t)nb;
+  void* args[] = {&x, &dy, &dw, &B, &H, &L, &K, &nranges, &nblocks};
+  return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream, args);
+}
+
 static const void* kernel_for(int kernel_id, int L, int K) {
   if (L < 1 || L > kMaxL || K < 1 || K > kMaxK) return nullptr;
   const int li = lbucket_index(L), ki = kbucket_index(K);
@@ -863,6 +886,26 @@ int pt_dwconv1d_dk_det_bf16(const void* dy, const void* x, float* dk,
   const uint32_t grid = (uint32_t)((ncoef + 3) / 4);
   return pt::launch((const void*)&pt::dk_reduce_kernel, grid, 256, 0, stream,
                     args);
+}
+
+// The Flash-DWC dW bridge's C ABI (benchmark/flashdwc_fp32_bridge.cu:6-34):
+// x and dy are [B, 1, L, H] FP32, dw is [1, K, H] and is accumulated into
+// (the caller zeroes it). Returns 0, or -2 for the arguments the bridge
+// rejects (NULL pointers; B, H, L, K, GZ <= 0; H % 32 != 0; B % GZ != 0;
+// (B / GZ) % 16 != 0) and for the ones this library does not serve (L or K
+// above 48, x or dy not 16-byte aligned, dw not 4-byte aligned), or
+// PT_ERR_HIP if the launch fails. GZ, the bridge's batch split, changes
+// nothing here: the kernel chooses its own sample ranges.
+int flash_dk_fp32(const float* x, const float* dy, float* dw, int B, int H,
+                  int L, int K, int GZ, void* stream) {
+  if (!x || !dy || !dw || B <= 0 || H <= 0 || H % 32 != 0 || L <= 0 ||
+      K <= 0 || GZ <= 0 || B % GZ != 0 || (B / GZ) % 16 != 0)
+    return PT_ERR_SHAPE;
+  if (pt::check_shape(B, H, L, K) != PT_OK) return PT_ERR_SHAPE;
+  if (!pt::aligned(x, 16) || !pt::aligned(dy, 16) || !pt::aligned(dw, 4))
+    return PT_ERR_SHAPE;
+  const int st = pt::dk_cl_launch(x, dy, dw, B, H, L, K, stream);
+  return st == PT_ERR_HIP ? PT_ERR_HIP : (st == PT_OK ? PT_OK : PT_ERR_SHAPE);
 }
 
 }  // extern "C"

@@ -1249,12 +1249,13 @@ __host__ __device__ constexpr size_t cg_lds_bytes(int lmax, int wpb, int L) {
 // of dk: they are collected in LDS and added with one coalesced atomic per
 // element (a few cache lines per workgroup, not one line operation per wave
 // and channel, which contended badly at small K). det: write the sums as
-// partials [h][j][nranges] instead.
-template <int LMAX>
+// partials [h][j][nranges] instead. CL: dk is [K][H] (the channels-last
+// layout's dw), whose hc channels of one tap are contiguous; atomics only.
+template <int LMAX, bool CL = false>
 __device__ __forceinline__ void dk_cg_epilogue(
     const f32x4 (&acc)[kCgChannelsPerWave][LMAX / 16][LMAX / 16], float* lds,
     float* __restrict__ dst, int wave, int wpb, int g, int r, int hc, int L,
-    int K, int nranges, int det) {
+    int K, int nranges, int det, int H = 0) {
   using G = CgGeo<LMAX>;
   constexpr int NT = G::nt;
   constexpr int CPW = kCgChannelsPerWave;
@@ -1301,8 +1302,15 @@ __device__ __forceinline__ void dk_cg_epilogue(
   }
   if (!det) {
     __syncthreads();
-    float* out = dst + (size_t)g * hc * K;
-    for (int e = threadIdx.x; e < hc * K; e += nthreads) atomicAdd(out + e, taps[e]);
+    if constexpr (CL) {
+      for (int e = threadIdx.x; e < hc * K; e += nthreads) {
+        const int j = e / hc, c = e - j * hc;
+        atomicAdd(dst + (size_t)j * H + (size_t)g * hc + c, taps[c * K + j]);
+      }
+    } else {
+      float* out = dst + (size_t)g * hc * K;
+      for (int e = threadIdx.x; e < hc * K; e += nthreads) atomicAdd(out + e, taps[e]);
+    }
   }
 }
 
@@ -1638,6 +1646,178 @@ __global__ __launch_bounds__(512) void dwconv_dk_bf16mma_kernel(
   }
 
   dk_cg_epilogue<LMAX>(acc, lds, dst, wave, wpb, g, r, hc, L, K, nranges, det);
+}
+
+// ---------------------------------------------------------------------------
+// Channels-last DK: x and dy as [B][L][H] (the [B, 1, L, H] layout of the
+// Flash-DWC dW kernel), dw as [K][H], dw += the taps' sums (the caller
+// zeroes dw first).
+//
+// The channel-group contraction above with the staging transposed: a
+// workgroup owns kClChannels = 32 consecutive channels (16 waves of two),
+// so each (sample, t) row it loads is one whole 128-byte line of 32
+// channels. Rows land in LDS as [sample][t][kClChannels + 1]: a lane that
+// gathers column t of channel c reads address t * 33 + c, so the 16 columns
+// of a tile hit 16 distinct banks, and the sample stride is padded to
+// 16 (mod 32) floats so the four 16-lane groups of a wave (four samples)
+// use disjoint banks. Steps are 4 samples (the FP32 MFMA K); the epilogue
+// is the shared one with the [K][H] output.
+// ---------------------------------------------------------------------------
+constexpr int kClChannels = 32;
+constexpr int kClWaves = kClChannels / kCgChannelsPerWave;  // 16
+
+// Floats between the samples of a channels-last stage: L rows of
+// kClChannels + 1, rounded up to 16 (mod 32).
+__host__ __device__ constexpr int cl_sample_stride(int L) {
+  return L * (kClChannels + 1) + ((16 - (L * (kClChannels + 1)) % 32) % 32 + 32) % 32;
+}
+
+__host__ __device__ constexpr size_t dk_cl_lds_bytes(int lmax, int L) {
+  const size_t stages = (size_t)2 * 2 * kCgStep * (size_t)cl_sample_stride(L) * sizeof(float);
+  const size_t dtile = ((size_t)kClWaves * (16 * (lmax / 16)) * (16 * (lmax / 16) + 1) +
+                        (size_t)kClChannels * kMaxK) *
+                       sizeof(float);
+  return stages > dtile ? stages : dtile;
+}
+
+template <int LMAX>
+__global__ __launch_bounds__(kClWaves * kWave) void dwconv_dk_cl_kernel(
+    const float* __restrict__ x, const float* __restrict__ gy,
+    float* __restrict__ dw, int B, int H, int L, int K, int nranges,
+    uint32_t nblocks) {
+  using G = CgGeo<LMAX>;
+  constexpr int NT = G::nt;
+  constexpr int CPW = kCgChannelsPerWave;
+  constexpr int HC = kClChannels;
+  constexpr int RW = HC + 1;           // LDS floats per (sample, t) row
+  constexpr int CPR = HC / 4;          // 16-byte chunks per row
+  constexpr int NTH = kClWaves * kWave;
+  constexpr int kNpt = (kCgStep * LMAX * CPR + NTH - 1) / NTH;
+  extern __shared__ float lds[];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int ngroups = H / HC;
+  const uint32_t blk = xcd_remap(blockIdx.x, nblocks);
+  const int g = (int)(blk % (uint32_t)ngroups);
+  const int r = (int)(blk / (uint32_t)ngroups);
+  const int tsteps = (B + kCgStep - 1) / kCgStep;
+  const int nsteps = r < tsteps ? (tsteps - 1 - r) / nranges + 1 : 0;
+
+  const int sks = cl_sample_stride(L);   // LDS floats between samples
+  const int sz = kCgStep * sks;          // one tensor's stage
+  const int rows = L * CPR;              // chunks per sample
+  const int per = kCgStep * rows;        // chunks per stage and tensor
+  const uint32_t smp_bytes = (uint32_t)L * (uint32_t)H * 4u;
+
+  // Loop-invariant part of each staged chunk: its sample within the step,
+  // its byte offset from the step's first sample, its LDS offset.
+  int ek[kNpt];
+  uint32_t eoff[kNpt], elds[kNpt];
+#pragma unroll
+  for (int i = 0; i < kNpt; ++i) {
+    const int e = i * NTH + (int)threadIdx.x;
+    const int k = e < per ? e / rows : kCgStep;  // kCgStep: no chunk
+    const int rem = e - (e / rows) * rows;
+    const int t = rem / CPR, q = rem - (rem / CPR) * CPR;
+    ek[i] = k;
+    eoff[i] = (uint32_t)k * smp_bytes + ((uint32_t)t * (uint32_t)H + (uint32_t)(g * HC + 4 * q)) * 4u;
+    elds[i] = (uint32_t)(k * sks + t * RW + 4 * q);
+  }
+
+  u32x4 stg[2][kNpt];
+  auto load_step = [&](int s) {
+    const int bs = (r + s * nranges) * kCgStep;
+    const size_t r0 = (size_t)bs * (size_t)L * (size_t)H;
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(gy + r0);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + r0);
+    const int klim = min(kCgStep, B - bs);
+#pragma unroll
+    for (int i = 0; i < kNpt; ++i) {
+      const uint32_t o = ek[i] < klim ? eoff[i] : kOob;
+      stg[0][i] = buf_load_chunk<kCpolNT>(rg, o);
+      stg[1][i] = buf_load_chunk<kCpolNT>(rx, o);
+    }
+  };
+  auto store_stage = [&](int buf) {
+    float* base = lds + buf * 2 * sz;
+#pragma unroll
+    for (int i = 0; i < kNpt; ++i) {
+      if (ek[i] < kCgStep) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          base[elds[i] + v] = __uint_as_float(stg[0][i][v]);
+          base[sz + elds[i] + v] = __uint_as_float(stg[1][i][v]);
+        }
+      }
+    }
+  };
+
+  f32x4 acc[CPW][NT][NT];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c)
+#pragma unroll
+    for (int a = 0; a < NT; ++a)
+#pragma unroll
+      for (int b = 0; b < NT; ++b) acc[c][a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Lane offsets: sample kq of the step, column 16 tt + (lane % 16) clamped
+  // to L - 1 (rows and columns of D_c at or past L are never read by the
+  // epilogue), channel wave * CPW + c.
+  const int kq = lane >> 4;
+  const int col = lane & 15;
+  int aoff[CPW][NT];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c)
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      const int cc = 16 * tt + col;
+      aoff[c][tt] = kq * sks + (cc < L ? cc : L - 1) * RW + wave * CPW + c;
+    }
+  auto mfma_step = [&](int buf) {
+    const float* gdy = lds + buf * 2 * sz;
+    const float* gxx = gdy + sz;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      float av[NT], bv[NT];
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) {
+        av[tt] = gdy[aoff[c][tt]];
+        bv[tt] = gxx[aoff[c][tt]];
+      }
+#pragma unroll
+      for (int a = 0; a < NT; ++a)
+#pragma unroll
+        for (int b = 0; b < NT; ++b)
+          acc[c][a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a], bv[b], acc[c][a][b], 0, 0, 0);
+    }
+  };
+
+  if (nsteps > 0) {
+    // Local step s is loaded into stg, stored to LDS stage s % 2 while step
+    // s - 1 is consumed from the other stage, and consumed after the next
+    // barrier; the loop is unrolled by 2 so the stage index is static.
+    load_step(0);
+    store_stage(0);
+    if (1 < nsteps) load_step(1);
+    __syncthreads();
+    for (int s0 = 0; s0 < nsteps; s0 += 2) {
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const int s = s0 + d;
+        if (s < nsteps) {
+          mfma_step(d);
+          if (s + 1 < nsteps) {
+            store_stage(d ^ 1);
+            if (s + 2 < nsteps) load_step(s + 2);
+          }
+          __syncthreads();
+        }
+      }
+    }
+  }
+
+  dk_cg_epilogue<LMAX, true>(acc, lds, dw, wave, kClWaves, g, r, HC, L, K, nranges, 0, H);
 }
 
 }  // namespace pt

@@ -611,6 +611,38 @@ class HipWarpRuntime:
 
         (collector or KERNEL_EVENTS).launch("bwd_weight_det_bf16", launch, {"B": B, "H": H, "L": L, "K": K})
 
+    def launch_bwd_weight_channels_last(self, x: torch.Tensor, gy: torch.Tensor,
+                                        dw: torch.Tensor, gz: int = 1,
+                                        collector: KernelEventCollector | None = None,
+                                        zero_first: bool = False) -> None:
+        """Channels-last FP32 dK through the Flash-DWC bridge ABI
+        (``flash_dk_fp32``, benchmark/flashdwc_fp32_bridge.cu:6-34): x and gy
+        are [B, 1, L, H], dw is [1, K, H] and is accumulated into
+        (zero_first clears it). ``gz`` is the bridge's batch split, checked as
+        the bridge checks it (B % gz == 0, (B / gz) % 16 == 0)."""
+        self._check_open()
+        if not x.is_cuda or not gy.is_cuda or not dw.is_cuda:
+            raise ValueError("x, gy, and dw must be CUDA tensors")
+        if x.dtype != torch.float32 or gy.dtype != torch.float32 or dw.dtype != torch.float32:
+            raise ValueError("x, gy, and dw must be float32")
+        if x.ndim != 4 or x.shape[1] != 1 or gy.shape != x.shape:
+            raise ValueError("x and gy must have the same [B,1,L,H] shape")
+        if dw.ndim != 3 or dw.shape[0] != 1 or dw.shape[2] != x.shape[3]:
+            raise ValueError("dw must have shape [1,K,H]")
+        self._require_contiguous(x, gy, dw)
+        B, _, L, H = map(int, x.shape)
+        K = int(dw.shape[1])
+        if zero_first:
+            dw.zero_()
+
+        def launch() -> None:
+            with torch.cuda.device(x.device):
+                st = self._lib.flash_dk_fp32(_ptr(x), _ptr(gy), _ptr(dw), B, H, L, K, int(gz),
+                                             _stream_handle(x.device))
+            _lib.check(st, "flash_dk_fp32")
+
+        (collector or KERNEL_EVENTS).launch("bwd_weight_cl", launch, {"B": B, "H": H, "L": L, "K": K})
+
     # ------------------------------------------------------------- reporting
     def kernel_attributes(self, kernel_id: int, L: int, K: int) -> dict[str, int]:
         regs, lds, scratch, maxt = (ctypes.c_int(0) for _ in range(4))

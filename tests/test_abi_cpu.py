@@ -22,7 +22,7 @@ HEADER = ROOT / "include" / "pathtile_hip.h"
 def _declared_symbols() -> list[str]:
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(pt_[a-z0-9_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b((?:pt_|flash_dk_)[a-z0-9_]+)\s*\(", text)))
 
 
 @pytest.fixture(scope="module")
@@ -45,6 +45,7 @@ def test_header_declares_the_expected_entry_points():
         "pt_kernel_attributes",
         "pt_status_string",
         "pt_abi_version",
+        "flash_dk_fp32",
     ):
         assert name in syms
 
@@ -55,7 +56,7 @@ def test_library_exports_every_declared_symbol(lib):
     syms = _declared_symbols()
     out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)],
                          capture_output=True, text=True, check=True).stdout
-    exported = set(re.findall(r"\bT (pt_[a-z0-9_]+)", out))
+    exported = set(re.findall(r"\bT ((?:pt_|flash_dk_)[a-z0-9_]+)", out))
     assert set(syms) <= exported, set(syms) - exported
     assert set(syms) == set(_lib.SIGNATURES), set(syms) ^ set(_lib.SIGNATURES)
     for name in syms:
@@ -141,6 +142,40 @@ def test_bf16_argument_validation_before_launch(lib):
     assert dk(pa, pb, None, 2, 8, 16, 5, 128, 0, S) == _lib.PT_ERR_NULL
     assert dk(mis, pb, pc, 2, 8, 16, 5, 128, 0, S) == _lib.PT_ERR_ALIGN
     assert lib.pt_dwconv1d_dk_det_bf16(pa, pb, pc, None, 0, 2, 8, 16, 5, 128, S) == _lib.PT_ERR_WORKSPACE
+
+
+def test_flash_dk_fp32_validation_before_launch(lib):
+    """The Flash-DWC bridge ABI returns -2 for every argument the bridge
+    rejects (benchmark/flashdwc_fp32_bridge.cu:14-19) and for the ones this
+    library does not serve (L or K above 48, misaligned tensors), before any
+    device work."""
+    buf = (ctypes.c_ubyte * 4096)()
+    base = ctypes.addressof(buf)
+    al = base + (-base) % 16
+    x, dy, dw = (ctypes.c_void_p(al + o) for o in (0, 1024, 2048))
+    fn = lib.flash_dk_fp32
+    S = None
+    ok = (32, 32, 48, 48, 1)  # B, H, L, K, GZ that pass every check
+    cases = [
+        ((None, dy, dw), ok),
+        ((x, None, dw), ok),
+        ((x, dy, None), ok),
+        ((x, dy, dw), (0, 32, 48, 48, 1)),        # B <= 0
+        ((x, dy, dw), (32, 0, 48, 48, 1)),        # H <= 0
+        ((x, dy, dw), (32, 48, 48, 48, 1)),       # H % 32
+        ((x, dy, dw), (32, 32, 0, 48, 1)),        # L <= 0
+        ((x, dy, dw), (32, 32, 48, 0, 1)),        # K <= 0
+        ((x, dy, dw), (32, 32, 48, 48, 0)),       # GZ <= 0
+        ((x, dy, dw), (32, 32, 48, 48, 3)),       # B % GZ
+        ((x, dy, dw), (48, 32, 48, 48, 2)),       # (B / GZ) % 16
+        ((x, dy, dw), (32, 32, 49, 48, 1)),       # L above 48
+        ((x, dy, dw), (32, 32, 48, 49, 1)),       # K above 48
+        ((ctypes.c_void_p(al + 4), dy, dw), ok),  # x not 16-byte aligned
+        ((x, ctypes.c_void_p(al + 1032), dw), ok),
+        ((x, dy, ctypes.c_void_p(al + 2050)), ok),
+    ]
+    for ptrs, (B, H, L, K, gz) in cases:
+        assert fn(*ptrs, B, H, L, K, gz, S) == -2, (ptrs, B, H, L, K, gz)
 
 
 def test_bf16_workspace_bytes(lib):
