@@ -40,6 +40,7 @@ WORKLOADS = {
     "edge": (1000, 96, 37, 48),
 }
 PEAK_HBM_GBPS = 8000.0
+PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense FP32 matrix
 # Published aggregate of the reference for this metric (README.md:96,
 # A100 PCIe 40 GB): 11.283 ms.
 REFERENCE_AGGREGATE_MS = 11.283
@@ -449,6 +450,36 @@ def main(argv=None) -> int:
                           "algorithmic bytes as the row-major dK"}
         del xc, dyc, dwc
 
+    # Long rows at the reference's long-row benchmark shape (kernels/
+    # shared_l192.py, benchmarked at B16384 H128 L192 K192 by
+    # benchmark/benchmark_gmc_vs_shared_l192.py:14-17): FP32 on the matrix
+    # cores, bound by them rather than HBM; roofline on useful flops
+    # (2 per multiply-add that touches a real element). Same loop.
+    LB, LH, LL, LK = 16384, 128, 192, 192
+    xl = torch.randn(LB, LH, LL, generator=torch.Generator().manual_seed(args.seed + 3)).to(dev)
+    dyl = torch.randn(LB, LH, LL, generator=torch.Generator().manual_seed(args.seed + 4)).to(dev)
+    wl = (torch.randn(LH, LK, generator=torch.Generator().manual_seed(args.seed + 5)) / LK ** 0.5).to(dev)
+    yl, dxl, gkl = torch.empty_like(xl), torch.empty_like(dyl), torch.empty(LH, LK, device=dev)
+    long_loops = {
+        "fwd": lambda: rt.launch_fwd_long(xl, wl, yl),
+        "bwd_input": lambda: rt.launch_bwd_input_long(dyl, wl, dxl),
+        "bwd_weight": lambda: rt.launch_bwd_weight_long(dyl, xl, gkl, LK),
+    }
+    long_ms = {ph: time_loop(fn) for ph, fn in long_loops.items()}
+    from pathtile_amd.tune.baselines import useful_products
+    long_flops = 2 * useful_products(LB, LH, LL, LK)
+    long_leg = {
+        "config": {"B": LB, "H": LH, "L": LL, "K": LK},
+        "paths": {ph: {"ms": round(ms, 5),
+                       "tflops_useful": round(long_flops / (ms / 1e3) / 1e12, 2),
+                       "frac_fp32_mfma_peak": round(long_flops / (ms / 1e3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)}
+                  for ph, ms in long_ms.items()},
+        "fwd_dx_dk_ms": round(sum(long_ms.values()), 5),
+        "note": "pt_dwconv1d_{fwd,dx,dk}_long_f32; useful flops 2 * sum over rows of "
+                "real multiply-adds; peak = MI355X dense FP32 matrix 157.3 TFLOP/s",
+    }
+    del xl, dyl, wl, yl, dxl, gkl
+
     # The VALU rows kernel (the reference's lane-per-row structure, bit-exact
     # with its fmaf chain) timed beside the default FWD/DX kernel, same loops.
     prev = os.environ.get("PATHTILE_ROWS_ALGO")
@@ -548,6 +579,7 @@ def main(argv=None) -> int:
                     "algorithmic bytes (2 B H L * 2 + H K * 4) per path",
         },
         "channels_last_dk": cl_leg,
+        "long_rows": long_leg,
         "rows_valu": {
             ph: {"ms": round(ms, 5), "pct_peak": round(100 * runtime.algorithmic_bandwidth_gbps(nbytes, ms)
                                                      / PEAK_HBM_GBPS, 2),

@@ -155,6 +155,30 @@ int pt_dwconv1d_dk_det_bf16(const void* dy, const void* x, float* dk,
                             void* stream);
 
 /*
+ * Long rows: L up to 192 and K up to 256 (taps past the row add nothing),
+ * the regime of the
+ * reference's kernels/shared_l192.py (DepthwiseConvShared, benchmarked at
+ * L = K = 192 by benchmark/benchmark_gmc_vs_shared_l192.py:14-17), whose
+ * forward / backward call the same three paths as the specialised API:
+ *   FWD  y[b,h,t]  = sum_j w[h,j] x[b,h,t+j-K/2]      (kernels/shared_l192.py
+ *   DX   gx[b,h,s] = sum_j w[h,j] gy[b,h,s-j+K/2]      :130-626, launched at
+ *   DK   gk[h,j]   = sum_b sum_t gy[b,h,t] x[b,h,t+j-K/2]  :840-1005)
+ * FP32 on the matrix cores. FWD/DX need only 4-byte aligned tensors. DK is
+ * deterministic (fixed-order partials plus a reduction, as
+ * pt_dwconv1d_dk_det_f32) and overwrites dk; its workspace size depends on
+ * (B, H) only. B * H * L < 2^31 and 16 * H * L * 4 < 2^31 (PT_ERR_SHAPE).
+ */
+int pt_dwconv1d_fwd_long_f32(const float* x, const float* w, float* y, int B,
+                             int H, int L, int K, void* stream);
+int pt_dwconv1d_dx_long_f32(const float* dy, const float* w, float* dx, int B,
+                            int H, int L, int K, void* stream);
+int pt_dwconv1d_dk_long_workspace_bytes(int B, int H, int L, int K,
+                                        size_t* bytes);
+int pt_dwconv1d_dk_long_f32(const float* dy, const float* x, float* dk,
+                            void* workspace, size_t workspace_bytes, int B,
+                            int H, int L, int K, void* stream);
+
+/*
  * Channels-last DK with the C ABI of the Flash-DWC dW bridge the reference
  * binds through ctypes (benchmark/flashdwc_fp32_bridge.cu:6-34; called from
  * benchmark/check_dk_fp64_comparison.py:16-65). x and dy are [B, 1, L, H]

@@ -1,4 +1,5 @@
-"""CPU oracle for the depthwise Conv1D hot path (FWD, dX, dK; L, K <= 48).
+"""CPU oracle for the depthwise Conv1D hot path (FWD, dX, dK; the FP32
+reference chains for L, K <= 48, the FP64 sums for L, K <= 256).
 
 TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import this package, and only as the
@@ -37,8 +38,9 @@ _LIB_PATH = _HERE / "liboracle.so"
 _LOCK = threading.Lock()
 _LIB: ctypes.CDLL | None = None
 
-MAX_L = 48
+MAX_L = 48          # the FP32 reference chains (the reference kernels' range)
 MAX_K = 48
+MAX_LONG = 256      # the FP64 sums (same formulas, long rows)
 
 
 def build(force: bool = False) -> Path:
@@ -81,15 +83,15 @@ def _f32(a) -> np.ndarray:
     return a
 
 
-def _shape(x: np.ndarray, w: np.ndarray) -> tuple[int, int, int, int]:
+def _shape(x: np.ndarray, w: np.ndarray, limit: int = MAX_L) -> tuple[int, int, int, int]:
     if x.ndim != 3 or w.ndim != 2:
         raise ValueError("expected x[B,H,L] and w[H,K]")
     B, H, L = x.shape
     Hw, K = w.shape
     if H != Hw:
         raise ValueError("channel mismatch")
-    if L < 1 or K < 1 or L > MAX_L or K > MAX_K:
-        raise ValueError("oracle supports 1 <= L, K <= 48")
+    if L < 1 or K < 1 or L > limit or K > limit:
+        raise ValueError(f"oracle supports 1 <= L, K <= {limit}")
     return int(B), int(H), int(L), int(K)
 
 
@@ -123,7 +125,7 @@ def dx_f32_refchain(dy, w) -> np.ndarray:
 
 def fwd_f64(x, w) -> np.ndarray:
     x, w = _f32(x), _f32(w)
-    dims = _shape(x, w)
+    dims = _shape(x, w, MAX_LONG)
     y = np.empty(x.shape, dtype=np.float64)
     _call("oracle_fwd_f64", x, w, y, dims)
     return y
@@ -131,7 +133,7 @@ def fwd_f64(x, w) -> np.ndarray:
 
 def dx_f64(dy, w) -> np.ndarray:
     dy, w = _f32(dy), _f32(w)
-    dims = _shape(dy, w)
+    dims = _shape(dy, w, MAX_LONG)
     dx = np.empty(dy.shape, dtype=np.float64)
     _call("oracle_dx_f64", dy, w, dx, dims)
     return dx
@@ -144,8 +146,8 @@ def dk_f64(dy, x, K: int) -> np.ndarray:
     if dy.shape != x.shape:
         raise ValueError("dy and x must have the same [B,H,L] shape")
     B, H, L = map(int, x.shape)
-    if L < 1 or K < 1 or L > MAX_L or K > MAX_K:
-        raise ValueError("oracle supports 1 <= L, K <= 48")
+    if L < 1 or K < 1 or L > MAX_LONG or K > MAX_LONG:
+        raise ValueError(f"oracle supports 1 <= L, K <= {MAX_LONG}")
     dk = np.empty((H, K), dtype=np.float64)
     _call("oracle_dk_f64", dy, x, dk, (B, H, L, K))
     return dk

@@ -1,6 +1,9 @@
 /*
  * dwconv1d_oracle.c — CPU restatement of the reference's depthwise Conv1D
- * (FWD, dX, dK) for L, K <= 48.
+ * (FWD, dX, dK): the FP32 reference chains for L, K <= 48 (the range of the
+ * reference kernels they restate), the FP64 sums for L, K <= 256 (the same
+ * formulas, which the reference's long-row module kernels/shared_l192.py
+ * computes for L = K = 192).
  *
  * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py may load this library, and only as the
@@ -27,18 +30,25 @@
 #include <stdint.h>
 #include <string.h>
 
-#define ORACLE_MAX 48
+#define ORACLE_MAX_CHAIN 48
+#define ORACLE_MAX 256
 
 int oracle_abi_version(void) { return 1; }
 
+static int bad_limit(int B, int H, int L, int K, int lim) {
+  return B < 0 || H < 0 || L < 1 || K < 1 || L > lim || K > lim;
+}
+static int bad_chain(int B, int H, int L, int K) {
+  return bad_limit(B, H, L, K, ORACLE_MAX_CHAIN);
+}
 static int bad(int B, int H, int L, int K) {
-  return B < 0 || H < 0 || L < 1 || K < 1 || L > ORACLE_MAX || K > ORACLE_MAX;
+  return bad_limit(B, H, L, K, ORACLE_MAX);
 }
 
 /* kernels/warp_tiled_ampere.py:372-434 */
 int oracle_fwd_f32_refchain(const float* x, const float* w, float* y, int B,
                             int H, int L, int K) {
-  if (bad(B, H, L, K)) return -2;
+  if (bad_chain(B, H, L, K)) return -2;
   const int pad = K >> 1;
   const long long rows = (long long)B * H;
 #pragma omp parallel for schedule(static)
@@ -62,7 +72,7 @@ int oracle_fwd_f32_refchain(const float* x, const float* w, float* y, int B,
 /* kernels/warp_tiled_ampere.py:440-502 */
 int oracle_dx_f32_refchain(const float* dy, const float* w, float* dx, int B,
                            int H, int L, int K) {
-  if (bad(B, H, L, K)) return -2;
+  if (bad_chain(B, H, L, K)) return -2;
   const int pad = K >> 1;
   const long long rows = (long long)B * H;
 #pragma omp parallel for schedule(static)

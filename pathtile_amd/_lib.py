@@ -56,6 +56,12 @@ SIGNATURES = {
         _i, [_vp, _vp, _vp, _vp, ctypes.c_size_t, _i, _i, _i, _i, _i, _vp]
     ),
     "flash_dk_fp32": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "pt_dwconv1d_fwd_long_f32": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "pt_dwconv1d_dx_long_f32": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "pt_dwconv1d_dk_long_workspace_bytes": (_i, [_i, _i, _i, _i, _szp]),
+    "pt_dwconv1d_dk_long_f32": (
+        _i, [_vp, _vp, _vp, _vp, ctypes.c_size_t, _i, _i, _i, _i, _vp]
+    ),
     "pt_kernel_attributes": (_i, [_i, _i, _i, _ip, _ip, _ip, _ip]),
     "pt_dynamic_lds_bytes": (_i, [_i, _i, _i, _i, _ip]),
 }

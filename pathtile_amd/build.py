@@ -32,6 +32,7 @@ SOURCES = [
     "inst_rows_mfma.hip",
     "inst_bf16.hip",
     "inst_dk_cl.hip",
+    "inst_long.hip",
 ]
 INCLUDE = ROOT / "include"
 BUILD_DIR = PKG / "_build"

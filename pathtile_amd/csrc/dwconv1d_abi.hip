@@ -635,6 +635,47 @@ static int dk_cl_launch(const float* x, const float* dy, float* dw, int B,
   return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream, args);
 }
 
+// --- long rows: L up to kLongMaxL, K up to kLongMaxK -----------------------
+static int check_long_shape(int B, int H, int L, int K) {
+  if (B < 0 || H < 0 || L < 1 || K < 1 || L > kLongMaxL || K > kLongMaxK)
+    return PT_ERR_SHAPE;
+  if ((long long)B * H * L >= (1LL << 31)) return PT_ERR_SHAPE;
+  // a 16-sample tile spans < 2 GiB (buffer offsets, see kOob)
+  if ((long long)16 * H * L * 4 >= (1LL << 31)) return PT_ERR_SHAPE;
+  return PT_OK;
+}
+
+static int long_index(int L) { return (L + 63) / 64 - 1; }  // row bucket of 64
+
+static int rows_long_path(bool dx, const float* in, const float* w, float* out,
+                          int B, int H, int L, int K, void* stream) {
+  int st = check_long_shape(B, H, L, K);
+  if (st != PT_OK) return st;
+  if (B == 0 || H == 0) return PT_OK;
+  if (!in || !w || !out) return PT_ERR_NULL;
+  if (!aligned(in, 4) || !aligned(w, 4) || !aligned(out, 4)) return PT_ERR_ALIGN;
+  const int li = long_index(L);
+  const size_t lds = rows_long_lds_bytes(64 * (li + 1));
+  const long long nb = (long long)H * (((long long)B + kLongRowsWaves * 16 - 1) / (kLongRowsWaves * 16));
+  if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
+  void* args[] = {&in, &w, &out, &B, &H, &L, &K};
+  const int ki = (K + 63) / 64 - 1;  // tap bucket of 64
+  return launch((const void*)kRowsLongTable[dx ? 1 : 0][li][ki], (uint32_t)nb,
+                kLongRowsWaves * kWave, lds, stream, args);
+}
+
+// Long-row DK: one workgroup per (channel, interleaved 16-sample range); the
+// range count aims at kLongDkTarget workgroups (two per CU of MI355X) and
+// depends on the shape only, so the workspace size does too.
+constexpr long long kLongDkTarget = 512;
+
+static long long long_dk_ranges(int B, int H) {
+  long long nr = (kLongDkTarget + H - 1) / (H > 0 ? H : 1);
+  const long long tsteps = ((long long)B + 15) / 16;
+  if (nr > tsteps) nr = tsteps;
+  return nr < 1 ? 1 : nr;
+}
+
 static const void* kernel_for(int kernel_id, int L, int K) {
   if (L < 1 || L > kMaxL || K < 1 || K > kMaxK) return nullptr;
   const int li = lbucket_index(L), ki = kbucket_index(K);
@@ -886,6 +927,61 @@ int pt_dwconv1d_dk_det_bf16(const void* dy, const void* x, float* dk,
   const uint32_t grid = (uint32_t)((ncoef + 3) / 4);
   return pt::launch((const void*)&pt::dk_reduce_kernel, grid, 256, 0, stream,
                     args);
+}
+
+int pt_dwconv1d_fwd_long_f32(const float* x, const float* w, float* y, int B,
+                             int H, int L, int K, void* stream) {
+  return pt::rows_long_path(false, x, w, y, B, H, L, K, stream);
+}
+
+int pt_dwconv1d_dx_long_f32(const float* dy, const float* w, float* dx, int B,
+                            int H, int L, int K, void* stream) {
+  return pt::rows_long_path(true, dy, w, dx, B, H, L, K, stream);
+}
+
+int pt_dwconv1d_dk_long_workspace_bytes(int B, int H, int L, int K,
+                                        size_t* bytes) {
+  if (!bytes) return PT_ERR_NULL;
+  const int st = pt::check_long_shape(B, H, L, K);
+  if (st != PT_OK) return st;
+  *bytes = (B == 0 || H == 0)
+               ? 0
+               : (size_t)H * (size_t)K * (size_t)pt::long_dk_ranges(B, H) * sizeof(float);
+  return PT_OK;
+}
+
+int pt_dwconv1d_dk_long_f32(const float* dy, const float* x, float* dk,
+                            void* workspace, size_t workspace_bytes, int B,
+                            int H, int L, int K, void* stream) {
+  int st = pt::check_long_shape(B, H, L, K);
+  if (st != PT_OK) return st;
+  if (H == 0) return PT_OK;
+  if (!dk) return PT_ERR_NULL;
+  if (!pt::aligned(dk, 4)) return PT_ERR_ALIGN;
+  if (B == 0) return pt::zero_fill(dk, H * K, stream);
+  if (!dy || !x) return PT_ERR_NULL;
+  if (!pt::aligned(dy, 4) || !pt::aligned(x, 4)) return PT_ERR_ALIGN;
+  const long long nr = pt::long_dk_ranges(B, H);
+  const size_t need = (size_t)H * (size_t)K * (size_t)nr * sizeof(float);
+  if (!workspace || workspace_bytes < need) return PT_ERR_WORKSPACE;
+  if (!pt::aligned(workspace, 4)) return PT_ERR_ALIGN;
+  const long long nb = (long long)H * nr;
+  if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
+  const int li = pt::long_index(L);
+  const int lmax = 64 * (li + 1);
+  float* partials = (float*)workspace;
+  int nranges = (int)nr, det = 1;
+  void* args[] = {&dy, &x, &partials, &B, &H, &L, &K, &nranges, &det};
+  st = pt::launch((const void*)pt::kDkLongTable[li], (uint32_t)nb,
+                  (uint32_t)((lmax / 16) * pt::kWave), pt::dk_long_lds_bytes(lmax),
+                  stream, args);
+  if (st != PT_OK) return st;
+  int ncoef = H * K;
+  int nbt = nranges;
+  const float* cp = partials;
+  void* rargs[] = {&cp, &dk, &ncoef, &nbt};
+  return pt::launch((const void*)&pt::dk_reduce_kernel, (uint32_t)((ncoef + 3) / 4), 256,
+                    0, stream, rargs);
 }
 
 // The Flash-DWC dW bridge's C ABI (benchmark/flashdwc_fp32_bridge.cu:6-34):

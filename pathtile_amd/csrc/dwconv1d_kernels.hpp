@@ -1820,4 +1820,323 @@ __global__ __launch_bounds__(kClWaves * kWave) void dwconv_dk_cl_kernel(
   dk_cg_epilogue<LMAX, true>(acc, lds, dw, wave, kClWaves, g, r, HC, L, K, nranges, 0, H);
 }
 
+// ---------------------------------------------------------------------------
+// Long rows (L up to kLongMaxL = 192, K up to kLongMaxK = 256): FWD / DX on
+// the matrix cores.
+//
+// At L = K = 192 a path does B H L K / 2-ish useful multiply-adds (58 G at
+// B16384 H128) against 3.2 GB of traffic, so it is bound by the FP32 matrix
+// cores, not HBM. A wave owns one channel and 16 samples:
+// v_mfma_f32_16x16x4_f32 with M = the 16 samples, N = 16 output columns and
+// K = the 4 consecutive input columns 4u .. 4u + 3 (lane l holds A[l % 16]
+// [l / 16] = x[sample l % 16][4u + l / 16] and B[l / 16][l % 16] = the tap
+// that joins input column 4u + l / 16 to output column 16 tt + l % 16).
+// Consecutive input columns per step make the band exact: step u and tile
+// tt meet only if some (s, t) in them has a tap, a test that is the same for
+// the whole wave, so out-of-band steps are skipped, not multiplied by zero.
+// The taps sit in LDS as one zero-padded window per channel; a lane's tap
+// for (u, tt) is window[lane base +/- (4u - 16tt)], an immediate offset.
+// Every output tile accumulates at once (NT accumulators), so consecutive
+// MFMAs never wait on each other. Rows go global -> LDS (the wave's own
+// 16-row region, no block barrier), A is read per step from there, and the
+// results return through the same region to coalesced stores.
+// ---------------------------------------------------------------------------
+// floor(a / b) for b > 0 and any sign of a.
+__host__ __device__ constexpr int floor_div(int a, int b) {
+  return a >= 0 ? a / b : -((-a + b - 1) / b);
+}
+
+constexpr int kLongMaxL = 192;         // largest L of the long path
+constexpr int kLongMaxK = 256;         // largest K (taps past the row add 0)
+constexpr int kLongRowsWaves = 4;      // waves (16-sample groups) per workgroup
+constexpr int kLongTapPad = 20;        // zero taps on each side of the window
+
+// Floats per LDS row of a wave's region: 4 (mod 64), so the 16 rows a wave
+// reads at once (one per sample) start in different banks.
+__host__ __device__ constexpr int long_row_stride(int lmax) { return lmax + 4; }
+
+__host__ __device__ constexpr size_t rows_long_lds_bytes(int lmax) {
+  return ((size_t)kLongRowsWaves * 16 * long_row_stride(lmax) +
+          (size_t)(kLongMaxK + 2 * kLongTapPad)) *
+         sizeof(float);
+}
+
+// KB: tap-count bucket (K <= KB, a multiple of 64).
+template <int LMAX, int KB, bool DX>
+__global__ __launch_bounds__(kLongRowsWaves * kWave) void dwconv_rows_long_kernel(
+    const float* __restrict__ in, const float* __restrict__ w,
+    float* __restrict__ out, int B, int H, int L, int K) {
+  constexpr int NT = LMAX / 16;   // output tiles
+  constexpr int NU = LMAX / 4;    // 4-column MFMA steps
+  constexpr int RS = long_row_stride(LMAX);
+  constexpr int NC = LMAX / kWave;  // row chunks of 64 floats (LMAX % 64 == 0)
+  extern __shared__ float lds[];
+  float* const wl = lds + kLongRowsWaves * 16 * RS;  // tap window
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int h = (int)(blockIdx.x % (uint32_t)H);
+  const int b0 = (int)(blockIdx.x / (uint32_t)H) * (kLongRowsWaves * 16) + wave * 16;
+  const int p = K >> 1;
+
+  // Tap window: wl[kLongTapPad + j] = w[h][j], zero elsewhere.
+  for (int i = threadIdx.x; i < K + 2 * kLongTapPad; i += kLongRowsWaves * kWave) {
+    const int j = i - kLongTapPad;
+    wl[i] = (j >= 0 && j < K) ? w[(size_t)h * K + j] : 0.0f;
+  }
+
+  // This wave's 16 rows: columns >= L (and rows past B) are zero.
+  float* const xr = lds + wave * 16 * RS;
+  {
+    const int nrow = min(16, B - b0);
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(in + ((size_t)(b0 < B ? b0 : 0) * (size_t)H + (size_t)h) * (size_t)L);
+    const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
+    float v[16][NC];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int col = c * kWave + lane;
+        const uint32_t off = (i < nrow && col < L) ? (uint32_t)i * row_bytes + 4u * (uint32_t)col : kOob;
+        v[i][c] = buf_load1(rs, off, 0);
+      }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) xr[i * RS + c * kWave + lane] = v[i][c];
+  }
+  __syncthreads();  // taps and rows in place
+
+  const int jj = lane & 15, kk = lane >> 4;
+  // Lane's tap for step u and tile tt: FWD j = (4u + kk) - (16 tt + jj) + p,
+  // DX j = (16 tt + jj) - (4u + kk) + p. Both depend on u and tt only through
+  // the diagonal d = u - 4 tt, as does the band test, so the loop runs over
+  // diagonals: one tap per diagonal, then one MFMA per output tile with step
+  // u = d + 4 tt, a compile-time index into the lane's A values. The loop
+  // covers every diagonal a tap count up to KB can reach (compile-time
+  // bounds, no branch around any MFMA); a diagonal outside this call's band
+  // multiplies by a zero tap. d is in the band when some (u, tt) on it
+  // shares a tap:
+  //   FWD 4d + 3 >= -p and 4d - 15 <= K - 1 - p,
+  //   DX  15 - 4d >= -p and -4d - 3 <= K - 1 - p.
+  // Taps read there stay in [-18, K + 17], inside the zero-padded window
+  // (out-of-band diagonals read the band's nearest one, then select 0).
+  // Columns at or past L are zeros in the rows, so steps past the row add 0.
+  constexpr int PB = KB / 2;  // largest p of the bucket
+  constexpr int DLO = DX ? floor_div(-PB + 1, 4) : floor_div(-PB, 4);
+  constexpr int DHI = DX ? floor_div(PB + 15, 4) : floor_div(PB + 14, 4);
+  constexpr int D0 = DLO > -(NU - 4) ? DLO : -(NU - 4);
+  constexpr int D1 = DHI < NU - 1 ? DHI : NU - 1;
+  const float* const wb = wl + kLongTapPad + (DX ? (jj - kk + p) : (kk - jj + p));
+  const float* const ar = xr + jj * RS + kk;  // A: row jj, column 4u + kk
+  const int dlo = DX ? floor_div(p - K - 2 + 3, 4) : floor_div(-p - 3 + 3, 4);
+  const int dhi = DX ? floor_div(p + 15, 4) : floor_div(K + 14 - p, 4);
+  float av[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) av[u] = ar[4 * u];
+  f32x4 acc[NT];
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int d = D0; d <= D1; ++d) {
+    const int dc = d < dlo ? dlo : (d > dhi ? dhi : d);  // uniform
+    const float tap = wb[DX ? -4 * dc : 4 * dc];
+    const float bv = d == dc ? tap : 0.0f;
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      const int u = d + 4 * tt;
+      if (u >= 0 && u < NU)  // compile-time
+        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], bv, acc[tt], 0, 0, 0);
+    }
+  }
+
+  // Results back through this wave's region (its A reads are complete: LDS
+  // operations of one wave run in order), then coalesced stores.
+  const int rq = 4 * kk;
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) xr[(rq + r) * RS + 16 * tt + jj] = acc[tt][r];
+  wave_lds_sync();
+  {
+    const int nrow = min(16, B - b0);
+    const __amdgpu_buffer_rsrc_t ro =
+        make_rsrc(out + ((size_t)(b0 < B ? b0 : 0) * (size_t)H + (size_t)h) * (size_t)L);
+    const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int col = c * kWave + lane;
+        const uint32_t off = (i < nrow && col < L) ? (uint32_t)i * row_bytes + 4u * (uint32_t)col : kOob;
+        buf_store1(xr[i * RS + col], ro, off);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Long rows: DK on the matrix cores. For channel h, D[t][s] = sum_b
+// dy[b,h,t] x[b,h,s] over the batch, then dk[h][j] = sum_t D[t][t + j - p].
+// A workgroup owns one channel and the interleaved 16-sample steps r,
+// r + nranges, ... of the batch; its NT = LMAX / 16 waves own one tile row
+// of D each (t in [16a, 16a + 16)) and accumulate the tiles of that row that
+// meet the band (v_mfma_f32_16x16x4_f32, K = 4 samples: lane l holds
+// A[l % 16][l / 16] = dy[sample l / 16][16a + l % 16] and B[l / 16][l % 16] =
+// x[sample l / 16][16 bb + l % 16]). Both tensors' 16 rows of a step are
+// staged in LDS, double buffered, loaded a step ahead into registers; the
+// stage rows are 16 (mod 64) floats apart so the four samples a wave reads
+// at once sit in disjoint banks.
+// Epilogue, in a fixed order: the waves' D rows go through the stage area
+// four at a time; wave a sums its 16 rows' diagonals into part[a][j], and
+// the workgroup adds part[0 .. NT)[j] in order. det: one partial per
+// (h, j, range) for dk_reduce_kernel; otherwise one atomic per tap and
+// workgroup.
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr int long_dk_row_stride(int lmax) { return lmax + 16; }
+
+__host__ __device__ constexpr size_t dk_long_lds_bytes(int lmax) {
+  return ((size_t)2 * 2 * 16 * long_dk_row_stride(lmax) + (size_t)(lmax / 16) * kLongMaxK) *
+         sizeof(float);
+}
+
+template <int LMAX>
+__global__ __launch_bounds__((LMAX / 16) * kWave) void dwconv_dk_long_kernel(
+    const float* __restrict__ gy, const float* __restrict__ x,
+    float* __restrict__ dst, int B, int H, int L, int K, int nranges, int det) {
+  constexpr int NT = LMAX / 16;
+  constexpr int NTH = NT * kWave;
+  constexpr int RS = long_dk_row_stride(LMAX);
+  constexpr int SZ = 16 * RS;                 // one tensor's stage
+  constexpr int kNpt = 16 * LMAX / NTH;       // dwords per thread and tensor
+  constexpr int DS = LMAX + 1;                // epilogue D-row stride
+  constexpr int kRound = (4 * SZ) / (16 * DS);  // waves per epilogue round
+  static_assert(16 * LMAX % NTH == 0, "whole rows per thread slice");
+  static_assert(kRound >= 1, "stage area holds one wave's D rows");
+  extern __shared__ float lds[];
+  float* const part = lds + 4 * SZ;           // [NT][kLongMaxK]
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int a = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // tile row
+  const int h = (int)(blockIdx.x % (uint32_t)H);
+  const int r = (int)(blockIdx.x / (uint32_t)H);
+  const int tsteps = (B + 15) / 16;
+  const int nsteps = r < tsteps ? (tsteps - 1 - r) / nranges + 1 : 0;
+  const int p = K >> 1;
+  const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
+
+  // Loop-invariant part of each staged dword: sample row, column, LDS slot.
+  int erow[kNpt], ecol[kNpt];
+#pragma unroll
+  for (int i = 0; i < kNpt; ++i) {
+    const int e = i * NTH + (int)threadIdx.x;
+    erow[i] = e / LMAX;
+    ecol[i] = e - (e / LMAX) * LMAX;
+  }
+  float stg[2][kNpt];
+  auto load_step = [&](int s) {
+    const int bs = (r + s * nranges) * 16;
+    const size_t r0 = ((size_t)bs * (size_t)H + (size_t)h) * (size_t)L;
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(gy + r0);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + r0);
+    const int klim = min(16, B - bs);
+#pragma unroll
+    for (int i = 0; i < kNpt; ++i) {
+      const uint32_t o = (erow[i] < klim && ecol[i] < L)
+                             ? (uint32_t)erow[i] * row_bytes + 4u * (uint32_t)ecol[i]
+                             : kOob;
+      stg[0][i] = buf_load1<kCpolNT>(rg, o, 0);
+      stg[1][i] = buf_load1<kCpolNT>(rx, o, 0);
+    }
+  };
+  auto store_stage = [&](int buf) {
+    float* base = lds + buf * 2 * SZ;
+#pragma unroll
+    for (int i = 0; i < kNpt; ++i) {
+      base[erow[i] * RS + ecol[i]] = stg[0][i];
+      base[SZ + erow[i] * RS + ecol[i]] = stg[1][i];
+    }
+  };
+
+  // Tiles of row a that meet the band: s - t in 16 (bb - a) + [-15, 15]
+  // against [-p, K - 1 - p] (the same for the whole wave).
+  auto in_band = [&](int bb) {
+    const int lo = 16 * (bb - a) - 15;
+    return lo + 30 >= -p && lo <= K - 1 - p && 16 * bb < L && 16 * a < L;
+  };
+  f32x4 acc[NT];
+#pragma unroll
+  for (int bb = 0; bb < NT; ++bb) acc[bb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int kq = lane >> 4, col = lane & 15;
+  auto mfma_step = [&](int buf) {
+    const float* dyst = lds + buf * 2 * SZ;
+    const float* xst = dyst + SZ;
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) {
+      const int row = (4 * k4 + kq) * RS;
+      const float av = dyst[row + 16 * a + col];
+#pragma unroll
+      for (int bb = 0; bb < NT; ++bb)
+        if (in_band(bb))
+          acc[bb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, xst[row + 16 * bb + col], acc[bb], 0, 0, 0);
+    }
+  };
+
+  if (nsteps > 0) {
+    load_step(0);
+    store_stage(0);
+    if (1 < nsteps) load_step(1);
+    __syncthreads();
+    for (int s0 = 0; s0 < nsteps; s0 += 2) {
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const int s = s0 + d;
+        if (s < nsteps) {
+          mfma_step(d);
+          if (s + 1 < nsteps) {
+            store_stage(d ^ 1);
+            if (s + 2 < nsteps) load_step(s + 2);
+          }
+          __syncthreads();
+        }
+      }
+    }
+  }
+
+  // Epilogue rounds: waves [q, q + kRound) put their D rows in the stage
+  // area (slot a - q), then sum their diagonals in order of t.
+  for (int q = 0; q < NT; q += kRound) {
+    const bool mine = a >= q && a < q + kRound;
+    float* const blk = lds + (mine ? a - q : 0) * 16 * DS;
+    if (mine) {
+#pragma unroll
+      for (int bb = 0; bb < NT; ++bb)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) blk[(4 * kq + rr) * DS + 16 * bb + col] = acc[bb][rr];
+    }
+    __syncthreads();
+    if (mine) {
+      for (int jb = 0; jb < K; jb += kWave) {
+        const int j = jb + lane;
+        float v = 0.0f;
+        for (int tr = 0; tr < 16; ++tr) {
+          const int t = 16 * a + tr;
+          const int sc = t + j - p;
+          if (j < K && t < L && sc >= 0 && sc < L) v += blk[tr * DS + sc];
+        }
+        if (j < K) part[a * kLongMaxK + j] = v;
+      }
+    }
+    __syncthreads();
+  }
+  for (int j = threadIdx.x; j < K; j += NTH) {
+    float v = 0.0f;
+    for (int aa = 0; aa < NT; ++aa) v += part[aa * kLongMaxK + j];
+    if (det)
+      dst[((size_t)h * K + j) * (size_t)nranges + r] = v;
+    else
+      atomicAdd(dst + (size_t)h * K + j, v);
+  }
+}
+
 }  // namespace pt

@@ -47,6 +47,10 @@ extern const RowsCgBf16Fn kRowsCgTableBf16[2][2][3];
 using DkClFn = void (*)(const float*, const float*, float*, int, int, int, int,
                        int, uint32_t);
 extern const DkClFn kDkClTable[3];
+using RowsLongFn = void (*)(const float*, const float*, float*, int, int, int, int);
+using DkLongFn = void (*)(const float*, const float*, float*, int, int, int, int, int, int);
+extern const RowsLongFn kRowsLongTable[2][3][4];
+extern const DkLongFn kDkLongTable[3];
 extern const DkBf16Fn kDkBf16mmaTable[3];
 extern const DkBf16Fn kDkBf16mmaTableNT[3];
 

@@ -36,6 +36,8 @@ WAVE_SIZE = 64
 WARP_SIZE = WAVE_SIZE  # the reference's name; 64 lanes on CDNA
 MAX_L = 48
 MAX_K = 48
+LONG_MAX_L = 192   # long-row kernels (pt_dwconv1d_*_long_f32)
+LONG_MAX_K = 256
 
 DEFAULT_B = 16_384
 DEFAULT_H = 128
@@ -643,6 +645,89 @@ class HipWarpRuntime:
 
         (collector or KERNEL_EVENTS).launch("bwd_weight_cl", launch, {"B": B, "H": H, "L": L, "K": K})
 
+    # ------------------------------------------------------------- long rows
+    @staticmethod
+    def _check_long(x: torch.Tensor, k: torch.Tensor, what: str = "k") -> tuple[int, int, int, int]:
+        if not x.is_cuda or not k.is_cuda:
+            raise ValueError(f"x and {what} must be CUDA tensors")
+        if x.dtype != torch.float32 or k.dtype != torch.float32:
+            raise ValueError("Only FP32 is supported")
+        if x.ndim != 3 or k.ndim != 2:
+            raise ValueError("Expected x[B,H,L] and k[H,K]")
+        B, H, L = map(int, x.shape)
+        Hk, K = map(int, k.shape)
+        if H != Hk:
+            raise ValueError("x and k channel dimensions do not match")
+        if L > LONG_MAX_L or K > LONG_MAX_K:
+            raise ValueError(f"Long-row kernels require L<={LONG_MAX_L}, K<={LONG_MAX_K}")
+        return B, H, L, K
+
+    def launch_fwd_long(self, x: torch.Tensor, k: torch.Tensor, y: torch.Tensor,
+                        collector: KernelEventCollector | None = None) -> None:
+        """FWD for rows up to 192 with up to 256 taps (matrix cores)."""
+        self._check_open()
+        B, H, L, K = self._check_long(x, k)
+        if y.shape != x.shape or y.dtype != torch.float32 or y.device != x.device:
+            raise ValueError("y must be a float32 tensor shaped like x on x's device")
+        self._require_contiguous(x, k, y)
+
+        def launch() -> None:
+            with torch.cuda.device(x.device):
+                st = self._lib.pt_dwconv1d_fwd_long_f32(_ptr(x), _ptr(k), _ptr(y), B, H, L, K,
+                                                        _stream_handle(x.device))
+            _lib.check(st, "pt_dwconv1d_fwd_long_f32")
+
+        (collector or KERNEL_EVENTS).launch("fwd_long", launch, {"B": B, "H": H, "L": L, "K": K})
+
+    def launch_bwd_input_long(self, gy: torch.Tensor, k: torch.Tensor, gx: torch.Tensor,
+                              collector: KernelEventCollector | None = None) -> None:
+        """dX for rows up to 192 with up to 256 taps (matrix cores)."""
+        self._check_open()
+        B, H, L, K = self._check_long(gy, k)
+        if gx.shape != gy.shape or gx.dtype != torch.float32 or gx.device != gy.device:
+            raise ValueError("gx must be a float32 tensor shaped like gy on gy's device")
+        self._require_contiguous(gy, k, gx)
+
+        def launch() -> None:
+            with torch.cuda.device(gy.device):
+                st = self._lib.pt_dwconv1d_dx_long_f32(_ptr(gy), _ptr(k), _ptr(gx), B, H, L, K,
+                                                       _stream_handle(gy.device))
+            _lib.check(st, "pt_dwconv1d_dx_long_f32")
+
+        (collector or KERNEL_EVENTS).launch("bwd_input_long", launch, {"B": B, "H": H, "L": L, "K": K})
+
+    def launch_bwd_weight_long(self, gy: torch.Tensor, x: torch.Tensor, gk: torch.Tensor, K: int,
+                               collector: KernelEventCollector | None = None) -> None:
+        """Deterministic dK for rows up to 192 with up to 256 taps: overwrites
+        gk, bitwise reproducible (fixed-order partials and reduction)."""
+        self._check_open()
+        K = int(K)
+        if not gy.is_cuda or not x.is_cuda or not gk.is_cuda:
+            raise ValueError("gy, x, and gk must be CUDA tensors")
+        if gy.dtype != torch.float32 or x.dtype != torch.float32 or gk.dtype != torch.float32:
+            raise ValueError("Only FP32 is supported")
+        if gy.shape != x.shape or x.ndim != 3:
+            raise ValueError("gy and x must have the same [B,H,L] shape")
+        B, H, L = map(int, x.shape)
+        if tuple(gk.shape) != (H, K):
+            raise ValueError(f"gk must have shape {(H, K)}")
+        if L > LONG_MAX_L or K > LONG_MAX_K:
+            raise ValueError(f"Long-row kernels require L<={LONG_MAX_L}, K<={LONG_MAX_K}")
+        self._require_contiguous(gy, x, gk)
+        out = ctypes.c_size_t(0)
+        st = self._lib.pt_dwconv1d_dk_long_workspace_bytes(B, H, L, K, ctypes.byref(out))
+        _lib.check(st, "pt_dwconv1d_dk_long_workspace_bytes")
+        ws = self._get_workspace(int(out.value), x.device)
+
+        def launch() -> None:
+            with torch.cuda.device(x.device):
+                st = self._lib.pt_dwconv1d_dk_long_f32(
+                    _ptr(gy), _ptr(x), _ptr(gk), _ptr(ws), ws.numel(), B, H, L, K,
+                    _stream_handle(x.device))
+            _lib.check(st, "pt_dwconv1d_dk_long_f32")
+
+        (collector or KERNEL_EVENTS).launch("bwd_weight_long", launch, {"B": B, "H": H, "L": L, "K": K})
+
     # ------------------------------------------------------------- reporting
     def kernel_attributes(self, kernel_id: int, L: int, K: int) -> dict[str, int]:
         regs, lds, scratch, maxt = (ctypes.c_int(0) for _ in range(4))
@@ -816,7 +901,7 @@ def configure_torch() -> None:
 
 
 __all__ = [
-    "WAVE_SIZE", "WARP_SIZE", "MAX_L", "MAX_K",
+    "WAVE_SIZE", "WARP_SIZE", "MAX_L", "MAX_K", "LONG_MAX_L", "LONG_MAX_K",
     "DEFAULT_B", "DEFAULT_H", "DEFAULT_L", "DEFAULT_K",
     "DEFAULT_WAVES_PER_BLOCK", "DEFAULT_DX_WAVES_PER_BLOCK", "DEFAULT_WARPS_PER_BLOCK",
     "DEFAULT_BWDK_BTILE", "DEFAULT_BWDK_KPACK", "DEFAULT_BWDK_BLOCK",

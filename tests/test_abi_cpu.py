@@ -178,6 +178,52 @@ def test_flash_dk_fp32_validation_before_launch(lib):
         assert fn(*ptrs, B, H, L, K, gz, S) == -2, (ptrs, B, H, L, K, gz)
 
 
+def test_long_row_validation_and_workspace(lib):
+    """Long-row entry points: L up to 192 and K up to 256, then NULL / 4-byte alignment
+    / workspace checks before any device work; the DK workspace is
+    [H, K, ranges] floats with ranges = ceil(512 / H), at most one per
+    16-sample step (a function of B and H only)."""
+    from pathtile_amd import _lib
+
+    buf = (ctypes.c_ubyte * 4096)()
+    base = ctypes.addressof(buf)
+    al = base + (-base) % 16
+    pa, pb, pc = (ctypes.c_void_p(al + o) for o in (0, 1024, 2048))
+    mis = ctypes.c_void_p(al + 2)
+    S = None
+    for fn in (lib.pt_dwconv1d_fwd_long_f32, lib.pt_dwconv1d_dx_long_f32):
+        assert fn(pa, pb, pc, 2, 4, 193, 5, S) == _lib.PT_ERR_SHAPE
+        assert fn(pa, pb, pc, 2, 4, 192, 257, S) == _lib.PT_ERR_SHAPE
+        assert fn(pa, pb, pc, 2, 4, 0, 5, S) == _lib.PT_ERR_SHAPE
+        assert fn(pa, pb, pc, -1, 4, 16, 5, S) == _lib.PT_ERR_SHAPE
+        assert fn(pa, pb, pc, 1 << 16, 1 << 12, 192, 5, S) == _lib.PT_ERR_SHAPE  # 2^31 elements
+        assert fn(pa, pb, pc, 0, 4, 192, 5, S) == _lib.PT_OK                      # empty
+        assert fn(None, pb, pc, 2, 4, 192, 5, S) == _lib.PT_ERR_NULL
+        assert fn(mis, pb, pc, 2, 4, 192, 5, S) == _lib.PT_ERR_ALIGN
+    out = ctypes.c_size_t(0)
+
+    def ranges(B, H):
+        return max(1, min(-(-512 // H), -(-B // 16)))
+
+    for (B, H, L, K) in [(16384, 128, 192, 192), (16384, 64, 192, 3), (100, 1000, 64, 64),
+                         (40, 8, 176, 256), (1, 3, 1, 1), (4096, 512, 128, 48)]:
+        assert lib.pt_dwconv1d_dk_long_workspace_bytes(B, H, L, K, ctypes.byref(out)) == _lib.PT_OK
+        assert out.value == H * K * ranges(B, H) * 4, (B, H, L, K)
+    lib.pt_dwconv1d_dk_long_workspace_bytes(16384, 128, 192, 192, ctypes.byref(out))
+    assert out.value == 128 * 192 * 4 * 4  # 4 ranges of 16-sample steps
+    lib.pt_dwconv1d_dk_long_workspace_bytes(0, 128, 192, 192, ctypes.byref(out))
+    assert out.value == 0
+    dk = lib.pt_dwconv1d_dk_long_f32
+    assert dk(pa, pb, pc, None, 0, 2, 4, 193, 5, S) == _lib.PT_ERR_SHAPE
+    assert dk(pa, pb, pc, None, 0, 2, 4, 192, 257, S) == _lib.PT_ERR_SHAPE
+    assert dk(pa, pb, None, None, 0, 2, 4, 192, 5, S) == _lib.PT_ERR_NULL
+    assert dk(pa, pb, mis, None, 0, 2, 4, 192, 5, S) == _lib.PT_ERR_ALIGN
+    assert dk(None, pb, pc, None, 0, 2, 4, 192, 5, S) == _lib.PT_ERR_NULL
+    assert dk(pa, pb, pc, None, 0, 2, 4, 192, 5, S) == _lib.PT_ERR_WORKSPACE
+    assert dk(pa, pb, pc, pa, 8, 2, 4, 192, 5, S) == _lib.PT_ERR_WORKSPACE   # needs 80 bytes
+    assert dk(pa, pb, pc, None, 0, 2, 0, 192, 5, S) == _lib.PT_OK            # H == 0
+
+
 def test_bf16_workspace_bytes(lib):
     """BF16 DK partials: [H, K, ranges] floats, one range per 16-sample step
     at most; the range count is, of 2^k and 3 * 2^(k-1) in [8, 256], the one

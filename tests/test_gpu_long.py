@@ -1,0 +1,148 @@
+"""Long rows (L up to 192, K up to 256) on the GPU (marked ``gpu``): the long-row
+FWD/dX/dK entry points against the FP64 oracle, and the
+``kernels/shared_l192`` API (the reference's long-row module) end to end.
+
+Bars: FWD/dX within 1e-5 and dK within 1e-4 max-abs-scaled of the FP64 sums
+(the path's FP32 bars), dK bitwise reproducible. At the reference's own
+benchmark shape (B16384 H128 L192 K192,
+benchmark/benchmark_gmc_vs_shared_l192.py:14-17) the oracle is too slow for
+the whole tensor: FWD/dX are checked on sampled samples (rows are
+independent), dK through its FP64 adjoint identity over the whole tensors,
+sum_hj dk[h,j] v[h,j] = sum_bht dy[b,h,t] (x conv v)[b,h,t].
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+FWD_TOL = 1e-5
+DK_TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def rt():
+    from pathtile_amd import runtime
+
+    r = runtime.HipWarpRuntime()
+    runtime.install_runtime(r)
+    yield r
+
+
+SHAPES = [
+    (16, 8, 192, 192),
+    (33, 4, 100, 37),
+    (8, 16, 192, 256),   # K > L
+    (40, 8, 64, 3),
+    (20, 4, 176, 256),   # K > L, ragged bucket
+    (7, 12, 49, 49),     # just past the specialised path
+    (64, 8, 130, 1),
+    (5, 3, 1, 256),      # one-column rows
+    (70, 2, 96, 48),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "B{}H{}L{}K{}".format(*s))
+def test_long_fwd_dx_dk_against_fp64(rt, shape):
+    B, H, L, K = shape
+    print(f"[case] long rows B={B} H={H} L={L} K={K}", flush=True)
+    x, w, dy = oracle.make_inputs(B, H, L, K, seed=15000 + B + L + K)
+    xd, wd, dyd = x.cuda(), w.cuda(), dy.cuda()
+    y = torch.full_like(xd, float("nan"))
+    dx = torch.full_like(dyd, float("nan"))
+    rt.launch_fwd_long(xd, wd, y)
+    rt.launch_bwd_input_long(dyd, wd, dx)
+    assert oracle.normalized_max_abs(y.cpu().numpy(), oracle.fwd_f64(x, w)) < FWD_TOL
+    assert oracle.normalized_max_abs(dx.cpu().numpy(), oracle.dx_f64(dy, w)) < FWD_TOL
+    g1 = torch.full((H, K), float("nan"), device="cuda")
+    g2 = torch.full((H, K), float("nan"), device="cuda")
+    rt.launch_bwd_weight_long(dyd, xd, g1, K)
+    rt.launch_bwd_weight_long(dyd, xd, g2, K)
+    ref = oracle.dk_f64(dy, x, K)
+    assert oracle.normalized_max_abs(g1.cpu().numpy(), ref) < DK_TOL
+    assert torch.equal(g1, g2)
+    for j in range(K):
+        lo, hi = oracle.valid_tap_range(L, K, j)
+        if hi <= lo:
+            assert torch.all(g1[:, j] == 0)
+
+
+def test_long_rows_on_short_shapes_match_the_specialised_path(rt):
+    """The long kernels also serve L, K <= 48; they agree with the
+    specialised kernels to the FP32 bars."""
+    B, H, L, K = 300, 16, 48, 48
+    x, w, dy = oracle.make_inputs(B, H, L, K, seed=16)
+    xd, wd, dyd = x.cuda(), w.cuda(), dy.cuda()
+    y1, y2 = torch.empty_like(xd), torch.empty_like(xd)
+    rt.launch_fwd_long(xd, wd, y1)
+    rt.launch_fwd(xd, wd, y2)
+    assert float((y1 - y2).abs().max() / y2.abs().max()) < FWD_TOL
+    g1, g2 = torch.empty(H, K, device="cuda"), torch.empty(H, K, device="cuda")
+    rt.launch_bwd_weight_long(dyd, xd, g1, K)
+    rt.launch_bwd_weight_deterministic(dyd, xd, g2, K)
+    assert float((g1 - g2).abs().max() / g2.abs().max()) < DK_TOL
+
+
+def test_shared_l192_module_autograd():
+    """The reference's long-row API: y, gx, gk against FP64, timing lists
+    appended once per launch, short shapes routed to the specialised path."""
+    from pathtile_amd.kernels import shared_l192 as sl
+
+    sl.reset_timing_collectors()
+    for (B, H, L, K) in [(64, 8, 192, 192), (32, 4, 48, 48)]:
+        x, w, dy = oracle.make_inputs(B, H, L, K, seed=17 + L)
+        xd = x.cuda().requires_grad_(True)
+        wd = w.cuda().requires_grad_(True)
+        y = sl.depthwise_conv_shared(xd, wd)
+        gx, gk = torch.autograd.grad(y, (xd, wd), dy.cuda())
+        assert oracle.normalized_max_abs(y.detach().cpu().numpy(), oracle.fwd_f64(x, w)) < FWD_TOL
+        assert oracle.normalized_max_abs(gx.cpu().numpy(), oracle.dx_f64(dy, w)) < FWD_TOL
+        assert oracle.normalized_max_abs(gk.cpu().numpy(), oracle.dk_f64(dy, x, K)) < DK_TOL
+    assert len(sl.FWD_TIMES) == len(sl.BWD_IN_TIMES) == len(sl.BWD_K_TIMES) == 2
+    assert all(t > 0 for t in sl.FWD_TIMES + sl.BWD_IN_TIMES + sl.BWD_K_TIMES)
+
+
+def test_shared_l192_module_errors():
+    from pathtile_amd.kernels import shared_l192 as sl
+
+    x = torch.zeros(2, 4, 300, device="cuda")
+    with pytest.raises(ValueError, match="L<=192"):
+        sl.depthwise_conv_shared(x, torch.zeros(4, 5, device="cuda"))
+    with pytest.raises(TypeError, match="x must be float32"):
+        sl.depthwise_conv_shared(x.double(), torch.zeros(4, 5, device="cuda"))
+    with pytest.raises(ValueError, match="Channel mismatch"):
+        sl.depthwise_conv_shared(x[:, :, :192], torch.zeros(3, 5, device="cuda"))
+
+
+def test_long_rows_reference_benchmark_shape(rt):
+    B, H, L, K = 16384, 128, 192, 192
+    print(f"[case] long rows at the reference shape B={B} H={H} L={L} K={K}", flush=True)
+    x, w, dy = oracle.make_inputs(B, H, L, K, seed=42)
+    xd, wd, dyd = x.cuda(), w.cuda(), dy.cuda()
+    y = torch.empty_like(xd)
+    dx = torch.empty_like(dyd)
+    rt.launch_fwd_long(xd, wd, y)
+    rt.launch_bwd_input_long(dyd, wd, dx)
+    idx = torch.from_numpy(np.random.default_rng(5).choice(B, 24, replace=False))
+    assert oracle.normalized_max_abs(y[idx.cuda()].cpu().numpy(), oracle.fwd_f64(x[idx], w)) < FWD_TOL
+    assert oracle.normalized_max_abs(dx[idx.cuda()].cpu().numpy(), oracle.dx_f64(dy[idx], w)) < FWD_TOL
+    del y, dx
+    gk = torch.empty(H, K, device="cuda")
+    rt.launch_bwd_weight_long(dyd, xd, gk, K)
+    v = torch.randn(H, K, generator=torch.Generator().manual_seed(8), dtype=torch.float64)
+    lhs = float((gk.double().cpu() * v).sum())
+    p = K // 2
+    vd = v.cuda()
+    rhs = 0.0
+    for c0 in range(0, B, 2048):   # FP64 on the GPU, in sample chunks
+        xs = torch.nn.functional.pad(xd[c0:c0 + 2048].double(), (p, K - 1 - p))
+        conv = torch.zeros(xs.shape[0], H, L, dtype=torch.float64, device="cuda")
+        for j in range(K):
+            conv += vd[None, :, j:j + 1] * xs[:, :, j:j + L]
+        rhs += float((dyd[c0:c0 + 2048].double() * conv).sum())
+    assert abs(lhs - rhs) <= 1e-5 * float((gk.double().cpu().abs() * v.abs()).sum())

@@ -257,11 +257,15 @@ def test_useful_fma_counts():
 
 
 def test_rejects_out_of_range():
-    x = np.zeros((1, 1, 49), dtype=np.float32)
+    """The FP64 sums serve L, K <= 256; beyond that, and for L or K < 1, the
+    oracle refuses the shape."""
+    x = np.zeros((1, 1, 257), dtype=np.float32)
     with pytest.raises(ValueError):
         oracle.fwd_f64(x, np.zeros((1, 3), dtype=np.float32))
     with pytest.raises(ValueError):
-        oracle.fwd_f64(np.zeros((1, 1, 8), dtype=np.float32), np.zeros((1, 49), dtype=np.float32))
+        oracle.fwd_f64(np.zeros((1, 1, 8), dtype=np.float32), np.zeros((1, 257), dtype=np.float32))
+    with pytest.raises(ValueError):
+        oracle.dk_f64(np.zeros((1, 1, 8), dtype=np.float32), np.zeros((1, 1, 8), dtype=np.float32), 0)
 
 
 # ---------------------------------------------------------------------------
@@ -320,3 +324,45 @@ def test_mutants_are_caught(name):
         e = np.zeros((H, K), dtype=np.float32)
         e[:, 0] = 1.0
         assert not np.array_equal(_conv_np(xn, e, **kw), oracle.fwd_f64(xn, e))
+
+
+@pytest.mark.parametrize("L,K", [(192, 192), (100, 37), (64, 256), (200, 256), (1, 256), (49, 49)])
+def test_fp64_sums_on_long_rows_match_numpy_correlate(L, K):
+    """The FP64 sums on long rows (L, K up to 256, the reference's
+    kernels/shared_l192.py regime) against numpy.correlate, a library
+    routine independent of the oracle's loops:
+    FWD y[t] = corr(pad(x, (p, K-1-p)), w)[t]; dX dx[s] = corr(pad(dy,
+    (K-1-p, p)), w[::-1])[s]; dK dk[j] = sum_b corr(pad(x, (p, K-1-p)),
+    dy)[j]."""
+    B, H = 3, 2
+    g = np.random.default_rng(L * 1000 + K)
+    x = g.standard_normal((B, H, L)).astype(np.float32)
+    dy = g.standard_normal((B, H, L)).astype(np.float32)
+    w = g.standard_normal((H, K)).astype(np.float32)
+    p = K // 2
+    y_ref = np.empty((B, H, L))
+    dx_ref = np.empty((B, H, L))
+    dk_ref = np.zeros((H, K))
+    for b in range(B):
+        for h in range(H):
+            xp = np.pad(x[b, h].astype(np.float64), (p, K - 1 - p))
+            y_ref[b, h] = np.correlate(xp, w[h].astype(np.float64), "valid")
+            dyp = np.pad(dy[b, h].astype(np.float64), (K - 1 - p, p))
+            dx_ref[b, h] = np.correlate(dyp, w[h, ::-1].astype(np.float64), "valid")
+            dk_ref[h] += np.correlate(xp, dy[b, h].astype(np.float64), "valid")
+    scale = lambda a: np.abs(a).max() + 1.0  # noqa: E731
+    np.testing.assert_allclose(oracle.fwd_f64(x, w), y_ref, rtol=0, atol=1e-12 * scale(y_ref))
+    np.testing.assert_allclose(oracle.dx_f64(dy, w), dx_ref, rtol=0, atol=1e-12 * scale(dx_ref))
+    np.testing.assert_allclose(oracle.dk_f64(dy, x, K), dk_ref, rtol=0, atol=1e-12 * scale(dk_ref))
+
+
+def test_reference_chains_keep_the_reference_kernel_range():
+    """The FP32 fmaf chains restate kernels limited to L, K <= 48
+    (kernels/warp_tiled_ampere.py:715-716) and refuse longer rows."""
+    x = np.zeros((1, 1, 49), dtype=np.float32)
+    with pytest.raises(ValueError, match="<= 48"):
+        oracle.fwd_f32_refchain(x, np.zeros((1, 3), dtype=np.float32))
+    with pytest.raises(ValueError, match="<= 48"):
+        oracle.dx_f32_refchain(x[:, :, :8], np.zeros((1, 49), dtype=np.float32))
+    with pytest.raises(ValueError, match="<= 256"):
+        oracle.fwd_f64(np.zeros((1, 1, 257), dtype=np.float32), np.zeros((1, 3), dtype=np.float32))
