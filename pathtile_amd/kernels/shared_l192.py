@@ -34,8 +34,7 @@ from __future__ import annotations
 
 import torch
 
-from .. import runtime as _rt
-from .warp_tiled import CudaContextGuard, TorchCudaInterop, _time_kernel  # noqa: F401
+from .warp_tiled import CudaContextGuard, TorchCudaInterop, make_shared_function  # noqa: F401
 
 # Legacy launch constants (kernels/shared_l192.py:109-118)
 TTILE = 32
@@ -66,61 +65,7 @@ def reset_timing_collectors():
     BWD_K_TIMES.clear()
 
 
-def _short(L: int, K: int) -> bool:
-    return L <= _rt.MAX_L and K <= _rt.MAX_K
-
-
-class DepthwiseConvShared(torch.autograd.Function):
-    """Checks, in the reference's order (:796-830), then FWD; backward dX and
-    a deterministic dK written into a fresh gk (:895-1005)."""
-
-    @staticmethod
-    def forward(ctx, x: torch.Tensor, kernel: torch.Tensor) -> torch.Tensor:
-        if not x.is_cuda or not kernel.is_cuda:
-            raise ValueError("x and kernel must be CUDA tensors")
-        if x.dtype != torch.float32:
-            raise TypeError("x must be float32")
-        if kernel.dtype != torch.float32:
-            raise TypeError("kernel must be float32")
-        if x.ndim != 3:
-            raise ValueError(f"x must be [B,H,L], got {tuple(x.shape)}")
-        if kernel.ndim != 2:
-            raise ValueError(f"kernel must be [H,K], got {tuple(kernel.shape)}")
-
-        x = x.contiguous()
-        kernel = kernel.contiguous()
-
-        B, H, L = x.shape
-        Hk, K = kernel.shape
-        if H != Hk:
-            raise ValueError(f"Channel mismatch: x H={H}, kernel H={Hk}")
-        if L > _rt.LONG_MAX_L or K > _rt.LONG_MAX_K:
-            raise ValueError(f"Long-row kernels require L<={_rt.LONG_MAX_L}, K<={_rt.LONG_MAX_K}")
-
-        ctx.save_for_backward(x, kernel)
-        ctx.params = (B, H, L, K)
-
-        y = torch.empty_like(x)
-        rt = _rt.get_or_create_runtime()
-        fwd = rt.launch_fwd if _short(L, K) else rt.launch_fwd_long
-        FWD_TIMES.append(_time_kernel(lambda: fwd(x, kernel, y)))
-        return y
-
-    @staticmethod
-    def backward(ctx, grad_y: torch.Tensor):
-        x, kernel = ctx.saved_tensors
-        B, H, L, K = ctx.params
-        grad_y = grad_y.contiguous()
-        gx = torch.empty_like(x)
-        gk = torch.empty_like(kernel)
-        rt = _rt.get_or_create_runtime()
-        if _short(L, K):
-            dx, dk = rt.launch_bwd_input, rt.launch_bwd_weight_deterministic
-        else:
-            dx, dk = rt.launch_bwd_input_long, rt.launch_bwd_weight_long
-        BWD_IN_TIMES.append(_time_kernel(lambda: dx(grad_y, kernel, gx)))
-        BWD_K_TIMES.append(_time_kernel(lambda: dk(grad_y, x, gk, K)))
-        return gx, gk
+DepthwiseConvShared = make_shared_function(FWD_TIMES, BWD_IN_TIMES, BWD_K_TIMES, __name__)
 
 
 def depthwise_conv_shared(x: torch.Tensor, kernel: torch.Tensor) -> torch.Tensor:

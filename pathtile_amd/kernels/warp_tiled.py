@@ -5,8 +5,8 @@ side effects as the reference module (``__all__`` at
 kernels/warp_tiled.py:1020-1031); underneath, the three paths run the
 hand-written gfx950 kernels of ``libpathtile_hip.so``:
 
-* ``DepthwiseConvShared.forward``  -> FWD kernel (one wave per 64 rows of a
-  channel, reference fmaf order);
+* ``DepthwiseConvShared.forward``  -> the FWD kernel chosen per shape (the
+  long-row kernel above L or K = 48);
 * ``DepthwiseConvShared.backward`` -> dX kernel, then the deterministic
   two-pass dK, which writes ``gk`` directly like the reference's shared
   kernel does (``gk = torch.empty_like(kernel)``, kernels/warp_tiled.py:902).
@@ -20,9 +20,11 @@ Differences from the reference, by design:
 * Importing this module does not need a GPU; the reference raises at import
   without CUDA (:15-18). Here the first call with CPU tensors raises
   ``ValueError("x and kernel must be CUDA tensors")``.
-* L and K are limited to 48 (``ValueError``, same message as
-  kernels/warp_tiled_ampere.py:715-716); the reference's shared kernels
-  accept longer rows.
+* Rows and taps up to 48 run the specialised kernels; longer rows (L up to
+  192, K up to 256) run the long-row matrix-core kernels, and beyond that
+  the call raises ``ValueError``. The reference's shared kernels have no
+  stated bound (their dK's shared memory, 2 * 64 * L * 4 bytes, caps L near
+  96 in practice).
 * ``CudaContextGuard`` is a no-op context manager (HIP has no context stack to
   push) and ``TorchCudaInterop.as_gpuarray`` validates like the reference and
   returns the tensor itself (there is no PyCUDA GPUArray).
@@ -142,52 +144,76 @@ def _runtime() -> HipWarpRuntime:
 # =============================================================================
 # Autograd (:787-1017)
 # =============================================================================
-class DepthwiseConvShared(torch.autograd.Function):
+def _is_short(L: int, K: int) -> bool:
+    return L <= MAX_L and K <= MAX_K
 
-    @staticmethod
-    def forward(ctx, x: torch.Tensor, kernel: torch.Tensor) -> torch.Tensor:
-        if not x.is_cuda or not kernel.is_cuda:
-            raise ValueError("x and kernel must be CUDA tensors")
-        if x.dtype != torch.float32:
-            raise TypeError("x must be float32")
-        if kernel.dtype != torch.float32:
-            raise TypeError("kernel must be float32")
-        if x.ndim != 3:
-            raise ValueError(f"x must be [B,H,L], got {tuple(x.shape)}")
-        if kernel.ndim != 2:
-            raise ValueError(f"kernel must be [H,K], got {tuple(kernel.shape)}")
 
-        x = x.contiguous()
-        kernel = kernel.contiguous()
+def make_shared_function(fwd_times: list, bwd_in_times: list, bwd_k_times: list,
+                         module: str = __name__):
+    """The reference's ``DepthwiseConvShared`` (:787-1005) appending its
+    kernel times to the given lists. Checks and messages in the reference's
+    order (:796-830). Rows and taps up to 48 run the specialised kernels;
+    longer ones (L up to 192, K up to 256) the long-row matrix-core kernels.
+    Backward: dX, then a deterministic dK written into a fresh ``gk``
+    (``gk = torch.empty_like(kernel)``, :902)."""
 
-        B, H, L = x.shape
-        Hk, K = kernel.shape
-        if H != Hk:
-            raise ValueError(f"Channel mismatch: x H={H}, kernel H={Hk}")
-        if L > MAX_L or K > MAX_K:
-            raise ValueError(f"Specialized kernels require L<={MAX_L}, K<={MAX_K}")
+    class DepthwiseConvShared(torch.autograd.Function):
 
-        ctx.save_for_backward(x, kernel)
-        ctx.params = (B, H, L, K)
+        @staticmethod
+        def forward(ctx, x: torch.Tensor, kernel: torch.Tensor) -> torch.Tensor:
+            if not x.is_cuda or not kernel.is_cuda:
+                raise ValueError("x and kernel must be CUDA tensors")
+            if x.dtype != torch.float32:
+                raise TypeError("x must be float32")
+            if kernel.dtype != torch.float32:
+                raise TypeError("kernel must be float32")
+            if x.ndim != 3:
+                raise ValueError(f"x must be [B,H,L], got {tuple(x.shape)}")
+            if kernel.ndim != 2:
+                raise ValueError(f"kernel must be [H,K], got {tuple(kernel.shape)}")
 
-        y = torch.empty_like(x)
-        rt = _runtime()
-        FWD_TIMES.append(_time_kernel(lambda: rt.launch_fwd(x, kernel, y)))
-        return y
+            x = x.contiguous()
+            kernel = kernel.contiguous()
 
-    @staticmethod
-    def backward(ctx, grad_y: torch.Tensor):
-        x, kernel = ctx.saved_tensors
-        B, H, L, K = ctx.params
-        grad_y = grad_y.contiguous()
-        gx = torch.empty_like(x)
-        gk = torch.empty_like(kernel)
-        rt = _runtime()
-        BWD_IN_TIMES.append(_time_kernel(lambda: rt.launch_bwd_input(grad_y, kernel, gx)))
-        BWD_K_TIMES.append(
-            _time_kernel(lambda: rt.launch_bwd_weight_deterministic(grad_y, x, gk, K))
-        )
-        return gx, gk
+            B, H, L = x.shape
+            Hk, K = kernel.shape
+            if H != Hk:
+                raise ValueError(f"Channel mismatch: x H={H}, kernel H={Hk}")
+            if L > _rt.LONG_MAX_L or K > _rt.LONG_MAX_K:
+                raise ValueError(
+                    f"Long-row kernels require L<={_rt.LONG_MAX_L}, K<={_rt.LONG_MAX_K}")
+
+            ctx.save_for_backward(x, kernel)
+            ctx.params = (B, H, L, K)
+
+            y = torch.empty_like(x)
+            rt = _runtime()
+            fwd = rt.launch_fwd if _is_short(L, K) else rt.launch_fwd_long
+            fwd_times.append(_time_kernel(lambda: fwd(x, kernel, y)))
+            return y
+
+        @staticmethod
+        def backward(ctx, grad_y: torch.Tensor):
+            x, kernel = ctx.saved_tensors
+            B, H, L, K = ctx.params
+            grad_y = grad_y.contiguous()
+            gx = torch.empty_like(x)
+            gk = torch.empty_like(kernel)
+            rt = _runtime()
+            if _is_short(L, K):
+                dx, dk = rt.launch_bwd_input, rt.launch_bwd_weight_deterministic
+            else:
+                dx, dk = rt.launch_bwd_input_long, rt.launch_bwd_weight_long
+            bwd_in_times.append(_time_kernel(lambda: dx(grad_y, kernel, gx)))
+            bwd_k_times.append(_time_kernel(lambda: dk(grad_y, x, gk, K)))
+            return gx, gk
+
+    DepthwiseConvShared.__qualname__ = "DepthwiseConvShared"
+    DepthwiseConvShared.__module__ = module
+    return DepthwiseConvShared
+
+
+DepthwiseConvShared = make_shared_function(FWD_TIMES, BWD_IN_TIMES, BWD_K_TIMES)
 
 
 def depthwise_conv_shared(x: torch.Tensor, kernel: torch.Tensor) -> torch.Tensor:

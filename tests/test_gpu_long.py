@@ -88,10 +88,14 @@ def test_long_rows_on_short_shapes_match_the_specialised_path(rt):
     assert float((g1 - g2).abs().max() / g2.abs().max()) < DK_TOL
 
 
-def test_shared_l192_module_autograd():
-    """The reference's long-row API: y, gx, gk against FP64, timing lists
-    appended once per launch, short shapes routed to the specialised path."""
-    from pathtile_amd.kernels import shared_l192 as sl
+@pytest.mark.parametrize("module", ["shared_l192", "warp_tiled"])
+def test_shared_l192_module_autograd(module):
+    """The reference's long-row API (and the warp_tiled module's, which
+    shares it): y, gx, gk against FP64, timing lists appended once per
+    launch, short shapes routed to the specialised path."""
+    import importlib
+
+    sl = importlib.import_module(f"pathtile_amd.kernels.{module}")
 
     sl.reset_timing_collectors()
     for (B, H, L, K) in [(64, 8, 192, 192), (32, 4, 48, 48)]:

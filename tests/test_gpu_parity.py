@@ -409,8 +409,8 @@ def test_api_errors_on_gpu_tensors():
         wt.depthwise_conv_shared(x, k[0])
     with pytest.raises(ValueError, match="Channel mismatch: x H=3, kernel H=2"):
         wt.depthwise_conv_shared(x, k[:2])
-    with pytest.raises(ValueError, match="L<=48, K<=48"):
-        wt.depthwise_conv_shared(torch.zeros(1, 3, 49, device="cuda:0"), k)
+    with pytest.raises(ValueError, match="L<=192, K<=256"):
+        wt.depthwise_conv_shared(torch.zeros(1, 3, 193, device="cuda:0"), k)
 
 
 def test_empty_batch(rt):
