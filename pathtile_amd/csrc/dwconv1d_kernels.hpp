@@ -800,53 +800,28 @@ __global__ __launch_bounds__(1024) void dwconv_dk_mfma_kernel(
 constexpr int kRowsCgWaves = 8;    // one channel per wave
 constexpr int kRowsCgStep = 16;    // samples per step (MFMA M)
 
-// 16-byte chunks of the staged segments: 4 FP32 or 8 BF16 elements (BF16 is
-// carried as uint16_t bit patterns). The kernels stage FP32 in LDS: BF16
-// widens to FP32 exactly, and FP32 results narrow to BF16 with
-// round-to-nearest-even (a NaN stays a quiet NaN).
-template <typename T>
-struct ChunkOf {
-  static constexpr int n = 16 / (int)sizeof(T);
-};
-
+// BF16 bit pattern of an FP32 value, round-to-nearest-even (a NaN stays a
+// quiet NaN).
 __device__ __forceinline__ uint32_t bf16_bits_rne(float f) {
   const uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
-template <typename T>
+// A 16-byte chunk (4 FP32 values) between registers and LDS.
 __device__ __forceinline__ void chunk_to_lds(float* dst, const u32x4 v) {
-  if constexpr (sizeof(T) == 4) {
-    *reinterpret_cast<float4*>(dst) =
-        make_float4(__uint_as_float(v.x), __uint_as_float(v.y),
-                    __uint_as_float(v.z), __uint_as_float(v.w));
-  } else {
-    *reinterpret_cast<float4*>(dst) =
-        make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
-                    __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
-    *reinterpret_cast<float4*>(dst + 4) =
-        make_float4(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xffff0000u),
-                    __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xffff0000u));
-  }
+  *reinterpret_cast<float4*>(dst) =
+      make_float4(__uint_as_float(v.x), __uint_as_float(v.y),
+                  __uint_as_float(v.z), __uint_as_float(v.w));
 }
 
-template <typename T>
 __device__ __forceinline__ u32x4 lds_to_chunk(const float* src) {
   const float4 a = *reinterpret_cast<const float4*>(src);
   u32x4 v;
-  if constexpr (sizeof(T) == 4) {
-    v.x = __float_as_uint(a.x);
-    v.y = __float_as_uint(a.y);
-    v.z = __float_as_uint(a.z);
-    v.w = __float_as_uint(a.w);
-  } else {
-    const float4 b = *reinterpret_cast<const float4*>(src + 4);
-    v.x = bf16_bits_rne(a.x) | (bf16_bits_rne(a.y) << 16);
-    v.y = bf16_bits_rne(a.z) | (bf16_bits_rne(a.w) << 16);
-    v.z = bf16_bits_rne(b.x) | (bf16_bits_rne(b.y) << 16);
-    v.w = bf16_bits_rne(b.z) | (bf16_bits_rne(b.w) << 16);
-  }
+  v.x = __float_as_uint(a.x);
+  v.y = __float_as_uint(a.y);
+  v.z = __float_as_uint(a.z);
+  v.w = __float_as_uint(a.w);
   return v;
 }
 
@@ -872,16 +847,16 @@ __host__ __device__ constexpr size_t rows_cg_lds_bytes(int L, int hc = kRowsCgWa
   return (size_t)4 * kRowsCgStep * (hc * L + 4) * sizeof(float);
 }
 
-// T: element type of in/out (float, or uint16_t holding bfloat16); the taps
-// w are FP32 either way. kDepth: steps in flight in registers.
-template <int LMAX, bool DX, int kDepth, typename T = float, int HC = kRowsCgWaves>
+// kDepth: steps in flight in registers; HC: channels (= waves) per
+// workgroup.
+template <int LMAX, bool DX, int kDepth, int HC = kRowsCgWaves>
 __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
-    const T* __restrict__ in, const float* __restrict__ w,
-    T* __restrict__ out, int B, int H, int L, int K, int nranges,
+    const float* __restrict__ in, const float* __restrict__ w,
+    float* __restrict__ out, int B, int H, int L, int K, int nranges,
     uint32_t nblocks) {
   constexpr int NT = LMAX / 16;  // 16-wide output tiles
   constexpr int NU = LMAX / 4;   // MFMA steps over the input columns
-  constexpr int EPC = ChunkOf<T>::n;  // elements per 16-byte chunk
+  constexpr int EPC = 4;  // floats per 16-byte chunk
   constexpr int kNpt = (HC * LMAX * kRowsCgStep / EPC + HC * kWave - 1) / (HC * kWave);
   extern __shared__ float lds[];
 
@@ -898,8 +873,8 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
   const int sk = seg + 4;                 // LDS stride between samples
   const int sz = kRowsCgStep * sk;        // one stage
   const int per = kRowsCgStep * segc;     // chunks per stage
-  const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * (uint32_t)sizeof(T);
-  const uint32_t grp_bytes = (uint32_t)g * (uint32_t)seg * (uint32_t)sizeof(T);
+  const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
+  const uint32_t grp_bytes = (uint32_t)g * (uint32_t)seg * 4u;
   float* inl = lds;                       // input stages 0, 1
   float* outl = lds + 2 * sz;             // output stages 0, 1
 
@@ -918,8 +893,7 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
   u32x4 stg[kDepth][kNpt];
   auto load_step = [&](int s, u32x4 (&st)[kNpt]) {
     const int bs = (r + s * nranges) * kRowsCgStep;
-    const __amdgpu_buffer_rsrc_t rs =
-        make_rsrc_t(in + (size_t)bs * (size_t)H * (size_t)L);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(in + (size_t)bs * (size_t)H * (size_t)L);
     const int klim = min(kRowsCgStep, B - bs);
 #pragma unroll
     for (int i = 0; i < kNpt; ++i)
@@ -928,17 +902,16 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
   auto store_stage = [&](int buf, const u32x4 (&st)[kNpt]) {
 #pragma unroll
     for (int i = 0; i < kNpt; ++i)
-      if (ek[i] < kRowsCgStep) chunk_to_lds<T>(inl + buf * sz + elds[i], st[i]);
+      if (ek[i] < kRowsCgStep) chunk_to_lds(inl + buf * sz + elds[i], st[i]);
   };
   auto flush_out = [&](int s) {
     const float* o = outl + (s & 1) * sz;
     const int bs = (r + s * nranges) * kRowsCgStep;
-    const __amdgpu_buffer_rsrc_t ro =
-        make_rsrc_t(out + (size_t)bs * (size_t)H * (size_t)L);
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(out + (size_t)bs * (size_t)H * (size_t)L);
     const int klim = min(kRowsCgStep, B - bs);
 #pragma unroll
     for (int i = 0; i < kNpt; ++i) {
-      const u32x4 v = lds_to_chunk<T>(o + (ek[i] < kRowsCgStep ? elds[i] : 0u));
+      const u32x4 v = lds_to_chunk(o + (ek[i] < kRowsCgStep ? elds[i] : 0u));
       buf_store_chunk<kCpolNT>(v, ro, ek[i] < klim ? eoff[i] : kOob);
     }
   };
@@ -1314,11 +1287,9 @@ __device__ __forceinline__ void dk_cg_epilogue(
   }
 }
 
-// T: element type of gy and x (float, or uint16_t holding bfloat16); dk and
-// its partials are FP32 either way.
-template <int LMAX, int LOAD_CPOL = kCpolNone, typename T = float>
+template <int LMAX, int LOAD_CPOL = kCpolNone>
 __global__ __launch_bounds__(512) void dwconv_dk_cg_kernel(
-    const T* __restrict__ gy, const T* __restrict__ x,
+    const float* __restrict__ gy, const float* __restrict__ x,
     float* __restrict__ dst, int B, int H, int L, int K, int nranges,
     uint32_t nblocks, int det) {
   using G = CgGeo<LMAX>;
@@ -1339,15 +1310,15 @@ __global__ __launch_bounds__(512) void dwconv_dk_cg_kernel(
   const int tsteps = (B + kCgStep - 1) / kCgStep;
   const int nsteps = r < tsteps ? (tsteps - 1 - r) / nranges + 1 : 0;
 
-  constexpr int EPC = ChunkOf<T>::n;           // elements per 16-byte chunk
+  constexpr int EPC = 4;                       // floats per 16-byte chunk
   const int seg = hc * L;                     // elements per sample segment
   const int segc = seg / EPC;                 // chunks per segment
   const int sk = seg + kCgPad;                // LDS stride between samples
   const int sz = kCgStep * sk;                // one tensor's stage
   const int per = kCgStep * segc;             // chunks per stage and tensor
   constexpr int kNpt = (CPW * LMAX * 4 / EPC + kWave - 1) / kWave;  // per thread, tensor
-  const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * (uint32_t)sizeof(T);  // one sample
-  const uint32_t grp_bytes = (uint32_t)g * (uint32_t)seg * (uint32_t)sizeof(T);
+  const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;  // one sample
+  const uint32_t grp_bytes = (uint32_t)g * (uint32_t)seg * 4u;
 
   // Loop-invariant part of each staged element: its sample within the
   // step, its byte offset from the step's first sample, its LDS offset.
@@ -1370,8 +1341,8 @@ __global__ __launch_bounds__(512) void dwconv_dk_cg_kernel(
   auto load_step = [&](int s, u32x4 (&st)[2][kNpt]) {
     const int bs = (r + s * nranges) * kCgStep;
     const size_t r0 = (size_t)bs * (size_t)H * (size_t)L;
-    const __amdgpu_buffer_rsrc_t rg = make_rsrc_t(gy + r0);
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc_t(x + r0);
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(gy + r0);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + r0);
     const int klim = min(kCgStep, B - bs);
 #pragma unroll
     for (int i = 0; i < kNpt; ++i) {
@@ -1385,8 +1356,8 @@ __global__ __launch_bounds__(512) void dwconv_dk_cg_kernel(
 #pragma unroll
     for (int i = 0; i < kNpt; ++i) {
       if (ek[i] < kCgStep) {
-        chunk_to_lds<T>(base + elds[i], st[0][i]);
-        chunk_to_lds<T>(base + sz + elds[i], st[1][i]);
+        chunk_to_lds(base + elds[i], st[0][i]);
+        chunk_to_lds(base + sz + elds[i], st[1][i]);
       }
     }
   };
@@ -1505,7 +1476,7 @@ __global__ __launch_bounds__(512) void dwconv_dk_bf16mma_kernel(
   constexpr int NT = G::nt;
   constexpr int CPW = kCgChannelsPerWave;
   constexpr int STEP = kBmStep;
-  constexpr int EPC = ChunkOf<uint16_t>::n;  // 8 values per 16-byte chunk
+  constexpr int EPC = 8;                     // BF16 values per 16-byte chunk
   constexpr int ROW = kBmRow(LMAX);
   constexpr int TSZ = STEP * ROW;            // one tensor's stage in a region
   constexpr int REGION = 2 * 2 * TSZ;        // one wave's region
