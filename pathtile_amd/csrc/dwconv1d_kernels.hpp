@@ -808,6 +808,16 @@ __device__ __forceinline__ uint32_t bf16_bits_rne(float f) {
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Two FP32 values as packed BF16 (a in the low half), round-to-nearest-even:
+// one v_cvt_pk_bf16_f32 on gfx950.
+__device__ __forceinline__ uint32_t bf16_pack2(float a, float b) {
+  const uint32_t lo = __builtin_bit_cast(uint16_t, (__bf16)a);
+  const uint32_t hi = __builtin_bit_cast(uint16_t, (__bf16)b);
+  return lo | (hi << 16);
+}
+
 // A 16-byte chunk (4 FP32 values) between registers and LDS.
 __device__ __forceinline__ void chunk_to_lds(float* dst, const u32x4 v) {
   *reinterpret_cast<float4*>(dst) =
@@ -950,17 +960,17 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
 #pragma unroll
       for (int u = 0; u < NU; ++u) a[u] = u + NU * kk < L ? a[u] : 0.0f;
     }
+    // The MFMA computes the transposed tile (taps as A, rows as B; each lane
+    // supplies the same values either way), so lane (jj, kk) holds output
+    // columns 16 tt + 4 kk .. + 3 of sample jj: one 16-byte LDS write.
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int u = 0; u < NU; ++u)
-        d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], bt[u][tt], d, 0, 0, 0);
-      const int t = 16 * tt + jj;
-      if (t < L) {
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) o[(rq + rr) * sk + cb + t] = d[rr];
-      }
+        d = __builtin_amdgcn_mfma_f32_16x16x4f32(bt[u][tt], a[u], d, 0, 0, 0);
+      const int t = 16 * tt + rq;  // L % 4 == 0: all four columns or none
+      if (t < L) *reinterpret_cast<f32x4*>(o + jj * sk + cb + t) = d;
     }
   };
 
@@ -1124,19 +1134,24 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_bf16mma_kernel(
       a[u] = *reinterpret_cast<const s16x4*>(src + 4 * u);
       if (L != LMAX && NUB * kg + 4 * u >= L) a[u] = s16x4{0, 0, 0, 0};
     }
+    // The MFMA computes the transposed tile (taps as A, rows as B; each lane
+    // supplies the same values either way), so lane (jj, kg) holds output
+    // columns 16 tt + 4 kg .. + 3 of sample jj: two packed conversions and
+    // one 8-byte LDS write.
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int u = 0; u < NG; ++u) {
-        d = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a[u], bh[u][tt], d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a[u], bl[u][tt], d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bh[u][tt], a[u], d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bl[u][tt], a[u], d, 0, 0, 0);
       }
-      const int t = 16 * tt + jj;
+      const int t = 16 * tt + rq;  // L % 4 == 0: all four columns or none
       if (t < L) {
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          o[(rq + rr) * sko + cb + t] = (uint16_t)bf16_bits_rne(d[rr]);
+        u32x2 v;
+        v.x = bf16_pack2(d[0], d[1]);
+        v.y = bf16_pack2(d[2], d[3]);
+        *reinterpret_cast<u32x2*>(o + jj * sko + cb + t) = v;
       }
     }
   };
