@@ -33,6 +33,7 @@ SOURCES = [
     "inst_bf16.hip",
     "inst_dk_cl.hip",
     "inst_long.hip",
+    "inst_long_vec.hip",
 ]
 INCLUDE = ROOT / "include"
 BUILD_DIR = PKG / "_build"

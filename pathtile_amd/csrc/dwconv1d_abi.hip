@@ -660,7 +660,8 @@ static int rows_long_path(bool dx, const float* in, const float* w, float* out,
   if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
   void* args[] = {&in, &w, &out, &B, &H, &L, &K};
   const int ki = (K + 63) / 64 - 1;  // tap bucket of 64
-  return launch((const void*)kRowsLongTable[dx ? 1 : 0][li][ki], (uint32_t)nb,
+  const bool vec = L % 4 == 0 && aligned(in, 16) && aligned(out, 16);
+  return launch((const void*)(vec ? kRowsLongTableVec : kRowsLongTable)[dx ? 1 : 0][li][ki], (uint32_t)nb,
                 kLongRowsWaves * kWave, lds, stream, args);
 }
 

@@ -1847,8 +1847,11 @@ __host__ __device__ constexpr size_t rows_long_lds_bytes(int lmax) {
          sizeof(float);
 }
 
-// KB: tap-count bucket (K <= KB, a multiple of 64).
-template <int LMAX, int KB, bool DX>
+// KB: tap-count bucket (K <= KB, a multiple of 64). VEC: rows move as
+// 16-byte chunks (L % 4 == 0, 16-byte aligned tensors), else as dwords; both
+// non-temporal (the rows are touched once). 16-byte moves measured 6-11%
+// faster than dwords at L = 64 and 192 on MI355X.
+template <int LMAX, int KB, bool DX, bool VEC>
 __global__ __launch_bounds__(kLongRowsWaves * kWave) void dwconv_rows_long_kernel(
     const float* __restrict__ in, const float* __restrict__ w,
     float* __restrict__ out, int B, int H, int L, int K) {
@@ -1856,6 +1859,7 @@ __global__ __launch_bounds__(kLongRowsWaves * kWave) void dwconv_rows_long_kerne
   constexpr int NU = LMAX / 4;    // 4-column MFMA steps
   constexpr int RS = long_row_stride(LMAX);
   constexpr int NC = LMAX / kWave;  // row chunks of 64 floats (LMAX % 64 == 0)
+  constexpr int kLongChunks = 16 * LMAX / 4 / kWave;  // 16-byte chunks per lane
   extern __shared__ float lds[];
   float* const wl = lds + kLongRowsWaves * 16 * RS;  // tap window
 
@@ -1878,19 +1882,36 @@ __global__ __launch_bounds__(kLongRowsWaves * kWave) void dwconv_rows_long_kerne
     const __amdgpu_buffer_rsrc_t rs =
         make_rsrc(in + ((size_t)(b0 < B ? b0 : 0) * (size_t)H + (size_t)h) * (size_t)L);
     const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
-    float v[16][NC];
+    if constexpr (VEC) {
+      u32x4 v[kLongChunks];
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int col = c * kWave + lane;
-        const uint32_t off = (i < nrow && col < L) ? (uint32_t)i * row_bytes + 4u * (uint32_t)col : kOob;
-        v[i][c] = buf_load1(rs, off, 0);
+      for (int c = 0; c < kLongChunks; ++c) {
+        const int e = c * kWave + lane;
+        const int i = e / (LMAX / 4), q = e - i * (LMAX / 4);
+        const uint32_t off = (i < nrow && 4 * q < L) ? (uint32_t)i * row_bytes + 16u * (uint32_t)q : kOob;
+        v[c] = buf_load_chunk<kCpolNT>(rs, off);
       }
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
+      for (int c = 0; c < kLongChunks; ++c) {
+        const int e = c * kWave + lane;
+        const int i = e / (LMAX / 4), q = e - i * (LMAX / 4);
+        chunk_to_lds(xr + i * RS + 4 * q, v[c]);
+      }
+    } else {
+      float v[16][NC];
 #pragma unroll
-      for (int c = 0; c < NC; ++c) xr[i * RS + c * kWave + lane] = v[i][c];
+      for (int i = 0; i < 16; ++i)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int col = c * kWave + lane;
+          const uint32_t off = (i < nrow && col < L) ? (uint32_t)i * row_bytes + 4u * (uint32_t)col : kOob;
+          v[i][c] = buf_load1<kCpolNT>(rs, off, 0);
+        }
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) xr[i * RS + c * kWave + lane] = v[i][c];
+    }
   }
   __syncthreads();  // taps and rows in place
 
@@ -1950,14 +1971,24 @@ __global__ __launch_bounds__(kLongRowsWaves * kWave) void dwconv_rows_long_kerne
     const __amdgpu_buffer_rsrc_t ro =
         make_rsrc(out + ((size_t)(b0 < B ? b0 : 0) * (size_t)H + (size_t)h) * (size_t)L);
     const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
+    if constexpr (VEC) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int col = c * kWave + lane;
-        const uint32_t off = (i < nrow && col < L) ? (uint32_t)i * row_bytes + 4u * (uint32_t)col : kOob;
-        buf_store1(xr[i * RS + col], ro, off);
+      for (int c = 0; c < kLongChunks; ++c) {
+        const int e = c * kWave + lane;
+        const int i = e / (LMAX / 4), q = e - i * (LMAX / 4);
+        const uint32_t off = (i < nrow && 4 * q < L) ? (uint32_t)i * row_bytes + 16u * (uint32_t)q : kOob;
+        buf_store_chunk<kCpolNT>(lds_to_chunk(xr + i * RS + 4 * q), ro, off);
       }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int col = c * kWave + lane;
+          const uint32_t off = (i < nrow && col < L) ? (uint32_t)i * row_bytes + 4u * (uint32_t)col : kOob;
+          buf_store1<kCpolNT>(xr[i * RS + col], ro, off);
+        }
+    }
   }
 }
 

@@ -150,3 +150,20 @@ def test_long_rows_reference_benchmark_shape(rt):
             conv += vd[None, :, j:j + 1] * xs[:, :, j:j + L]
         rhs += float((dyd[c0:c0 + 2048].double() * conv).sum())
     assert abs(lhs - rhs) <= 1e-5 * float((gk.double().cpu().abs() * v.abs()).sum())
+
+
+def test_long_rows_misaligned_tensors_take_the_dword_path(rt):
+    """L % 4 == 0 but a 4-byte aligned (not 16-byte) view: the dword-move
+    kernel serves it, with the same results as the aligned call."""
+    B, H, L, K = 24, 4, 96, 33
+    x, w, dy = oracle.make_inputs(B, H, L, K, seed=18)
+    buf = torch.empty(B * H * L + 1, device="cuda")
+    xm = buf[1:].view(B, H, L)
+    xm.copy_(x.cuda())
+    assert xm.data_ptr() % 16 != 0
+    y = torch.empty(B * H * L + 1, device="cuda")[1:].view(B, H, L)
+    rt.launch_fwd_long(xm, w.cuda(), y)
+    y2 = torch.empty(B, H, L, device="cuda")
+    rt.launch_fwd_long(x.cuda(), w.cuda(), y2)
+    assert torch.equal(y, y2)
+    assert oracle.normalized_max_abs(y.cpu().numpy(), oracle.fwd_f64(x, w)) < FWD_TOL
