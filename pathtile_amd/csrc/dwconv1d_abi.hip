@@ -973,7 +973,8 @@ int pt_dwconv1d_dk_long_f32(const float* dy, const float* x, float* dk,
   float* partials = (float*)workspace;
   int nranges = (int)nr, det = 1;
   void* args[] = {&dy, &x, &partials, &B, &H, &L, &K, &nranges, &det};
-  st = pt::launch((const void*)pt::kDkLongTable[li], (uint32_t)nb,
+  const bool vec = L % 4 == 0 && pt::aligned(dy, 16) && pt::aligned(x, 16);
+  st = pt::launch((const void*)pt::kDkLongTable[vec ? 1 : 0][li], (uint32_t)nb,
                   (uint32_t)((lmax / 16) * pt::kWave), pt::dk_long_lds_bytes(lmax),
                   stream, args);
   if (st != PT_OK) return st;

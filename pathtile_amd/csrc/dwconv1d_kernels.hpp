@@ -2017,7 +2017,9 @@ __host__ __device__ constexpr size_t dk_long_lds_bytes(int lmax) {
          sizeof(float);
 }
 
-template <int LMAX>
+// VEC: each thread stages one 16-byte chunk per tensor and step (L % 4 == 0,
+// 16-byte aligned tensors), else four dwords.
+template <int LMAX, bool VEC>
 __global__ __launch_bounds__((LMAX / 16) * kWave) void dwconv_dk_long_kernel(
     const float* __restrict__ gy, const float* __restrict__ x,
     float* __restrict__ dst, int B, int H, int L, int K, int nranges, int det) {
@@ -2042,15 +2044,19 @@ __global__ __launch_bounds__((LMAX / 16) * kWave) void dwconv_dk_long_kernel(
   const int p = K >> 1;
   const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
 
-  // Loop-invariant part of each staged dword: sample row, column, LDS slot.
-  int erow[kNpt], ecol[kNpt];
+  // Loop-invariant part of each staged dword (or 16-byte chunk): sample
+  // row, first column.
+  constexpr int NE = VEC ? 1 : kNpt;       // loads per thread and tensor
+  constexpr int EW = VEC ? 4 : 1;          // floats per load
+  int erow[NE], ecol[NE];
 #pragma unroll
-  for (int i = 0; i < kNpt; ++i) {
+  for (int i = 0; i < NE; ++i) {
     const int e = i * NTH + (int)threadIdx.x;
-    erow[i] = e / LMAX;
-    ecol[i] = e - (e / LMAX) * LMAX;
+    erow[i] = e / (LMAX / EW);
+    ecol[i] = EW * (e - erow[i] * (LMAX / EW));
   }
-  float stg[2][kNpt];
+  u32x4 stv[2][NE];  // VEC
+  float stg[2][NE];  // dwords
   auto load_step = [&](int s) {
     const int bs = (r + s * nranges) * 16;
     const size_t r0 = ((size_t)bs * (size_t)H + (size_t)h) * (size_t)L;
@@ -2058,20 +2064,30 @@ __global__ __launch_bounds__((LMAX / 16) * kWave) void dwconv_dk_long_kernel(
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + r0);
     const int klim = min(16, B - bs);
 #pragma unroll
-    for (int i = 0; i < kNpt; ++i) {
+    for (int i = 0; i < NE; ++i) {
       const uint32_t o = (erow[i] < klim && ecol[i] < L)
                              ? (uint32_t)erow[i] * row_bytes + 4u * (uint32_t)ecol[i]
                              : kOob;
-      stg[0][i] = buf_load1<kCpolNT>(rg, o, 0);
-      stg[1][i] = buf_load1<kCpolNT>(rx, o, 0);
+      if constexpr (VEC) {
+        stv[0][i] = buf_load_chunk<kCpolNT>(rg, o);
+        stv[1][i] = buf_load_chunk<kCpolNT>(rx, o);
+      } else {
+        stg[0][i] = buf_load1<kCpolNT>(rg, o, 0);
+        stg[1][i] = buf_load1<kCpolNT>(rx, o, 0);
+      }
     }
   };
   auto store_stage = [&](int buf) {
     float* base = lds + buf * 2 * SZ;
 #pragma unroll
-    for (int i = 0; i < kNpt; ++i) {
-      base[erow[i] * RS + ecol[i]] = stg[0][i];
-      base[SZ + erow[i] * RS + ecol[i]] = stg[1][i];
+    for (int i = 0; i < NE; ++i) {
+      if constexpr (VEC) {
+        chunk_to_lds(base + erow[i] * RS + ecol[i], stv[0][i]);
+        chunk_to_lds(base + SZ + erow[i] * RS + ecol[i], stv[1][i]);
+      } else {
+        base[erow[i] * RS + ecol[i]] = stg[0][i];
+        base[SZ + erow[i] * RS + ecol[i]] = stg[1][i];
+      }
     }
   };
 

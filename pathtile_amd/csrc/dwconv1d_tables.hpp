@@ -51,7 +51,7 @@ using RowsLongFn = void (*)(const float*, const float*, float*, int, int, int, i
 using DkLongFn = void (*)(const float*, const float*, float*, int, int, int, int, int, int);
 extern const RowsLongFn kRowsLongTable[2][3][4];
 extern const RowsLongFn kRowsLongTableVec[2][3][4];
-extern const DkLongFn kDkLongTable[3];
+extern const DkLongFn kDkLongTable[2][3];
 extern const DkBf16Fn kDkBf16mmaTable[3];
 extern const DkBf16Fn kDkBf16mmaTableNT[3];
 

@@ -17,6 +17,10 @@ const RowsLongFn kRowsLongTable[2][3][4] = {
         {&dwconv_rows_long_kernel<192, 64, true, false>, &dwconv_rows_long_kernel<192, 128, true, false>, &dwconv_rows_long_kernel<192, 192, true, false>, &dwconv_rows_long_kernel<192, 256, true, false>},
     },
 };
-const DkLongFn kDkLongTable[3] = {&dwconv_dk_long_kernel<64>, &dwconv_dk_long_kernel<128>,
-                                  &dwconv_dk_long_kernel<192>};
+// DK: [16-byte staging][row bucket]
+const DkLongFn kDkLongTable[2][3] = {
+    {&dwconv_dk_long_kernel<64, false>, &dwconv_dk_long_kernel<128, false>,
+     &dwconv_dk_long_kernel<192, false>},
+    {&dwconv_dk_long_kernel<64, true>, &dwconv_dk_long_kernel<128, true>,
+     &dwconv_dk_long_kernel<192, true>}};
 }  // namespace pt
