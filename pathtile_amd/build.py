@@ -34,6 +34,8 @@ SOURCES = [
     "inst_dk_cl.hip",
     "inst_long.hip",
     "inst_long_vec.hip",
+    "inst_long_s3.hip",
+    "inst_long_s3_vec.hip",
 ]
 INCLUDE = ROOT / "include"
 BUILD_DIR = PKG / "_build"

@@ -647,6 +647,14 @@ static int check_long_shape(int B, int H, int L, int K) {
 
 static int long_index(int L) { return (L + 63) / 64 - 1; }  // row bucket of 64
 
+// Long-row FWD / DX algorithm: the BF16 matrix cores on three-way split
+// operands (default), or the FP32 matrix-core instructions
+// (PATHTILE_LONG_ALGO=fp32). Both are within FP32 rounding of the exact sums.
+static bool long_split_algo() {
+  const char* env = getenv("PATHTILE_LONG_ALGO");
+  return !(env && strcmp(env, "fp32") == 0);
+}
+
 static int rows_long_path(bool dx, const float* in, const float* w, float* out,
                           int B, int H, int L, int K, void* stream) {
   int st = check_long_shape(B, H, L, K);
@@ -655,13 +663,21 @@ static int rows_long_path(bool dx, const float* in, const float* w, float* out,
   if (!in || !w || !out) return PT_ERR_NULL;
   if (!aligned(in, 4) || !aligned(w, 4) || !aligned(out, 4)) return PT_ERR_ALIGN;
   const int li = long_index(L);
-  const size_t lds = rows_long_lds_bytes(64 * (li + 1));
+  const int ki = (K + 63) / 64 - 1;  // tap bucket of 64
+  const int di = dx ? 1 : 0;
+  const bool vec = L % 4 == 0 && aligned(in, 16) && aligned(out, 16);
+  if (long_split_algo()) {
+    const long long nb = (long long)H * (((long long)B + kLongS3Waves * 16 - 1) / (kLongS3Waves * 16));
+    if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
+    void* args[] = {&in, &w, &out, &B, &H, &L, &K};
+    return launch((const void*)(vec ? kRowsLongS3TableVec : kRowsLongS3Table)[di][li][ki],
+                  (uint32_t)nb, kLongS3Waves * kWave, kRowsLongS3Lds[di][li][ki], stream, args);
+  }
   const long long nb = (long long)H * (((long long)B + kLongRowsWaves * 16 - 1) / (kLongRowsWaves * 16));
   if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
   void* args[] = {&in, &w, &out, &B, &H, &L, &K};
-  const int ki = (K + 63) / 64 - 1;  // tap bucket of 64
-  const bool vec = L % 4 == 0 && aligned(in, 16) && aligned(out, 16);
-  return launch((const void*)(vec ? kRowsLongTableVec : kRowsLongTable)[dx ? 1 : 0][li][ki], (uint32_t)nb,
+  const size_t lds = rows_long_lds_bytes(64 * (li + 1));
+  return launch((const void*)(vec ? kRowsLongTableVec : kRowsLongTable)[di][li][ki], (uint32_t)nb,
                 kLongRowsWaves * kWave, lds, stream, args);
 }
 

@@ -1847,6 +1847,83 @@ __host__ __device__ constexpr size_t rows_long_lds_bytes(int lmax) {
          sizeof(float);
 }
 
+// A wave's 16 rows b0 .. b0 + 15 of channel h -> LDS rows xr[i * RS], columns
+// >= L and rows >= B as zeros; VEC moves 16-byte chunks (L % 4 == 0 and
+// 16-byte aligned tensors), otherwise dwords, both non-temporal.
+template <int LMAX, bool VEC>
+__device__ __forceinline__ void long_rows_to_lds(float* xr, const float* in, int b0,
+                                                 int h, int B, int H, int L, int lane) {
+  constexpr int RS = long_row_stride(LMAX);
+  constexpr int NC = LMAX / kWave;                    // row chunks of 64 floats
+  constexpr int kLongChunks = 16 * LMAX / 4 / kWave;  // 16-byte chunks per lane
+  const int nrow = min(16, B - b0);
+  const __amdgpu_buffer_rsrc_t rs =
+      make_rsrc(in + ((size_t)(b0 < B ? b0 : 0) * (size_t)H + (size_t)h) * (size_t)L);
+  const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
+  if constexpr (VEC) {
+    u32x4 v[kLongChunks];
+#pragma unroll
+    for (int c = 0; c < kLongChunks; ++c) {
+      const int e = c * kWave + lane;
+      const int i = e / (LMAX / 4), q = e - i * (LMAX / 4);
+      const uint32_t off = (i < nrow && 4 * q < L) ? (uint32_t)i * row_bytes + 16u * (uint32_t)q : kOob;
+      v[c] = buf_load_chunk<kCpolNT>(rs, off);
+    }
+#pragma unroll
+    for (int c = 0; c < kLongChunks; ++c) {
+      const int e = c * kWave + lane;
+      const int i = e / (LMAX / 4), q = e - i * (LMAX / 4);
+      chunk_to_lds(xr + i * RS + 4 * q, v[c]);
+    }
+  } else {
+    float v[16][NC];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int col = c * kWave + lane;
+        const uint32_t off = (i < nrow && col < L) ? (uint32_t)i * row_bytes + 4u * (uint32_t)col : kOob;
+        v[i][c] = buf_load1<kCpolNT>(rs, off, 0);
+      }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) xr[i * RS + c * kWave + lane] = v[i][c];
+  }
+}
+
+// The wave's 16 result rows in xr -> out (rows < B, columns < L), as the
+// loads above. The caller orders its LDS writes before (wave_lds_sync).
+template <int LMAX, bool VEC>
+__device__ __forceinline__ void long_rows_from_lds(const float* xr, float* out, int b0,
+                                                   int h, int B, int H, int L, int lane) {
+  constexpr int RS = long_row_stride(LMAX);
+  constexpr int NC = LMAX / kWave;
+  constexpr int kLongChunks = 16 * LMAX / 4 / kWave;
+  const int nrow = min(16, B - b0);
+  const __amdgpu_buffer_rsrc_t ro =
+      make_rsrc(out + ((size_t)(b0 < B ? b0 : 0) * (size_t)H + (size_t)h) * (size_t)L);
+  const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
+  if constexpr (VEC) {
+#pragma unroll
+    for (int c = 0; c < kLongChunks; ++c) {
+      const int e = c * kWave + lane;
+      const int i = e / (LMAX / 4), q = e - i * (LMAX / 4);
+      const uint32_t off = (i < nrow && 4 * q < L) ? (uint32_t)i * row_bytes + 16u * (uint32_t)q : kOob;
+      buf_store_chunk<kCpolNT>(lds_to_chunk(xr + i * RS + 4 * q), ro, off);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int col = c * kWave + lane;
+        const uint32_t off = (i < nrow && col < L) ? (uint32_t)i * row_bytes + 4u * (uint32_t)col : kOob;
+        buf_store1<kCpolNT>(xr[i * RS + col], ro, off);
+      }
+  }
+}
+
 // KB: tap-count bucket (K <= KB, a multiple of 64). VEC: rows move as
 // 16-byte chunks (L % 4 == 0, 16-byte aligned tensors), else as dwords; both
 // non-temporal (the rows are touched once). 16-byte moves measured 6-11%
@@ -1858,8 +1935,6 @@ __global__ __launch_bounds__(kLongRowsWaves * kWave) void dwconv_rows_long_kerne
   constexpr int NT = LMAX / 16;   // output tiles
   constexpr int NU = LMAX / 4;    // 4-column MFMA steps
   constexpr int RS = long_row_stride(LMAX);
-  constexpr int NC = LMAX / kWave;  // row chunks of 64 floats (LMAX % 64 == 0)
-  constexpr int kLongChunks = 16 * LMAX / 4 / kWave;  // 16-byte chunks per lane
   extern __shared__ float lds[];
   float* const wl = lds + kLongRowsWaves * 16 * RS;  // tap window
 
@@ -1877,42 +1952,7 @@ __global__ __launch_bounds__(kLongRowsWaves * kWave) void dwconv_rows_long_kerne
 
   // This wave's 16 rows: columns >= L (and rows past B) are zero.
   float* const xr = lds + wave * 16 * RS;
-  {
-    const int nrow = min(16, B - b0);
-    const __amdgpu_buffer_rsrc_t rs =
-        make_rsrc(in + ((size_t)(b0 < B ? b0 : 0) * (size_t)H + (size_t)h) * (size_t)L);
-    const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
-    if constexpr (VEC) {
-      u32x4 v[kLongChunks];
-#pragma unroll
-      for (int c = 0; c < kLongChunks; ++c) {
-        const int e = c * kWave + lane;
-        const int i = e / (LMAX / 4), q = e - i * (LMAX / 4);
-        const uint32_t off = (i < nrow && 4 * q < L) ? (uint32_t)i * row_bytes + 16u * (uint32_t)q : kOob;
-        v[c] = buf_load_chunk<kCpolNT>(rs, off);
-      }
-#pragma unroll
-      for (int c = 0; c < kLongChunks; ++c) {
-        const int e = c * kWave + lane;
-        const int i = e / (LMAX / 4), q = e - i * (LMAX / 4);
-        chunk_to_lds(xr + i * RS + 4 * q, v[c]);
-      }
-    } else {
-      float v[16][NC];
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const int col = c * kWave + lane;
-          const uint32_t off = (i < nrow && col < L) ? (uint32_t)i * row_bytes + 4u * (uint32_t)col : kOob;
-          v[i][c] = buf_load1<kCpolNT>(rs, off, 0);
-        }
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-#pragma unroll
-        for (int c = 0; c < NC; ++c) xr[i * RS + c * kWave + lane] = v[i][c];
-    }
-  }
+  long_rows_to_lds<LMAX, VEC>(xr, in, b0, h, B, H, L, lane);
   __syncthreads();  // taps and rows in place
 
   const int jj = lane & 15, kk = lane >> 4;
@@ -1966,30 +2006,201 @@ __global__ __launch_bounds__(kLongRowsWaves * kWave) void dwconv_rows_long_kerne
 #pragma unroll
     for (int r = 0; r < 4; ++r) xr[(rq + r) * RS + 16 * tt + jj] = acc[tt][r];
   wave_lds_sync();
-  {
-    const int nrow = min(16, B - b0);
-    const __amdgpu_buffer_rsrc_t ro =
-        make_rsrc(out + ((size_t)(b0 < B ? b0 : 0) * (size_t)H + (size_t)h) * (size_t)L);
-    const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
-    if constexpr (VEC) {
+  long_rows_from_lds<LMAX, VEC>(xr, out, b0, h, B, H, L, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Long rows, FWD / DX on the BF16 matrix cores at FP32 accuracy.
+//
+// Every FP32 operand v (row element or tap) is split into three BF16 parts,
+// hi = bf16(v), mid = bf16(v - hi), lo = bf16(v - hi - mid), each rounded to
+// nearest even; both differences are exact in FP32, so |v - hi - mid - lo|
+// <= 2^-27 |v|. Of the nine part products of x w, the six with hi hi,
+// hi mid, mid hi, mid mid, hi lo and lo hi carry every term above
+// 2^-25 |x w|; each is exact in FP32 and the matrix cores sum them in FP32.
+// This is the bf16x6 scheme of Henry, Tang and Heinecke, "Leveraging the
+// bfloat16 artificial intelligence datatype for higher-precision
+// computations" (ARITH 2019). On MI355X v_mfma_f32_16x16x32_bf16 measured
+// 9.3x the multiply-adds per cycle of v_mfma_f32_16x16x4_f32 (independent
+// accumulators, every SIMD busy), so six of them cost 1.5x less than the
+// FP32 instructions for the same products.
+//
+// Mapping (per wave and tile: one channel, 16 samples): the MFMA computes
+// the transposed tile, M = 16 output columns 16 tt + m, N = the 16 samples,
+// K = 32 input columns. Lane l (m = l % 16, g = l / 16) gives its eight K
+// slots i the input columns s_i = 32 c + 4 g + i (i < 4) and
+// 32 c + 16 + 4 g + (i - 4) (i >= 4), two 16-byte LDS reads. Lane l
+// supplies the taps joining s_i to output column 16 tt + m as A and
+// x[sample m][s_i] as B, and receives output columns 16 tt + 4 g .. + 3 of
+// sample m. A lane's tap index for slot i < 4 is
+//   FWD j = 16 d + (4 g - m + p) + i,   DX j = -16 d + (m - 4 g + p) - i,
+// with d = 2 c - tt, and 16 more (FWD) or less (DX) for slot i + 4. The walk
+// runs over diagonals d: per diagonal and part two 8-byte LDS reads, then
+// six MFMAs for each tile on it (tt = 2 c - d, compile-time). The taps are
+// split once per workgroup into a zero-padded window held as four copies
+// shifted by 0 .. 3 values, so each run of four consecutive taps is one
+// aligned 8-byte vector of one copy.
+// The diagonal range covers every tap count up to KB; the zero padding makes
+// out-of-band diagonals multiply by zero without a branch around any MFMA.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// Three-way BF16 split of eight FP32 values (round to nearest even).
+__device__ __forceinline__ void split3_bf16x8(const float (&v)[8], bf16x8& hi,
+                                              bf16x8& mid, bf16x8& lo) {
 #pragma unroll
-      for (int c = 0; c < kLongChunks; ++c) {
-        const int e = c * kWave + lane;
-        const int i = e / (LMAX / 4), q = e - i * (LMAX / 4);
-        const uint32_t off = (i < nrow && 4 * q < L) ? (uint32_t)i * row_bytes + 16u * (uint32_t)q : kOob;
-        buf_store_chunk<kCpolNT>(lds_to_chunk(xr + i * RS + 4 * q), ro, off);
+  for (int i = 0; i < 8; ++i) {
+    const __bf16 h = (__bf16)v[i];
+    const float r1 = v[i] - (float)h;
+    const __bf16 m = (__bf16)r1;
+    const float r2 = r1 - (float)m;
+    hi[i] = h;
+    mid[i] = m;
+    lo[i] = (__bf16)r2;
+  }
+}
+
+// Diagonal range of the split kernel for row bucket LMAX and tap bucket KB
+// (p <= KB / 2, K <= KB). A diagonal is in a call's band when some lane
+// and slot on it has 0 <= j < K:
+//   FWD j in 16 d + p + [-15, 31],  DX j in -16 d + p + [-31, 15].
+template <int LMAX, int KB, bool DX>
+struct LongSplitDiag {
+  static constexpr int NT = LMAX / 16, NC = LMAX / 32, PB = KB / 2;
+  static constexpr int lo_band = DX ? floor_div(-PB - 15, 16) : floor_div(-PB - 16, 16);
+  static constexpr int hi_band = DX ? floor_div(PB + 15, 16) : floor_div(PB + 14, 16);
+  static constexpr int D0 = lo_band > -(NT - 1) ? lo_band : -(NT - 1);
+  static constexpr int D1 = hi_band < 2 * (NC - 1) ? hi_band : 2 * (NC - 1);
+  // The tap window spans taps j in [-WLO, WHI] (zero outside [0, K)): every
+  // tap a lane reads on the diagonals [D0, D1].
+  static constexpr int WLO = DX ? 16 * D1 + 31 : 15 - 16 * D0;
+  static constexpr int WHI = DX ? -16 * D0 + 15 + PB : 16 * D1 + 31 + PB;
+  static constexpr int WN = WLO + WHI + 1;
+  // Copy length: a lane reads positions e0 .. e0 + 3 and e0 + 16 .. + 19
+  // <= WN - 1 of copy e0 % 4 from index e0 - e0 % 4, so a copy spans WN + 3
+  // values (rounded to whole 16-byte vectors).
+  static constexpr int WNP = (WN + 3 + 7) / 8 * 8;
+};
+
+constexpr int kLongS3Waves = 4;  // waves per workgroup of the split kernel
+constexpr int kLongS3MinWaves = 2;  // resident waves per SIMD the registers allow
+
+// LDS of the split kernel: the rows of its waves, then the split tap window
+// (3 parts x 4 copies).
+template <int LMAX, int KB, bool DX>
+__host__ __device__ constexpr size_t rows_long_s3_lds_bytes() {
+  return (size_t)kLongS3Waves * 16 * long_row_stride(LMAX) * sizeof(float) +
+         (size_t)3 * 4 * LongSplitDiag<LMAX, KB, DX>::WNP * sizeof(__bf16);
+}
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+// Slots 0 .. 3 from w[0 .. 3] and slots 4 .. 7 from w[16 .. 19] (8-byte
+// aligned LDS reads).
+__device__ __forceinline__ bf16x8 tap_runs(const __bf16* w) {
+  const bf16x4 a = *reinterpret_cast<const bf16x4*>(w);
+  const bf16x4 b = *reinterpret_cast<const bf16x4*>(w + 16);
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// A workgroup owns one channel and kLongS3Waves tiles of 16 samples (one per
+// wave). Each wave stages its rows in LDS (whole-row 16-byte moves), takes
+// its B operands from there, and returns the results through the same
+// region to coalesced stores.
+template <int LMAX, int KB, bool DX, bool VEC>
+__global__ __launch_bounds__(kLongS3Waves * kWave, kLongS3MinWaves) void dwconv_rows_long_s3_kernel(
+    const float* __restrict__ in, const float* __restrict__ w,
+    float* __restrict__ out, int B, int H, int L, int K) {
+  using G = LongSplitDiag<LMAX, KB, DX>;
+  constexpr int NT = G::NT, NC = G::NC;
+  constexpr int WNP = G::WNP;
+  constexpr int RS = long_row_stride(LMAX);
+  extern __shared__ float lds[];
+  // Split tap window after the rows: part q (hi, mid, lo) of copy r holds
+  // window position e + r at index e. FWD position e is tap e - WLO, DX
+  // position e is tap WHI - e (reversed, so a lane's DX taps also run
+  // upwards).
+  __bf16* const wsp = reinterpret_cast<__bf16*>(lds + kLongS3Waves * 16 * RS);
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int h = (int)(blockIdx.x % (uint32_t)H);
+  const int b0 = (int)(blockIdx.x / (uint32_t)H) * (kLongS3Waves * 16) + wave * 16;
+  const int p = K >> 1;
+
+  for (int e = threadIdx.x; e < WNP; e += kLongS3Waves * kWave) {
+    const int j = DX ? G::WHI - e : e - G::WLO;
+    const float v = (e < G::WN && j >= 0 && j < K) ? w[(size_t)h * K + j] : 0.0f;
+    const __bf16 hi = (__bf16)v;
+    const float r1 = v - (float)hi;
+    const __bf16 mid = (__bf16)r1;
+    const __bf16 lo = (__bf16)(r1 - (float)mid);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (e - c >= 0) {
+        wsp[(0 * 4 + c) * WNP + e - c] = hi;
+        wsp[(1 * 4 + c) * WNP + e - c] = mid;
+        wsp[(2 * 4 + c) * WNP + e - c] = lo;
       }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const int col = c * kWave + lane;
-          const uint32_t off = (i < nrow && col < L) ? (uint32_t)i * row_bytes + 4u * (uint32_t)col : kOob;
-          buf_store1<kCpolNT>(xr[i * RS + col], ro, off);
-        }
     }
   }
+  float* const xr = lds + wave * 16 * RS;
+  long_rows_to_lds<LMAX, VEC>(xr, in, b0, h, B, H, L, lane);
+  __syncthreads();  // window and rows in place
+
+  const int m = lane & 15, g = lane >> 4;
+  // B operands: x[sample m][s_i], split once.
+  bf16x8 xh[NC], xm[NC], xl[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const float* src = xr + m * RS + 32 * c + 4 * g;
+    const float4 v0 = *reinterpret_cast<const float4*>(src);
+    const float4 v1 = *reinterpret_cast<const float4*>(src + 16);
+    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    split3_bf16x8(v, xh[c], xm[c], xl[c]);
+  }
+  // Window position of the lane's slot 0 on diagonal d: e0 = eb + 16 d (slot
+  // 4: e0 + 16), read from copy eb % 4 (16 d is a multiple of 4) at the
+  // 8-byte aligned index e0 - eb % 4.
+  const int eb = DX ? G::WHI - (m - 4 * g + p) : G::WLO + (4 * g - m + p);
+  const int rc = eb & 3;
+  const __bf16* const wh = wsp + (0 * 4 + rc) * WNP + (eb - rc);
+  const __bf16* const wm = wsp + (1 * 4 + rc) * WNP + (eb - rc);
+  const __bf16* const wlo = wsp + (2 * 4 + rc) * WNP + (eb - rc);
+
+  f32x4 acc[NT];
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int d = G::D0; d <= G::D1; ++d) {
+    const bf16x8 th = tap_runs(wh + 16 * d);
+    const bf16x8 tm = tap_runs(wm + 16 * d);
+    const bf16x8 tl = tap_runs(wlo + 16 * d);
+    // Six products per tile, each a pass over the diagonal's tiles
+    // (independent accumulators back to back).
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+      const bf16x8 av = (q == 0 || q == 1 || q == 4) ? th : (q == 5 ? tl : tm);
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) {
+        const int c2 = d + tt;  // 2 c, compile-time
+        if (c2 >= 0 && c2 < 2 * NC && (c2 & 1) == 0) {
+          const int c = c2 >> 1;
+          const bf16x8 bv = (q == 0 || q == 2 || q == 5) ? xh[c] : (q == 4 ? xl[c] : xm[c]);
+          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[tt], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // Lane l holds output columns 16 tt + 4 g .. + 3 of sample m: one 16-byte
+  // LDS write per tile into this wave's region (its B reads are complete:
+  // LDS operations of one wave run in order), then coalesced stores.
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt)
+    *reinterpret_cast<f32x4*>(xr + m * RS + 16 * tt + 4 * g) = acc[tt];
+  wave_lds_sync();
+  long_rows_from_lds<LMAX, VEC>(xr, out, b0, h, B, H, L, lane);
 }
 
 // ---------------------------------------------------------------------------

@@ -51,6 +51,9 @@ using RowsLongFn = void (*)(const float*, const float*, float*, int, int, int, i
 using DkLongFn = void (*)(const float*, const float*, float*, int, int, int, int, int, int);
 extern const RowsLongFn kRowsLongTable[2][3][4];
 extern const RowsLongFn kRowsLongTableVec[2][3][4];
+extern const RowsLongFn kRowsLongS3Table[2][3][4];
+extern const RowsLongFn kRowsLongS3TableVec[2][3][4];
+extern const size_t kRowsLongS3Lds[2][3][4];
 extern const DkLongFn kDkLongTable[2][3];
 extern const DkBf16Fn kDkBf16mmaTable[3];
 extern const DkBf16Fn kDkBf16mmaTableNT[3];

@@ -1,0 +1,21 @@
+// Instantiates the long-row FWD / DX kernels on the BF16 matrix cores with
+// three-way split operands, 16-byte row moves (L % 4 == 0, 16-byte
+// aligned tensors).
+#include "dwconv1d_kernels.hpp"
+#include "dwconv1d_tables.hpp"
+
+namespace pt {
+// [dx][row bucket][tap bucket]
+const RowsLongFn kRowsLongS3TableVec[2][3][4] = {
+    {
+        {&dwconv_rows_long_s3_kernel<64, 64, false, true>, &dwconv_rows_long_s3_kernel<64, 128, false, true>, &dwconv_rows_long_s3_kernel<64, 192, false, true>, &dwconv_rows_long_s3_kernel<64, 256, false, true>},
+        {&dwconv_rows_long_s3_kernel<128, 64, false, true>, &dwconv_rows_long_s3_kernel<128, 128, false, true>, &dwconv_rows_long_s3_kernel<128, 192, false, true>, &dwconv_rows_long_s3_kernel<128, 256, false, true>},
+        {&dwconv_rows_long_s3_kernel<192, 64, false, true>, &dwconv_rows_long_s3_kernel<192, 128, false, true>, &dwconv_rows_long_s3_kernel<192, 192, false, true>, &dwconv_rows_long_s3_kernel<192, 256, false, true>},
+    },
+    {
+        {&dwconv_rows_long_s3_kernel<64, 64, true, true>, &dwconv_rows_long_s3_kernel<64, 128, true, true>, &dwconv_rows_long_s3_kernel<64, 192, true, true>, &dwconv_rows_long_s3_kernel<64, 256, true, true>},
+        {&dwconv_rows_long_s3_kernel<128, 64, true, true>, &dwconv_rows_long_s3_kernel<128, 128, true, true>, &dwconv_rows_long_s3_kernel<128, 192, true, true>, &dwconv_rows_long_s3_kernel<128, 256, true, true>},
+        {&dwconv_rows_long_s3_kernel<192, 64, true, true>, &dwconv_rows_long_s3_kernel<192, 128, true, true>, &dwconv_rows_long_s3_kernel<192, 192, true, true>, &dwconv_rows_long_s3_kernel<192, 256, true, true>},
+    },
+};
+}  // namespace pt

@@ -47,10 +47,21 @@ SHAPES = [
 ]
 
 
+@pytest.fixture(params=["split", "fp32"])
+def long_algo(request, monkeypatch):
+    """FWD/dX algorithm of the long path: BF16 matrix cores on three-way
+    split operands (default) or the FP32 matrix-core instructions."""
+    if request.param == "fp32":
+        monkeypatch.setenv("PATHTILE_LONG_ALGO", "fp32")
+    else:
+        monkeypatch.delenv("PATHTILE_LONG_ALGO", raising=False)
+    return request.param
+
+
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "B{}H{}L{}K{}".format(*s))
-def test_long_fwd_dx_dk_against_fp64(rt, shape):
+def test_long_fwd_dx_dk_against_fp64(rt, shape, long_algo):
     B, H, L, K = shape
-    print(f"[case] long rows B={B} H={H} L={L} K={K}", flush=True)
+    print(f"[case] long rows B={B} H={H} L={L} K={K} {long_algo}", flush=True)
     x, w, dy = oracle.make_inputs(B, H, L, K, seed=15000 + B + L + K)
     xd, wd, dyd = x.cuda(), w.cuda(), dy.cuda()
     y = torch.full_like(xd, float("nan"))
@@ -70,6 +81,34 @@ def test_long_fwd_dx_dk_against_fp64(rt, shape):
         lo, hi = oracle.valid_tap_range(L, K, j)
         if hi <= lo:
             assert torch.all(g1[:, j] == 0)
+
+
+@pytest.mark.parametrize("shape", [(32, 4, 192, 192), (24, 3, 130, 77), (16, 2, 61, 256)],
+                         ids=lambda s: "B{}H{}L{}K{}".format(*s))
+def test_long_fwd_dx_wide_exponent_range(rt, shape, long_algo):
+    """Inputs and taps with random exponents over 2^-40 .. 2^40 and full
+    FP32 mantissas: every element within 1e-5 of the FP64 sum relative to
+    that element's sum of |w| |x| (the FP32 bound of a K-term dot product,
+    with a wide margin). A dropped split part (2^-8 of a product) or a
+    mis-scaled one fails it by orders of magnitude."""
+    B, H, L, K = shape
+    print(f"[case] long rows wide exponents B={B} H={H} L={L} K={K} {long_algo}", flush=True)
+    g = np.random.default_rng(19 + L)
+
+    def wide(*shape):
+        m = g.uniform(1.0, 2.0, size=shape) * g.choice([-1.0, 1.0], size=shape)
+        return torch.from_numpy((m * np.exp2(g.integers(-40, 41, size=shape))).astype(np.float32))
+
+    x, w = wide(B, H, L), wide(H, K)
+    y = torch.empty(B, H, L, device="cuda")
+    dx = torch.empty(B, H, L, device="cuda")
+    rt.launch_fwd_long(x.cuda(), w.cuda(), y)
+    rt.launch_bwd_input_long(x.cuda(), w.cuda(), dx)
+    ax, aw = x.abs(), w.abs()
+    for out, ref, bound in ((y, oracle.fwd_f64(x, w), oracle.fwd_f64(ax, aw)),
+                            (dx, oracle.dx_f64(x, w), oracle.dx_f64(ax, aw))):
+        err = np.abs(out.cpu().numpy().astype(np.float64) - ref)
+        assert np.all(err <= 1e-5 * bound)
 
 
 def test_long_rows_on_short_shapes_match_the_specialised_path(rt):
