@@ -647,12 +647,26 @@ static int check_long_shape(int B, int H, int L, int K) {
 
 static int long_index(int L) { return (L + 63) / 64 - 1; }  // row bucket of 64
 
-// Long-row FWD / DX algorithm: the BF16 matrix cores on three-way split
-// operands (default), or the FP32 matrix-core instructions
-// (PATHTILE_LONG_ALGO=fp32). Both are within FP32 rounding of the exact sums.
-static bool long_split_algo() {
+// Long-row algorithm: the BF16 matrix cores on three-way split operands, or
+// the FP32 matrix-core instructions. Both are within FP32 rounding of the
+// exact sums. FWD / DX split everywhere (never slower on MI355X); DK splits
+// where the band spans at least half the row (2 K >= L): with fewer taps a
+// row meets few tiles, and the split kernel's fixed per-step work (gather,
+// split, publish, two barriers) made it up to 11% slower at L = 192,
+// K = 33. PATHTILE_LONG_ALGO=fp32 forces the FP32 kernels, =split the split
+// ones.
+static int long_algo_env() {
   const char* env = getenv("PATHTILE_LONG_ALGO");
-  return !(env && strcmp(env, "fp32") == 0);
+  if (env && strcmp(env, "fp32") == 0) return 0;
+  if (env && strcmp(env, "split") == 0) return 1;
+  return -1;
+}
+
+static bool long_split_algo() { return long_algo_env() != 0; }
+
+static bool long_dk_split(int L, int K) {
+  const int e = long_algo_env();
+  return e < 0 ? 2 * K >= L : e == 1;
 }
 
 static int rows_long_path(bool dx, const float* in, const float* w, float* out,
@@ -681,14 +695,16 @@ static int rows_long_path(bool dx, const float* in, const float* w, float* out,
                 kLongRowsWaves * kWave, lds, stream, args);
 }
 
-// Long-row DK: one workgroup per (channel, interleaved 16-sample range); the
-// range count aims at kLongDkTarget workgroups (two per CU of MI355X) and
-// depends on the shape only, so the workspace size does too.
+// Long-row DK: one workgroup per (channel, interleaved range of sample
+// steps); the range count aims at kLongDkTarget workgroups (two per CU of
+// MI355X), at most one per 32 samples (the split kernel's step; the FP32
+// kernel's 16-sample steps then number at least two per range), and depends
+// on the shape only, so the workspace size does too.
 constexpr long long kLongDkTarget = 512;
 
 static long long long_dk_ranges(int B, int H) {
   long long nr = (kLongDkTarget + H - 1) / (H > 0 ? H : 1);
-  const long long tsteps = ((long long)B + 15) / 16;
+  const long long tsteps = ((long long)B + 31) / 32;
   if (nr > tsteps) nr = tsteps;
   return nr < 1 ? 1 : nr;
 }
@@ -990,8 +1006,10 @@ int pt_dwconv1d_dk_long_f32(const float* dy, const float* x, float* dk,
   int nranges = (int)nr, det = 1;
   void* args[] = {&dy, &x, &partials, &B, &H, &L, &K, &nranges, &det};
   const bool vec = L % 4 == 0 && pt::aligned(dy, 16) && pt::aligned(x, 16);
-  st = pt::launch((const void*)pt::kDkLongTable[vec ? 1 : 0][li], (uint32_t)nb,
-                  (uint32_t)((lmax / 16) * pt::kWave), pt::dk_long_lds_bytes(lmax),
+  const bool split = pt::long_dk_split(L, K);
+  st = pt::launch((const void*)(split ? pt::kDkLongS3Table : pt::kDkLongTable)[vec ? 1 : 0][li],
+                  (uint32_t)nb, (uint32_t)((lmax / 16) * pt::kWave),
+                  split ? pt::dk_long_s3_lds_bytes(lmax) : pt::dk_long_lds_bytes(lmax),
                   stream, args);
   if (st != PT_OK) return st;
   int ncoef = H * K;

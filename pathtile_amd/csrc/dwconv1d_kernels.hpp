@@ -2383,4 +2383,214 @@ __global__ __launch_bounds__((LMAX / 16) * kWave) void dwconv_dk_long_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Long rows: DK on the BF16 matrix cores at FP32 accuracy (the three-way
+// split and six part products of the split FWD / DX kernel). D[t][s] =
+// sum_b dy[b,h,t] x[b,h,s] with v_mfma_f32_16x16x32_bf16, K = 32 samples:
+// lane (m, g) holds A[m][8 g + i] = dy[sample 8 g + i][16 a + m] and
+// B[8 g + i][n] = x[sample 8 g + i][16 bb + n] (n = m = l % 16), and
+// receives D[16 a + 4 g + r][16 bb + n], the layout of the FP32 kernel, so
+// the epilogue is the same.
+// A workgroup owns one channel and the interleaved 32-sample steps r,
+// r + nranges, ...; wave a owns D tile row a. Both tensors' 32 rows of a
+// step sit in LDS as FP32 (double buffered, coalesced 16-byte loads two
+// steps ahead). Per step, wave a gathers column tile a of both, keeps the
+// dy parts (its A operands) in registers and publishes the x parts in lane
+// order for every wave (one split per element, not one per wave that uses
+// it); after a barrier it multiplies by the published parts of the tiles of
+// row a that meet the band. (Interleaving four tiles' MFMAs, or double
+// buffering the publication behind a single stage, measured 10-12% slower
+// on MI355X.)
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr int long_dk_s3_row_stride(int lmax) { return lmax + 2; }
+
+__host__ __device__ constexpr size_t dk_long_s3_lds_bytes(int lmax) {
+  // stages [2][2 tensors][32][RS] floats, publication [3][LMAX / 16][64][8]
+  // BF16, the epilogue's per-wave tap sums [LMAX / 16][kLongMaxK] floats
+  return (size_t)2 * 2 * 32 * long_dk_s3_row_stride(lmax) * sizeof(float) +
+         (size_t)3 * (lmax / 16) * 64 * 8 * sizeof(__bf16) +
+         (size_t)(lmax / 16) * kLongMaxK * sizeof(float);
+}
+
+// VEC: rows move as 16-byte chunks (L % 4 == 0, 16-byte aligned tensors),
+// else as dwords.
+template <int LMAX, bool VEC>
+__global__ __launch_bounds__((LMAX / 16) * kWave) void dwconv_dk_long_s3_kernel(
+    const float* __restrict__ gy, const float* __restrict__ x,
+    float* __restrict__ dst, int B, int H, int L, int K, int nranges, int det) {
+  constexpr int NT = LMAX / 16;
+  constexpr int NTH = NT * kWave;
+  constexpr int RS = long_dk_s3_row_stride(LMAX);
+  constexpr int SZ = 32 * RS;                 // one tensor's stage (floats)
+  constexpr int PUB = 3 * NT * 64;            // the publication (bf16x8)
+  constexpr int NE = VEC ? 2 : 8;             // loads per thread, tensor and step
+  constexpr int EW = VEC ? 4 : 1;             // floats per load
+  constexpr int DS = LMAX + 1;                // epilogue D-row stride
+  // waves per epilogue round: D rows go through the stages and publication
+  constexpr int kRound = (4 * SZ + PUB * 4) / (16 * DS);
+  static_assert(32 * LMAX == NE * EW * NTH, "whole rows per thread slice");
+  static_assert(kRound >= 1, "staging area holds one wave's D rows");
+  extern __shared__ float lds[];
+  bf16x8* const pub = reinterpret_cast<bf16x8*>(lds + 4 * SZ);  // [3][NT][64]
+  float* const part = lds + 4 * SZ + PUB * 4;                   // [NT][kLongMaxK]
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int a = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // tile row
+  const int h = (int)(blockIdx.x % (uint32_t)H);
+  const int r = (int)(blockIdx.x / (uint32_t)H);
+  const int tsteps = (B + 31) / 32;
+  const int nsteps = r < tsteps ? (tsteps - 1 - r) / nranges + 1 : 0;
+  const int p = K >> 1;
+  const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
+  const int g = lane >> 4, col = lane & 15;
+
+  // Staging: loop-invariant sample row and first column of each load.
+  int erow[NE], ecol[NE];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) {
+    const int e = i * NTH + (int)threadIdx.x;
+    erow[i] = e / (LMAX / EW);
+    ecol[i] = EW * (e - erow[i] * (LMAX / EW));
+  }
+  u32x4 stv[2][NE];  // VEC
+  float stg[2][NE];  // dwords
+  auto load_step = [&](int s) {
+    const int bs = (r + s * nranges) * 32;
+    const size_t r0 = ((size_t)bs * (size_t)H + (size_t)h) * (size_t)L;
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(gy + r0);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + r0);
+    const int klim = min(32, B - bs);
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const uint32_t o = (erow[i] < klim && ecol[i] < L)
+                             ? (uint32_t)erow[i] * row_bytes + 4u * (uint32_t)ecol[i]
+                             : kOob;
+      if constexpr (VEC) {
+        stv[0][i] = buf_load_chunk<kCpolNT>(rg, o);
+        stv[1][i] = buf_load_chunk<kCpolNT>(rx, o);
+      } else {
+        stg[0][i] = buf_load1<kCpolNT>(rg, o, 0);
+        stg[1][i] = buf_load1<kCpolNT>(rx, o, 0);
+      }
+    }
+  };
+  // Rows are 8-byte aligned (RS even): 16-byte chunks go in as two halves.
+  auto store_stage = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        float* d = lds + (2 * buf + t) * SZ + erow[i] * RS + ecol[i];
+        if constexpr (VEC) {
+          const u32x4 v = stv[t][i];
+          *reinterpret_cast<float2*>(d) = make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
+          *reinterpret_cast<float2*>(d + 2) = make_float2(__uint_as_float(v.z), __uint_as_float(v.w));
+        } else {
+          *d = stg[t][i];
+        }
+      }
+    }
+  };
+  // Column 16 a + col of samples 8 g .. + 7 of tensor t in stage buf, split.
+  auto gather_split = [&](int buf, int t, bf16x8& hi, bf16x8& mid, bf16x8& lo) {
+    const float* src = lds + (2 * buf + t) * SZ + (8 * g) * RS + 16 * a + col;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = src[i * RS];
+    split3_bf16x8(v, hi, mid, lo);
+  };
+
+  auto in_band = [&](int bb) {
+    const int lo = 16 * (bb - a) - 15;
+    return lo + 30 >= -p && lo <= K - 1 - p && 16 * bb < L && 16 * a < L;
+  };
+  f32x4 acc[NT];
+#pragma unroll
+  for (int bb = 0; bb < NT; ++bb) acc[bb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto mfma_step = [&](int buf) {
+    bf16x8 ah, am, al;
+    gather_split(buf, 0, ah, am, al);
+    {
+      bf16x8 xh, xm, xl;
+      gather_split(buf, 1, xh, xm, xl);
+      pub[(0 * NT + a) * 64 + lane] = xh;
+      pub[(1 * NT + a) * 64 + lane] = xm;
+      pub[(2 * NT + a) * 64 + lane] = xl;
+    }
+    __syncthreads();  // every wave's x parts published
+#pragma unroll
+    for (int bb = 0; bb < NT; ++bb) {
+      if (in_band(bb)) {
+        const bf16x8 bh = pub[(0 * NT + bb) * 64 + lane];
+        const bf16x8 bm = pub[(1 * NT + bb) * 64 + lane];
+        const bf16x8 bl = pub[(2 * NT + bb) * 64 + lane];
+        acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc[bb], 0, 0, 0);
+        acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bm, acc[bb], 0, 0, 0);
+        acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bh, acc[bb], 0, 0, 0);
+        acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bm, acc[bb], 0, 0, 0);
+        acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc[bb], 0, 0, 0);
+        acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc[bb], 0, 0, 0);
+      }
+    }
+  };
+
+  if (nsteps > 0) {
+    load_step(0);
+    store_stage(0);
+    if (1 < nsteps) load_step(1);
+    __syncthreads();
+    for (int s0 = 0; s0 < nsteps; s0 += 2) {
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const int s = s0 + d;
+        if (s < nsteps) {
+          mfma_step(d);
+          if (s + 1 < nsteps) {
+            store_stage(d ^ 1);
+            if (s + 2 < nsteps) load_step(s + 2);
+          }
+          // Stage s + 1 in place, and every wave's reads of the publication
+          // of step s complete before step s + 1 overwrites it.
+          __syncthreads();
+        }
+      }
+    }
+  }
+
+  // Epilogue rounds: waves [q, q + kRound) put their D rows in the staging
+  // area (slot a - q), then sum their diagonals in order of t.
+  for (int q = 0; q < NT; q += kRound) {
+    const bool mine = a >= q && a < q + kRound;
+    float* const blk = lds + (mine ? a - q : 0) * 16 * DS;
+    if (mine) {
+#pragma unroll
+      for (int bb = 0; bb < NT; ++bb)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) blk[(4 * g + rr) * DS + 16 * bb + col] = acc[bb][rr];
+    }
+    __syncthreads();
+    if (mine) {
+      for (int jb = 0; jb < K; jb += kWave) {
+        const int j = jb + lane;
+        float v = 0.0f;
+        for (int tr = 0; tr < 16; ++tr) {
+          const int t = 16 * a + tr;
+          const int sc = t + j - p;
+          if (j < K && t < L && sc >= 0 && sc < L) v += blk[tr * DS + sc];
+        }
+        if (j < K) part[a * kLongMaxK + j] = v;
+      }
+    }
+    __syncthreads();
+  }
+  for (int j = threadIdx.x; j < K; j += NTH) {
+    float v = 0.0f;
+    for (int aa = 0; aa < NT; ++aa) v += part[aa * kLongMaxK + j];
+    if (det)
+      dst[((size_t)h * K + j) * (size_t)nranges + r] = v;
+    else
+      atomicAdd(dst + (size_t)h * K + j, v);
+  }
+}
+
 }  // namespace pt

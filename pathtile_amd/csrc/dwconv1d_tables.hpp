@@ -55,6 +55,7 @@ extern const RowsLongFn kRowsLongS3Table[2][3][4];
 extern const RowsLongFn kRowsLongS3TableVec[2][3][4];
 extern const size_t kRowsLongS3Lds[2][3][4];
 extern const DkLongFn kDkLongTable[2][3];
+extern const DkLongFn kDkLongS3Table[2][3];
 extern const DkBf16Fn kDkBf16mmaTable[3];
 extern const DkBf16Fn kDkBf16mmaTableNT[3];
 

@@ -23,4 +23,10 @@ const DkLongFn kDkLongTable[2][3] = {
      &dwconv_dk_long_kernel<192, false>},
     {&dwconv_dk_long_kernel<64, true>, &dwconv_dk_long_kernel<128, true>,
      &dwconv_dk_long_kernel<192, true>}};
+// DK on the BF16 matrix cores with split operands: [16-byte staging][row bucket]
+const DkLongFn kDkLongS3Table[2][3] = {
+    {&dwconv_dk_long_s3_kernel<64, false>, &dwconv_dk_long_s3_kernel<128, false>,
+     &dwconv_dk_long_s3_kernel<192, false>},
+    {&dwconv_dk_long_s3_kernel<64, true>, &dwconv_dk_long_s3_kernel<128, true>,
+     &dwconv_dk_long_s3_kernel<192, true>}};
 }  // namespace pt

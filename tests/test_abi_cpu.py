@@ -182,7 +182,7 @@ def test_long_row_validation_and_workspace(lib):
     """Long-row entry points: L up to 192 and K up to 256, then NULL / 4-byte alignment
     / workspace checks before any device work; the DK workspace is
     [H, K, ranges] floats with ranges = ceil(512 / H), at most one per
-    16-sample step (a function of B and H only)."""
+    32 samples (a function of B and H only)."""
     from pathtile_amd import _lib
 
     buf = (ctypes.c_ubyte * 4096)()
@@ -203,14 +203,16 @@ def test_long_row_validation_and_workspace(lib):
     out = ctypes.c_size_t(0)
 
     def ranges(B, H):
-        return max(1, min(-(-512 // H), -(-B // 16)))
+        return max(1, min(-(-512 // H), -(-B // 32)))
 
     for (B, H, L, K) in [(16384, 128, 192, 192), (16384, 64, 192, 3), (100, 1000, 64, 64),
                          (40, 8, 176, 256), (1, 3, 1, 1), (4096, 512, 128, 48)]:
         assert lib.pt_dwconv1d_dk_long_workspace_bytes(B, H, L, K, ctypes.byref(out)) == _lib.PT_OK
         assert out.value == H * K * ranges(B, H) * 4, (B, H, L, K)
     lib.pt_dwconv1d_dk_long_workspace_bytes(16384, 128, 192, 192, ctypes.byref(out))
-    assert out.value == 128 * 192 * 4 * 4  # 4 ranges of 16-sample steps
+    assert out.value == 128 * 192 * 4 * 4  # 4 ranges
+    lib.pt_dwconv1d_dk_long_workspace_bytes(40, 128, 192, 192, ctypes.byref(out))
+    assert out.value == 128 * 192 * 2 * 4  # B = 40: two 32-sample steps, two ranges
     lib.pt_dwconv1d_dk_long_workspace_bytes(0, 128, 192, 192, ctypes.byref(out))
     assert out.value == 0
     dk = lib.pt_dwconv1d_dk_long_f32

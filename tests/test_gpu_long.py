@@ -47,14 +47,15 @@ SHAPES = [
 ]
 
 
-@pytest.fixture(params=["split", "fp32"])
+@pytest.fixture(params=["auto", "split", "fp32"])
 def long_algo(request, monkeypatch):
-    """FWD/dX algorithm of the long path: BF16 matrix cores on three-way
-    split operands (default) or the FP32 matrix-core instructions."""
-    if request.param == "fp32":
-        monkeypatch.setenv("PATHTILE_LONG_ALGO", "fp32")
-    else:
+    """Algorithm of the long path: the default choice, the BF16 matrix
+    cores on three-way split operands everywhere, or the FP32 matrix-core
+    instructions everywhere."""
+    if request.param == "auto":
         monkeypatch.delenv("PATHTILE_LONG_ALGO", raising=False)
+    else:
+        monkeypatch.setenv("PATHTILE_LONG_ALGO", request.param)
     return request.param
 
 
