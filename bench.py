@@ -452,9 +452,11 @@ def main(argv=None) -> int:
 
     # Long rows at the reference's long-row benchmark shape (kernels/
     # shared_l192.py, benchmarked at B16384 H128 L192 K192 by
-    # benchmark/benchmark_gmc_vs_shared_l192.py:14-17): FP32 on the matrix
-    # cores, bound by them rather than HBM; roofline on useful flops
-    # (2 per multiply-add that touches a real element). Same loop.
+    # benchmark/benchmark_gmc_vs_shared_l192.py:14-17). The default kernels
+    # run on the BF16 matrix cores with three-way split FP32 operands (six
+    # part products); the FP32 matrix-core kernels (PATHTILE_LONG_ALGO=fp32)
+    # are timed beside them. Useful flops: 2 per multiply-add that touches a
+    # real element. Same loop.
     LB, LH, LL, LK = 16384, 128, 192, 192
     xl = torch.randn(LB, LH, LL, generator=torch.Generator().manual_seed(args.seed + 3)).to(dev)
     dyl = torch.randn(LB, LH, LL, generator=torch.Generator().manual_seed(args.seed + 4)).to(dev)
@@ -465,18 +467,47 @@ def main(argv=None) -> int:
         "bwd_input": lambda: rt.launch_bwd_input_long(dyl, wl, dxl),
         "bwd_weight": lambda: rt.launch_bwd_weight_long(dyl, xl, gkl, LK),
     }
-    long_ms = {ph: time_loop(fn) for ph, fn in long_loops.items()}
     from pathtile_amd.tune.baselines import useful_products
     long_flops = 2 * useful_products(LB, LH, LL, LK)
+    long_bytes = 2 * LB * LH * LL * 4 + LH * LK * 4
+
+    def long_paths(ms_by_path):
+        return {ph: {"ms": round(ms, 5),
+                     "tflops_useful": round(long_flops / (ms / 1e3) / 1e12, 2),
+                     "frac_fp32_mfma_peak": round(long_flops / (ms / 1e3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+                     "hbm_pct_peak": round(100 * long_bytes / (ms / 1e3) / 1e9 / PEAK_HBM_GBPS, 2)}
+                for ph, ms in ms_by_path.items()}
+
+    prev_long = os.environ.pop("PATHTILE_LONG_ALGO", None)
+    long_ms = {ph: time_loop(fn) for ph, fn in long_loops.items()}
+    # gate on the first 256 samples (a small copy: the profiles' copy probe
+    # is the largest plain copy of the run)
+    y_split = yl[:256].clone()
+    os.environ["PATHTILE_LONG_ALGO"] = "fp32"
+    long_ms_fp32 = {ph: time_loop(fn) for ph, fn in long_loops.items()}
+    rt.launch_fwd_long(xl, wl, yl)
+    torch.cuda.synchronize()
+    long_gate = float((y_split - yl[:256]).abs().max() / yl[:256].abs().max())
+    if prev_long is None:
+        del os.environ["PATHTILE_LONG_ALGO"]
+    else:
+        os.environ["PATHTILE_LONG_ALGO"] = prev_long
+    if not long_gate < 1e-5:
+        raise SystemExit(f"long-row split vs FP32 gate failed: {long_gate}")
     long_leg = {
         "config": {"B": LB, "H": LH, "L": LL, "K": LK},
-        "paths": {ph: {"ms": round(ms, 5),
-                       "tflops_useful": round(long_flops / (ms / 1e3) / 1e12, 2),
-                       "frac_fp32_mfma_peak": round(long_flops / (ms / 1e3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)}
-                  for ph, ms in long_ms.items()},
+        "paths": long_paths(long_ms),
         "fwd_dx_dk_ms": round(sum(long_ms.values()), 5),
-        "note": "pt_dwconv1d_{fwd,dx,dk}_long_f32; useful flops 2 * sum over rows of "
-                "real multiply-adds; peak = MI355X dense FP32 matrix 157.3 TFLOP/s",
+        "kernels": {"fwd": "dwconv_rows_long_s3_kernel<192, 192, false, true>",
+                    "bwd_input": "dwconv_rows_long_s3_kernel<192, 192, true, true>",
+                    "bwd_weight": "dwconv_dk_long_s3_kernel<192, true>"},
+        "fp32_mfma_kernels": {"paths": long_paths(long_ms_fp32),
+                              "fwd_dx_dk_ms": round(sum(long_ms_fp32.values()), 5)},
+        "gate_split_vs_fp32_fwd": float(f"{long_gate:.3e}"),
+        "note": "pt_dwconv1d_{fwd,dx,dk}_long_f32; default = BF16 matrix cores on three-way split "
+                "FP32 operands (FP32-accurate), fp32_mfma_kernels = PATHTILE_LONG_ALGO=fp32; useful "
+                "flops 2 * sum over rows of real multiply-adds; FP32 matrix peak 157.3 TFLOP/s; "
+                "HBM bytes 2 B H L 4 + H K 4 per path",
     }
     del xl, dyl, wl, yl, dxl, gkl
 
