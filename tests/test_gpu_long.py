@@ -112,6 +112,38 @@ def test_long_fwd_dx_wide_exponent_range(rt, shape, long_algo):
         assert np.all(err <= 1e-5 * bound)
 
 
+def _random_long_shapes(n, seed):
+    g = np.random.default_rng(seed)
+    return [(int(g.integers(1, 81)), int(g.integers(1, 13)), int(g.integers(1, 193)),
+             int(g.integers(1, 257))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("shape", _random_long_shapes(16, 2026), ids=lambda s: "B{}H{}L{}K{}".format(*s))
+def test_long_split_kernels_random_shapes(rt, shape, monkeypatch):
+    """The split kernels forced on seeded random shapes over the whole long
+    range (every row and tap bucket, ragged rows, K above and below L):
+    FWD/dX within 1e-5 and dK within 1e-4 of FP64."""
+    monkeypatch.setenv("PATHTILE_LONG_ALGO", "split")
+    B, H, L, K = shape
+    print(f"[case] long split random B={B} H={H} L={L} K={K}", flush=True)
+    x, w, dy = oracle.make_inputs(B, H, L, K, seed=B * 7 + L * 3 + K)
+    xd, wd, dyd = x.cuda(), w.cuda(), dy.cuda()
+    y = torch.full_like(xd, float("nan"))
+    dx = torch.full_like(dyd, float("nan"))
+    gk = torch.full((H, K), float("nan"), device="cuda")
+    rt.launch_fwd_long(xd, wd, y)
+    rt.launch_bwd_input_long(dyd, wd, dx)
+    rt.launch_bwd_weight_long(dyd, xd, gk, K)
+    assert oracle.normalized_max_abs(y.cpu().numpy(), oracle.fwd_f64(x, w)) < FWD_TOL
+    assert oracle.normalized_max_abs(dx.cpu().numpy(), oracle.dx_f64(dy, w)) < FWD_TOL
+    ref = oracle.dk_f64(dy, x, K)
+    assert oracle.normalized_max_abs(gk.cpu().numpy(), ref) < DK_TOL
+    for j in range(K):
+        lo, hi = oracle.valid_tap_range(L, K, j)
+        if hi <= lo:
+            assert torch.all(gk[:, j] == 0)
+
+
 def test_long_rows_on_short_shapes_match_the_specialised_path(rt):
     """The long kernels also serve L, K <= 48; they agree with the
     specialised kernels to the FP32 bars."""
