@@ -2014,10 +2014,13 @@ __global__ __launch_bounds__(kLongRowsWaves * kWave) void dwconv_rows_long_kerne
 //
 // Every FP32 operand v (row element or tap) is split into three BF16 parts,
 // hi = bf16(v), mid = bf16(v - hi), lo = bf16(v - hi - mid), each rounded to
-// nearest even; both differences are exact in FP32, so |v - hi - mid - lo|
-// <= 2^-27 |v|. Of the nine part products of x w, the six with hi hi,
-// hi mid, mid hi, mid mid, hi lo and lo hi carry every term above
-// 2^-25 |x w|; each is exact in FP32 and the matrix cores sum them in FP32.
+// nearest even (8 significant bits, so each step leaves at most 2^-8 of the
+// rest); both differences are exact in FP32, |mid| <= 2^-8 |v|,
+// |lo| <= 2^-16 |v| and |v - hi - mid - lo| <= 2^-24 |v|. The six part
+// products hi hi, hi mid, mid hi, mid mid, hi lo and lo hi leave out mid lo
+// and lo mid (at most 2^-24 |x w| each) and lo lo (2^-32), so a product is
+// off by at most about 2^-22 |x w|, the order of FP32 rounding. Each part
+// product is exact in FP32 and the matrix cores sum them in FP32.
 // This is the bf16x6 scheme of Henry, Tang and Heinecke, "Leveraging the
 // bfloat16 artificial intelligence datatype for higher-precision
 // computations" (ARITH 2019). On MI355X v_mfma_f32_16x16x32_bf16 measured

@@ -5,7 +5,7 @@ the reference (FP32 only).
 Bars: the inputs are BF16 values, so the exact result is the FP64 sum over
 those values (oracle.fwd_f64 / dx_f64 / dk_f64 of the widened inputs).
 FWD/dX run on the BF16 matrix cores with each FP32 tap as a hi + lo BF16
-pair (|w - hi - lo| <= 2^-18 |w|) and FP32 accumulation, then one round to
+pair (|w - hi - lo| <= 2^-16 |w|) and FP32 accumulation, then one round to
 BF16: every element within one BF16 ulp of the FP64 sum plus 2^-16 of the
 largest output (the tap split and the accumulation), and at least 99% of
 elements equal to the FP64 sum rounded to BF16 (they differ only where those
