@@ -10,8 +10,11 @@ the hand-written gfx950 kernels of ``libpathtile_hip.so``:
 * rows and taps up to 48: the specialised path (the FWD/dX kernels chosen
   per shape, the deterministic two-pass dK);
 * anything up to L = 192, K = 256: the long-row matrix-core kernels
-  (``pt_dwconv1d_{fwd,dx,dk}_long_f32``), FP32, dK deterministic and written
-  into ``gk`` as the reference's dK kernel writes it (one thread per tap,
+  (``pt_dwconv1d_{fwd,dx,dk}_long_f32``), at FP32 accuracy (by default the
+  BF16 matrix cores on FP32 operands split three ways, six exact part
+  products summed in FP32; ``PATHTILE_LONG_ALGO=fp32`` selects the FP32
+  instructions), dK deterministic and written into ``gk`` as the
+  reference's dK kernel writes it (one thread per tap,
   kernels/shared_l192.py:966-1001).
 
 Every launch is host-synchronous and its kernel time (ms, HIP events) is

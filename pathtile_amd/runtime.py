@@ -664,7 +664,8 @@ class HipWarpRuntime:
 
     def launch_fwd_long(self, x: torch.Tensor, k: torch.Tensor, y: torch.Tensor,
                         collector: KernelEventCollector | None = None) -> None:
-        """FWD for rows up to 192 with up to 256 taps (matrix cores)."""
+        """FWD for rows up to 192 with up to 256 taps (matrix cores, FP32
+        accuracy; see pt_dwconv1d_fwd_long_f32)."""
         self._check_open()
         B, H, L, K = self._check_long(x, k)
         if y.shape != x.shape or y.dtype != torch.float32 or y.device != x.device:
@@ -681,7 +682,8 @@ class HipWarpRuntime:
 
     def launch_bwd_input_long(self, gy: torch.Tensor, k: torch.Tensor, gx: torch.Tensor,
                               collector: KernelEventCollector | None = None) -> None:
-        """dX for rows up to 192 with up to 256 taps (matrix cores)."""
+        """dX for rows up to 192 with up to 256 taps (matrix cores, FP32
+        accuracy; see pt_dwconv1d_dx_long_f32)."""
         self._check_open()
         B, H, L, K = self._check_long(gy, k)
         if gx.shape != gy.shape or gx.dtype != torch.float32 or gx.device != gy.device:
