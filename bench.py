@@ -404,25 +404,43 @@ def main(argv=None) -> int:
 
     # BF16 I/O (no reference counterpart): the same workload with x, dY and
     # the FWD/dX outputs in bfloat16, taps and dK in FP32, same loops. Its
-    # algorithmic bytes are (2 B H L * 2 + H K * 4) per path.
-    xb, dyb = x.to(torch.bfloat16), dy.to(torch.bfloat16)
-    yb, dxb = torch.empty_like(xb), torch.empty_like(dyb)
-    bf16_loops = {
-        "fwd": lambda: rt.launch_fwd_bf16(xb, w, yb),
-        "bwd_input": lambda: rt.launch_bwd_input_bf16(dyb, w, dxb),
-        "bwd_weight": lambda: rt.launch_bwd_weight_bf16(dyb, xb, gk, K),
-        "bwd_weight_det": lambda: rt.launch_bwd_weight_deterministic_bf16(dyb, xb, gk, K),
-    }
-    bf16_ms = {ph: time_loop(fn) for ph, fn in bf16_loops.items()}
-    # gate: BF16 FWD against the FP32 path on the same (BF16-valued) input
-    rows_b = min(512, B)
-    y32 = torch.empty(rows_b, H, L, device=dev)
-    rt.launch_fwd(xb[:rows_b].float().contiguous(), w, y32)
-    torch.cuda.synchronize()
-    bf16_gate = float((yb[:rows_b].float() - y32).abs().max() / y32.abs().max().clamp_min(1e-30))
-    if not bf16_gate < 2.0 ** -8:
-        raise SystemExit(f"BF16 gate failed: {bf16_gate}")
-    del xb, dyb, yb, dxb, y32
+    # algorithmic bytes are (2 B H L * 2 + H K * 4) per path. The BF16 entry
+    # points serve the channel-group layout only (L % 4 == 0, H % 8 == 0 and
+    # the dK block's channel rule), so other shapes skip the leg.
+    bf16_leg = None
+    dk_channels = 2 * (rt.bwdk_block // 64)
+    if L % 4 == 0 and H % 8 == 0 and H % dk_channels == 0 and rt.bwdk_block <= 512:
+        xb, dyb = x.to(torch.bfloat16), dy.to(torch.bfloat16)
+        yb, dxb = torch.empty_like(xb), torch.empty_like(dyb)
+        bf16_loops = {
+            "fwd": lambda: rt.launch_fwd_bf16(xb, w, yb),
+            "bwd_input": lambda: rt.launch_bwd_input_bf16(dyb, w, dxb),
+            "bwd_weight": lambda: rt.launch_bwd_weight_bf16(dyb, xb, gk, K),
+            "bwd_weight_det": lambda: rt.launch_bwd_weight_deterministic_bf16(dyb, xb, gk, K),
+        }
+        bf16_ms = {ph: time_loop(fn) for ph, fn in bf16_loops.items()}
+        # gate: BF16 FWD against the FP32 path on the same (BF16-valued) input
+        rows_b = min(512, B)
+        y32 = torch.empty(rows_b, H, L, device=dev)
+        rt.launch_fwd(xb[:rows_b].float().contiguous(), w, y32)
+        torch.cuda.synchronize()
+        bf16_gate = float((yb[:rows_b].float() - y32).abs().max() / y32.abs().max().clamp_min(1e-30))
+        if not bf16_gate < 2.0 ** -8:
+            raise SystemExit(f"BF16 gate failed: {bf16_gate}")
+        del xb, dyb, yb, dxb, y32
+        bf16_bytes = 2 * B * H * L * 2 + H * K * 4
+        bf16_leg = {
+            "paths": {
+                ph: {"ms": round(ms, 5),
+                     "gbps": round(bf16_bytes / (ms / 1e3) / 1e9, 1),
+                     "pct_peak": round(100 * bf16_bytes / (ms / 1e3) / 1e9 / PEAK_HBM_GBPS, 2)}
+                for ph, ms in bf16_ms.items()
+            },
+            "fwd_dx_dk_ms": round(bf16_ms["fwd"] + bf16_ms["bwd_input"] + bf16_ms["bwd_weight"], 5),
+            "gate_vs_fp32_path": float(f"{bf16_gate:.3e}"),
+            "note": "x, dY, y, dX bfloat16; taps and dK FP32; FP32 accumulation; "
+                    "algorithmic bytes (2 B H L * 2 + H K * 4) per path",
+        }
 
     # Channels-last dK through the Flash-DWC bridge ABI (flash_dk_fp32): x and
     # dY permuted to [B, 1, L, H] outside the timed region, dw [1, K, H]
@@ -596,19 +614,7 @@ def main(argv=None) -> int:
         "algorithmic_bytes_per_path": nbytes,
         "paths": paths,
         "correctness_gate": {k: float(f"{v:.3e}") for k, v in gate.items()},
-        "bf16_io": {
-            "paths": {
-                ph: {"ms": round(ms, 5),
-                     "gbps": round((2 * B * H * L * 2 + H * K * 4) / (ms / 1e3) / 1e9, 1),
-                     "pct_peak": round(100 * (2 * B * H * L * 2 + H * K * 4) / (ms / 1e3) / 1e9
-                                       / PEAK_HBM_GBPS, 2)}
-                for ph, ms in bf16_ms.items()
-            },
-            "fwd_dx_dk_ms": round(bf16_ms["fwd"] + bf16_ms["bwd_input"] + bf16_ms["bwd_weight"], 5),
-            "gate_vs_fp32_path": float(f"{bf16_gate:.3e}"),
-            "note": "x, dY, y, dX bfloat16; taps and dK FP32; FP32 accumulation; "
-                    "algorithmic bytes (2 B H L * 2 + H K * 4) per path",
-        },
+        "bf16_io": bf16_leg,
         "channels_last_dk": cl_leg,
         "long_rows": long_leg,
         "rows_valu": {
