@@ -649,12 +649,14 @@ static int long_index(int L) { return (L + 63) / 64 - 1; }  // row bucket of 64
 
 // Long-row algorithm: the BF16 matrix cores on three-way split operands, or
 // the FP32 matrix-core instructions. Both are within FP32 rounding of the
-// exact sums. FWD / DX split everywhere (never slower on MI355X); DK splits
-// where the band spans at least half the row (2 K >= L): with fewer taps a
-// row meets few tiles, and the split kernel's fixed per-step work (gather,
-// split, publish, two barriers) made it up to 11% slower at L = 192,
-// K = 33. PATHTILE_LONG_ALGO=fp32 forces the FP32 kernels, =split the split
-// ones.
+// exact sums. FWD / DX split everywhere (never slower on MI355X). DK splits
+// from 40 taps up, and at L = 64 for any K. With fewer taps a row meets few
+// tiles, and the split kernel's fixed per-step work (gather, split,
+// publish, two barriers, for every wave of the row bucket) made it 7-18%
+// slower at (L, K) = (192, 33), (160, 33), (80, 24) and (52, 16) on MI355X;
+// at L = 64 it was 11-25% faster for K = 3 .. 64, and from K = 40 it won or
+// tied (within 2%) at L = 96 .. 192. PATHTILE_LONG_ALGO=fp32 forces the
+// FP32 kernels, =split the split ones.
 static int long_algo_env() {
   const char* env = getenv("PATHTILE_LONG_ALGO");
   if (env && strcmp(env, "fp32") == 0) return 0;
@@ -666,7 +668,7 @@ static bool long_split_algo() { return long_algo_env() != 0; }
 
 static bool long_dk_split(int L, int K) {
   const int e = long_algo_env();
-  return e < 0 ? 2 * K >= L : e == 1;
+  return e < 0 ? (K >= 40 || L == 64) : e == 1;
 }
 
 static int rows_long_path(bool dx, const float* in, const float* w, float* out,
