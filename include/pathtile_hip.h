@@ -165,7 +165,7 @@ int pt_dwconv1d_dk_det_bf16(const void* dy, const void* x, float* dk,
  *   DK   gk[h,j]   = sum_b sum_t gy[b,h,t] x[b,h,t+j-K/2]  :840-1005)
  * FP32 accuracy on the matrix cores: by default the BF16 instructions on
  * FP32 operands split three ways (six part products, each exact in FP32;
- * DK from 40 taps up and at L = 64), else the FP32 instructions; PATHTILE_LONG_ALGO=fp32
+ * DK from 40 taps up and at L = 64, 96), else the FP32 instructions; PATHTILE_LONG_ALGO=fp32
  * or =split forces one kind. FWD/DX need only 4-byte aligned tensors. DK is
  * deterministic (fixed-order partials plus a reduction, as
  * pt_dwconv1d_dk_det_f32) and overwrites dk; its workspace size depends on

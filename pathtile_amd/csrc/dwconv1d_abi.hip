@@ -645,18 +645,21 @@ static int check_long_shape(int B, int H, int L, int K) {
   return PT_OK;
 }
 
-static int long_index(int L) { return (L + 63) / 64 - 1; }  // row bucket of 64
+// Long-row buckets: LMAX = 64, 96, 128, 160, 192 (L > 64 takes the smallest
+// multiple of 32 that holds it; the kernels' work grows with LMAX, not L).
+static int long_index(int L) { return L <= 64 ? 0 : (L + 31) / 32 - 2; }
+static int long_lmax(int li) { return 32 * (li + 2); }
 
 // Long-row algorithm: the BF16 matrix cores on three-way split operands, or
 // the FP32 matrix-core instructions. Both are within FP32 rounding of the
 // exact sums. FWD / DX split everywhere (never slower on MI355X). DK splits
-// from 40 taps up, and at L = 64 for any K. With fewer taps a row meets few
-// tiles, and the split kernel's fixed per-step work (gather, split,
-// publish, two barriers, for every wave of the row bucket) made it 7-18%
-// slower at (L, K) = (192, 33), (160, 33), (80, 24) and (52, 16) on MI355X;
-// at L = 64 it was 11-25% faster for K = 3 .. 64, and from K = 40 it won or
-// tied (within 2%) at L = 96 .. 192. PATHTILE_LONG_ALGO=fp32 forces the
-// FP32 kernels, =split the split ones.
+// from 40 taps up, and at L = 64 and 96 (full small buckets) for any K. With
+// fewer taps a row meets few tiles, and the split kernel's fixed per-step
+// work (gather, split, publish, two barriers, for every wave of the row
+// bucket) made it 5-11% slower at (L, K) = (192, 33), (160, 33) and
+// (52, 16) on MI355X; at L = 64 and 96 it was 8-25% faster for every K
+// tried, and from K = 40 it won or came within 2.5%.
+// PATHTILE_LONG_ALGO=fp32 forces the FP32 kernels, =split the split ones.
 static int long_algo_env() {
   const char* env = getenv("PATHTILE_LONG_ALGO");
   if (env && strcmp(env, "fp32") == 0) return 0;
@@ -668,7 +671,7 @@ static bool long_split_algo() { return long_algo_env() != 0; }
 
 static bool long_dk_split(int L, int K) {
   const int e = long_algo_env();
-  return e < 0 ? (K >= 40 || L == 64) : e == 1;
+  return e < 0 ? (K >= 40 || L == 64 || L == 96) : e == 1;
 }
 
 static int rows_long_path(bool dx, const float* in, const float* w, float* out,
@@ -692,7 +695,7 @@ static int rows_long_path(bool dx, const float* in, const float* w, float* out,
   const long long nb = (long long)H * (((long long)B + kLongRowsWaves * 16 - 1) / (kLongRowsWaves * 16));
   if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
   void* args[] = {&in, &w, &out, &B, &H, &L, &K};
-  const size_t lds = rows_long_lds_bytes(64 * (li + 1));
+  const size_t lds = rows_long_lds_bytes(long_lmax(li));
   return launch((const void*)(vec ? kRowsLongTableVec : kRowsLongTable)[di][li][ki], (uint32_t)nb,
                 kLongRowsWaves * kWave, lds, stream, args);
 }
@@ -1003,7 +1006,7 @@ int pt_dwconv1d_dk_long_f32(const float* dy, const float* x, float* dk,
   const long long nb = (long long)H * nr;
   if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
   const int li = pt::long_index(L);
-  const int lmax = 64 * (li + 1);
+  const int lmax = pt::long_lmax(li);
   float* partials = (float*)workspace;
   int nranges = (int)nr, det = 1;
   void* args[] = {&dy, &x, &partials, &B, &H, &L, &K, &nranges, &det};

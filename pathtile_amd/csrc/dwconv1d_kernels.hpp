@@ -1854,8 +1854,9 @@ template <int LMAX, bool VEC>
 __device__ __forceinline__ void long_rows_to_lds(float* xr, const float* in, int b0,
                                                  int h, int B, int H, int L, int lane) {
   constexpr int RS = long_row_stride(LMAX);
-  constexpr int NC = LMAX / kWave;                    // row chunks of 64 floats
+  constexpr int NC = (LMAX + kWave - 1) / kWave;      // row chunks of 64 floats
   constexpr int kLongChunks = 16 * LMAX / 4 / kWave;  // 16-byte chunks per lane
+  static_assert(LMAX % 16 == 0, "whole 16-byte chunks per lane");
   const int nrow = min(16, B - b0);
   const __amdgpu_buffer_rsrc_t rs =
       make_rsrc(in + ((size_t)(b0 < B ? b0 : 0) * (size_t)H + (size_t)h) * (size_t)L);
@@ -1888,7 +1889,8 @@ __device__ __forceinline__ void long_rows_to_lds(float* xr, const float* in, int
 #pragma unroll
     for (int i = 0; i < 16; ++i)
 #pragma unroll
-      for (int c = 0; c < NC; ++c) xr[i * RS + c * kWave + lane] = v[i][c];
+      for (int c = 0; c < NC; ++c)
+        if (c * kWave + lane < LMAX) xr[i * RS + c * kWave + lane] = v[i][c];
   }
 }
 
@@ -1898,7 +1900,7 @@ template <int LMAX, bool VEC>
 __device__ __forceinline__ void long_rows_from_lds(const float* xr, float* out, int b0,
                                                    int h, int B, int H, int L, int lane) {
   constexpr int RS = long_row_stride(LMAX);
-  constexpr int NC = LMAX / kWave;
+  constexpr int NC = (LMAX + kWave - 1) / kWave;
   constexpr int kLongChunks = 16 * LMAX / 4 / kWave;
   const int nrow = min(16, B - b0);
   const __amdgpu_buffer_rsrc_t ro =
@@ -1919,7 +1921,7 @@ __device__ __forceinline__ void long_rows_from_lds(const float* xr, float* out, 
       for (int c = 0; c < NC; ++c) {
         const int col = c * kWave + lane;
         const uint32_t off = (i < nrow && col < L) ? (uint32_t)i * row_bytes + 4u * (uint32_t)col : kOob;
-        buf_store1<kCpolNT>(xr[i * RS + col], ro, off);
+        buf_store1<kCpolNT>(col < LMAX ? xr[i * RS + col] : 0.0f, ro, off);
       }
   }
 }

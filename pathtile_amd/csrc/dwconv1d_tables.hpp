@@ -49,13 +49,14 @@ using DkClFn = void (*)(const float*, const float*, float*, int, int, int, int,
 extern const DkClFn kDkClTable[3];
 using RowsLongFn = void (*)(const float*, const float*, float*, int, int, int, int);
 using DkLongFn = void (*)(const float*, const float*, float*, int, int, int, int, int, int);
-extern const RowsLongFn kRowsLongTable[2][3][4];
-extern const RowsLongFn kRowsLongTableVec[2][3][4];
-extern const RowsLongFn kRowsLongS3Table[2][3][4];
-extern const RowsLongFn kRowsLongS3TableVec[2][3][4];
-extern const size_t kRowsLongS3Lds[2][3][4];
-extern const DkLongFn kDkLongTable[2][3];
-extern const DkLongFn kDkLongS3Table[2][3];
+constexpr int kNumLongLB = 5;  // long-row buckets 64, 96, 128, 160, 192
+extern const RowsLongFn kRowsLongTable[2][kNumLongLB][4];
+extern const RowsLongFn kRowsLongTableVec[2][kNumLongLB][4];
+extern const RowsLongFn kRowsLongS3Table[2][kNumLongLB][4];
+extern const RowsLongFn kRowsLongS3TableVec[2][kNumLongLB][4];
+extern const size_t kRowsLongS3Lds[2][kNumLongLB][4];
+extern const DkLongFn kDkLongTable[2][kNumLongLB];
+extern const DkLongFn kDkLongS3Table[2][kNumLongLB];
 extern const DkBf16Fn kDkBf16mmaTable[3];
 extern const DkBf16Fn kDkBf16mmaTableNT[3];
 

@@ -5,28 +5,36 @@
 
 namespace pt {
 // [dx][row bucket][tap bucket]
-const RowsLongFn kRowsLongS3Table[2][3][4] = {
+const RowsLongFn kRowsLongS3Table[2][kNumLongLB][4] = {
     {
         {&dwconv_rows_long_s3_kernel<64, 64, false, false>, &dwconv_rows_long_s3_kernel<64, 128, false, false>, &dwconv_rows_long_s3_kernel<64, 192, false, false>, &dwconv_rows_long_s3_kernel<64, 256, false, false>},
+        {&dwconv_rows_long_s3_kernel<96, 64, false, false>, &dwconv_rows_long_s3_kernel<96, 128, false, false>, &dwconv_rows_long_s3_kernel<96, 192, false, false>, &dwconv_rows_long_s3_kernel<96, 256, false, false>},
         {&dwconv_rows_long_s3_kernel<128, 64, false, false>, &dwconv_rows_long_s3_kernel<128, 128, false, false>, &dwconv_rows_long_s3_kernel<128, 192, false, false>, &dwconv_rows_long_s3_kernel<128, 256, false, false>},
+        {&dwconv_rows_long_s3_kernel<160, 64, false, false>, &dwconv_rows_long_s3_kernel<160, 128, false, false>, &dwconv_rows_long_s3_kernel<160, 192, false, false>, &dwconv_rows_long_s3_kernel<160, 256, false, false>},
         {&dwconv_rows_long_s3_kernel<192, 64, false, false>, &dwconv_rows_long_s3_kernel<192, 128, false, false>, &dwconv_rows_long_s3_kernel<192, 192, false, false>, &dwconv_rows_long_s3_kernel<192, 256, false, false>},
     },
     {
         {&dwconv_rows_long_s3_kernel<64, 64, true, false>, &dwconv_rows_long_s3_kernel<64, 128, true, false>, &dwconv_rows_long_s3_kernel<64, 192, true, false>, &dwconv_rows_long_s3_kernel<64, 256, true, false>},
+        {&dwconv_rows_long_s3_kernel<96, 64, true, false>, &dwconv_rows_long_s3_kernel<96, 128, true, false>, &dwconv_rows_long_s3_kernel<96, 192, true, false>, &dwconv_rows_long_s3_kernel<96, 256, true, false>},
         {&dwconv_rows_long_s3_kernel<128, 64, true, false>, &dwconv_rows_long_s3_kernel<128, 128, true, false>, &dwconv_rows_long_s3_kernel<128, 192, true, false>, &dwconv_rows_long_s3_kernel<128, 256, true, false>},
+        {&dwconv_rows_long_s3_kernel<160, 64, true, false>, &dwconv_rows_long_s3_kernel<160, 128, true, false>, &dwconv_rows_long_s3_kernel<160, 192, true, false>, &dwconv_rows_long_s3_kernel<160, 256, true, false>},
         {&dwconv_rows_long_s3_kernel<192, 64, true, false>, &dwconv_rows_long_s3_kernel<192, 128, true, false>, &dwconv_rows_long_s3_kernel<192, 192, true, false>, &dwconv_rows_long_s3_kernel<192, 256, true, false>},
     },
 };
 // dynamic LDS bytes: [dx][row bucket][tap bucket]
-const size_t kRowsLongS3Lds[2][3][4] = {
+const size_t kRowsLongS3Lds[2][kNumLongLB][4] = {
     {
         {rows_long_s3_lds_bytes<64, 64, false>(), rows_long_s3_lds_bytes<64, 128, false>(), rows_long_s3_lds_bytes<64, 192, false>(), rows_long_s3_lds_bytes<64, 256, false>()},
+        {rows_long_s3_lds_bytes<96, 64, false>(), rows_long_s3_lds_bytes<96, 128, false>(), rows_long_s3_lds_bytes<96, 192, false>(), rows_long_s3_lds_bytes<96, 256, false>()},
         {rows_long_s3_lds_bytes<128, 64, false>(), rows_long_s3_lds_bytes<128, 128, false>(), rows_long_s3_lds_bytes<128, 192, false>(), rows_long_s3_lds_bytes<128, 256, false>()},
+        {rows_long_s3_lds_bytes<160, 64, false>(), rows_long_s3_lds_bytes<160, 128, false>(), rows_long_s3_lds_bytes<160, 192, false>(), rows_long_s3_lds_bytes<160, 256, false>()},
         {rows_long_s3_lds_bytes<192, 64, false>(), rows_long_s3_lds_bytes<192, 128, false>(), rows_long_s3_lds_bytes<192, 192, false>(), rows_long_s3_lds_bytes<192, 256, false>()},
     },
     {
         {rows_long_s3_lds_bytes<64, 64, true>(), rows_long_s3_lds_bytes<64, 128, true>(), rows_long_s3_lds_bytes<64, 192, true>(), rows_long_s3_lds_bytes<64, 256, true>()},
+        {rows_long_s3_lds_bytes<96, 64, true>(), rows_long_s3_lds_bytes<96, 128, true>(), rows_long_s3_lds_bytes<96, 192, true>(), rows_long_s3_lds_bytes<96, 256, true>()},
         {rows_long_s3_lds_bytes<128, 64, true>(), rows_long_s3_lds_bytes<128, 128, true>(), rows_long_s3_lds_bytes<128, 192, true>(), rows_long_s3_lds_bytes<128, 256, true>()},
+        {rows_long_s3_lds_bytes<160, 64, true>(), rows_long_s3_lds_bytes<160, 128, true>(), rows_long_s3_lds_bytes<160, 192, true>(), rows_long_s3_lds_bytes<160, 256, true>()},
         {rows_long_s3_lds_bytes<192, 64, true>(), rows_long_s3_lds_bytes<192, 128, true>(), rows_long_s3_lds_bytes<192, 192, true>(), rows_long_s3_lds_bytes<192, 256, true>()},
     },
 };

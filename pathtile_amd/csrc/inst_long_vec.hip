@@ -5,15 +5,19 @@
 
 namespace pt {
 // [dx][row bucket][tap bucket]
-const RowsLongFn kRowsLongTableVec[2][3][4] = {
+const RowsLongFn kRowsLongTableVec[2][kNumLongLB][4] = {
     {
         {&dwconv_rows_long_kernel<64, 64, false, true>, &dwconv_rows_long_kernel<64, 128, false, true>, &dwconv_rows_long_kernel<64, 192, false, true>, &dwconv_rows_long_kernel<64, 256, false, true>},
+        {&dwconv_rows_long_kernel<96, 64, false, true>, &dwconv_rows_long_kernel<96, 128, false, true>, &dwconv_rows_long_kernel<96, 192, false, true>, &dwconv_rows_long_kernel<96, 256, false, true>},
         {&dwconv_rows_long_kernel<128, 64, false, true>, &dwconv_rows_long_kernel<128, 128, false, true>, &dwconv_rows_long_kernel<128, 192, false, true>, &dwconv_rows_long_kernel<128, 256, false, true>},
+        {&dwconv_rows_long_kernel<160, 64, false, true>, &dwconv_rows_long_kernel<160, 128, false, true>, &dwconv_rows_long_kernel<160, 192, false, true>, &dwconv_rows_long_kernel<160, 256, false, true>},
         {&dwconv_rows_long_kernel<192, 64, false, true>, &dwconv_rows_long_kernel<192, 128, false, true>, &dwconv_rows_long_kernel<192, 192, false, true>, &dwconv_rows_long_kernel<192, 256, false, true>},
     },
     {
         {&dwconv_rows_long_kernel<64, 64, true, true>, &dwconv_rows_long_kernel<64, 128, true, true>, &dwconv_rows_long_kernel<64, 192, true, true>, &dwconv_rows_long_kernel<64, 256, true, true>},
+        {&dwconv_rows_long_kernel<96, 64, true, true>, &dwconv_rows_long_kernel<96, 128, true, true>, &dwconv_rows_long_kernel<96, 192, true, true>, &dwconv_rows_long_kernel<96, 256, true, true>},
         {&dwconv_rows_long_kernel<128, 64, true, true>, &dwconv_rows_long_kernel<128, 128, true, true>, &dwconv_rows_long_kernel<128, 192, true, true>, &dwconv_rows_long_kernel<128, 256, true, true>},
+        {&dwconv_rows_long_kernel<160, 64, true, true>, &dwconv_rows_long_kernel<160, 128, true, true>, &dwconv_rows_long_kernel<160, 192, true, true>, &dwconv_rows_long_kernel<160, 256, true, true>},
         {&dwconv_rows_long_kernel<192, 64, true, true>, &dwconv_rows_long_kernel<192, 128, true, true>, &dwconv_rows_long_kernel<192, 192, true, true>, &dwconv_rows_long_kernel<192, 256, true, true>},
     },
 };

@@ -44,6 +44,8 @@ SHAPES = [
     (64, 8, 130, 1),
     (5, 3, 1, 256),      # one-column rows
     (70, 2, 96, 48),
+    (12, 5, 160, 96),    # 160-column bucket, full
+    (9, 6, 80, 24),      # 96-column bucket, partial
 ]
 
 
