@@ -686,11 +686,13 @@ static int rows_long_path(bool dx, const float* in, const float* w, float* out,
   const int di = dx ? 1 : 0;
   const bool vec = L % 4 == 0 && aligned(in, 16) && aligned(out, 16);
   if (long_split_algo()) {
+    // tap buckets of 32: the diagonal walk covers the bucket's whole band
+    const int k3 = (K + 31) / 32 - 1;
     const long long nb = (long long)H * (((long long)B + kLongS3Waves * 16 - 1) / (kLongS3Waves * 16));
     if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
     void* args[] = {&in, &w, &out, &B, &H, &L, &K};
-    return launch((const void*)(vec ? kRowsLongS3TableVec : kRowsLongS3Table)[di][li][ki],
-                  (uint32_t)nb, kLongS3Waves * kWave, kRowsLongS3Lds[di][li][ki], stream, args);
+    return launch((const void*)(vec ? kRowsLongS3TableVec : kRowsLongS3Table)[di][li][k3],
+                  (uint32_t)nb, kLongS3Waves * kWave, kRowsLongS3Lds[di][li][k3], stream, args);
   }
   const long long nb = (long long)H * (((long long)B + kLongRowsWaves * 16 - 1) / (kLongRowsWaves * 16));
   if (nb >= (1LL << 31)) return PT_ERR_SHAPE;

@@ -52,9 +52,10 @@ using DkLongFn = void (*)(const float*, const float*, float*, int, int, int, int
 constexpr int kNumLongLB = 5;  // long-row buckets 64, 96, 128, 160, 192
 extern const RowsLongFn kRowsLongTable[2][kNumLongLB][4];
 extern const RowsLongFn kRowsLongTableVec[2][kNumLongLB][4];
-extern const RowsLongFn kRowsLongS3Table[2][kNumLongLB][4];
-extern const RowsLongFn kRowsLongS3TableVec[2][kNumLongLB][4];
-extern const size_t kRowsLongS3Lds[2][kNumLongLB][4];
+constexpr int kNumLongS3KB = 8;  // split FWD / DX tap buckets 32, 64, ..., 256
+extern const RowsLongFn kRowsLongS3Table[2][kNumLongLB][kNumLongS3KB];
+extern const RowsLongFn kRowsLongS3TableVec[2][kNumLongLB][kNumLongS3KB];
+extern const size_t kRowsLongS3Lds[2][kNumLongLB][kNumLongS3KB];
 extern const DkLongFn kDkLongTable[2][kNumLongLB];
 extern const DkLongFn kDkLongS3Table[2][kNumLongLB];
 extern const DkBf16Fn kDkBf16mmaTable[3];
