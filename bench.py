@@ -333,7 +333,9 @@ def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (--gpus {args.gpus} requested): the "
-              "path is a single-GPU kernel; see DESIGN.md for how it would shard.",
+              "path is built and measured as a single-GPU kernel; across GPUs it would "
+              "shard by samples (FWD/dX independent, one H*K all-reduce for dK) or by "
+              "channels (no exchange).",
               file=sys.stderr, flush=True)
         return 2
     import torch
