@@ -746,7 +746,7 @@ const char* pt_status_string(int status) {
   switch (status) {
     case PT_OK: return "ok";
     case PT_ERR_NULL: return "null pointer argument";
-    case PT_ERR_SHAPE: return "invalid shape (need 1<=L<=48, 1<=K<=48, B,H>=0, B*H*L<2^31)";
+    case PT_ERR_SHAPE: return "invalid shape (need B,H>=0, B*H*L<2^31, and L, K within the entry point's range: 1..48, or 1..192 and 1..256 for the long-row entry points)";
     case PT_ERR_CONFIG: return "unsupported launch configuration";
     case PT_ERR_WORKSPACE: return "workspace missing or too small";
     case PT_ERR_HIP: return "HIP runtime launch error";
