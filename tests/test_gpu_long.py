@@ -146,6 +146,32 @@ def test_long_split_kernels_random_shapes(rt, shape, monkeypatch):
             assert torch.all(gk[:, j] == 0)
 
 
+@pytest.mark.parametrize("shape", [(20, 6, 192, 192), (9, 4, 100, 37)], ids=lambda s: "B{}H{}L{}K{}".format(*s))
+def test_long_rows_non_finite_input_stays_in_its_channel(rt, shape, long_algo):
+    """An infinity or NaN in one channel's rows must not reach another
+    channel: the odd channels hold them, the even channels' outputs (FWD,
+    dX, dK) must equal a run without them and match FP64."""
+    B, H, L, K = shape
+    print(f"[case] long rows non-finite B={B} H={H} L={L} K={K} {long_algo}", flush=True)
+    x, w, dy = oracle.make_inputs(B, H, L, K, seed=31 + L)
+    xb, dyb = x.clone(), dy.clone()
+    xb[:, 1::2, L // 2] = float("inf")
+    xb[:, 1::2, 0] = float("nan")
+    dyb[:, 1::2, L // 3] = float("-inf")
+    y = torch.empty(B, H, L, device="cuda")
+    dx = torch.empty(B, H, L, device="cuda")
+    gk = torch.empty(H, K, device="cuda")
+    rt.launch_fwd_long(xb.cuda(), w.cuda(), y)
+    rt.launch_bwd_input_long(dyb.cuda(), w.cuda(), dx)
+    rt.launch_bwd_weight_long(dyb.cuda(), xb.cuda(), gk, K)
+    ev = slice(0, H, 2)
+    xe, dye, we = x[:, ev].contiguous(), dy[:, ev].contiguous(), w[ev].contiguous()
+    assert torch.isfinite(y[:, ev]).all() and torch.isfinite(dx[:, ev]).all() and torch.isfinite(gk[ev]).all()
+    assert oracle.normalized_max_abs(y[:, ev].cpu().numpy(), oracle.fwd_f64(xe, we)) < FWD_TOL
+    assert oracle.normalized_max_abs(dx[:, ev].cpu().numpy(), oracle.dx_f64(dye, we)) < FWD_TOL
+    assert oracle.normalized_max_abs(gk[ev].cpu().numpy(), oracle.dk_f64(dye, xe, K)) < DK_TOL
+
+
 def test_long_rows_on_short_shapes_match_the_specialised_path(rt):
     """The long kernels also serve L, K <= 48; they agree with the
     specialised kernels to the FP32 bars."""
