@@ -399,6 +399,11 @@ __global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kerne
 
   float wt[W::n];
   int hcur = -1;
+  bool tbad = false;  // a tap of this lane's channel is not finite
+  // Padded terms (elements past L, taps outside [0, K) in the bucket's
+  // window) are exact no-ops only for finite operands: 0 * Inf is NaN where
+  // the reference skips the term. Without padding no such term exists.
+  const bool padded = L != LMAX || K != KB;
 
   for (uint32_t t0 = gwave; t0 < ntiles; t0 += nwaves) {
     // readfirstlane keeps per-tile bases opaque to loop strength reduction.
@@ -458,6 +463,10 @@ __global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kerne
     if (__builtin_amdgcn_ballot_w64(h != hcur)) {
       load_lane_taps<W::lo, W::n, DX>(w, h, K, wt);
       hcur = h;
+      float ts = 0.0f;
+#pragma unroll
+      for (int i = 0; i < W::n; ++i) ts += wt[i];
+      tbad = !__builtin_isfinite(ts);
     }
 
     wave_lds_sync();
@@ -474,26 +483,57 @@ __global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kerne
 #pragma unroll
       for (int s = 0; s < LMAX; ++s) xr[s] = s < L ? xr[s] : 0.0f;
     }
+    // A row with a non-finite element (or a lane with a non-finite tap)
+    // meets a padded term: its sum is not finite.
+    bool slow = false;
+    if (padded) {
+      float xs = 0.0f;
+#pragma unroll
+      for (int s = 0; s < LMAX; ++s) xs += xr[s];
+      slow = tbad || !__builtin_isfinite(xs);
+    }
     wave_lds_sync();
 
-    // The reference's fmaf chain per output, taps in reference order
-    // (FWD: j = p + m ascending <=> i ascending; DX: j = p - m ascending
-    // <=> i descending); four outputs at a time (four independent chains)
-    // go to the lane's own row.
-#pragma unroll
-    for (int t4 = 0; t4 < LMAX; t4 += 4) {
-      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int ii = 0; ii < W::n; ++ii) {
-        const int i = DX ? (W::n - 1 - ii) : ii;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int s = t4 + u + W::lo + i;
-          if (s >= 0 && s < LMAX) acc[u] = fmaf(xr[s], wt[i], acc[u]);
+    if (__builtin_amdgcn_ballot_w64(slow)) {
+      // The reference's chain with its skipped terms, every lane of the
+      // wave (on finite rows it gives the fast path's bits). Elements come
+      // from the input tensor (rows past R read 0 and are never stored) and
+      // taps from memory, so the lane's LDS row can take each output as it
+      // is made and the path holds no row in registers.
+      const float* wh = w + (size_t)h * K;
+      const int p = K >> 1;
+      const uint32_t rowb = (uint32_t)lane * uL * 4u;
+#pragma unroll 1
+      for (int t = 0; t < L; ++t) {
+        float acc = 0.0f;
+#pragma unroll 1
+        for (int j = 0; j < K; ++j) {
+          const int e = DX ? t - j + p : t + j - p;
+          if ((unsigned)e < (unsigned)L)
+            acc = fmaf(buf_load1(rin, rowb + 4u * (uint32_t)e, 0), wh[j], acc);
         }
+        tile[lane * S + t] = acc;
       }
-      *reinterpret_cast<float4*>(tile + lane * S + t4) =
-          make_float4(acc[0], acc[1], acc[2], acc[3]);
+    } else {
+      // The reference's fmaf chain per output, taps in reference order
+      // (FWD: j = p + m ascending <=> i ascending; DX: j = p - m ascending
+      // <=> i descending); four outputs at a time (four independent chains)
+      // go to the lane's own row.
+#pragma unroll
+      for (int t4 = 0; t4 < LMAX; t4 += 4) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ii = 0; ii < W::n; ++ii) {
+          const int i = DX ? (W::n - 1 - ii) : ii;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int s = t4 + u + W::lo + i;
+            if (s >= 0 && s < LMAX) acc[u] = fmaf(xr[s], wt[i], acc[u]);
+          }
+        }
+        *reinterpret_cast<float4*>(tile + lane * S + t4) =
+            make_float4(acc[0], acc[1], acc[2], acc[3]);
+      }
     }
     wave_lds_sync();
 
@@ -859,6 +899,22 @@ __host__ __device__ constexpr size_t rows_cg_lds_bytes(int L, int hc = kRowsCgWa
 
 // kDepth: steps in flight in registers; HC: channels (= waves) per
 // workgroup.
+//
+// Non-finite values. The band matrix multiplies every input column of a
+// sample by every output column's taps, zeros included, so one Inf or NaN
+// input turns every output of its sample (in that channel) into NaN, where
+// the reference's fmaf chain touches an input only through the taps whose
+// window holds it (kernels/warp_tiled_ampere.py:411-430, :479-498). Because
+// every output's sum meets every input column, one output per lane shows
+// it: a lane whose first output is not finite recomputes its outputs with
+// the reference's chain (same start value, tap order and skipped terms)
+// from the input stage, so those outputs are bit-exact with the reference.
+// A non-finite tap needs no such care: band entries are the taps themselves
+// where the window holds an element and exact zeros elsewhere, so a
+// non-finite tap multiplies exactly the reference's terms, and a sum of
+// terms of which some are infinite or NaN has the same non-finite value in
+// any order (sums that overflow FP32 aside). A wave whose lanes all see
+// finite first outputs skips the chain.
 template <int LMAX, bool DX, int kDepth, int HC = kRowsCgWaves>
 __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
     const float* __restrict__ in, const float* __restrict__ w,
@@ -931,6 +987,7 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
   const int kk = lane >> 4, jj = lane & 15;
   const int p = K >> 1;
   const int h = g * HC + wave;
+  const float* wh = w + (size_t)h * K;
   float bt[NU][NT];
 #pragma unroll
   for (int u = 0; u < NU; ++u)
@@ -939,14 +996,15 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
       const int sc = u + NU * kk, tc = 16 * tt + jj;
       const int j = DX ? (tc - sc + p) : (sc - tc + p);
       const bool ok = j >= 0 && j < K && sc < L && tc < L;
-      bt[u][tt] = ok ? w[(size_t)h * K + j] : 0.0f;
+      bt[u][tt] = ok ? wh[j] : 0.0f;
     }
 
   const int rq = 4 * kk;
   const int cb = wave * L;
   auto mfma_step = [&](int s) {
-    const float* src = inl + (s & 1) * sz + jj * sk + cb + NU * kk;  // sample jj
-    float* o = outl + (s & 1) * sz;
+    const float* row = inl + (s & 1) * sz + jj * sk + cb;  // sample jj, this channel
+    const float* src = row + NU * kk;
+    float* orow = outl + (s & 1) * sz + jj * sk + cb;
     float a[NU];
 #pragma unroll
     for (int q = 0; q < NU / 4; ++q) {
@@ -963,14 +1021,33 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
     // The MFMA computes the transposed tile (taps as A, rows as B; each lane
     // supplies the same values either way), so lane (jj, kk) holds output
     // columns 16 tt + 4 kk .. + 3 of sample jj: one 16-byte LDS write.
+    bool bad = false;
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int u = 0; u < NU; ++u)
         d = __builtin_amdgcn_mfma_f32_16x16x4f32(bt[u][tt], a[u], d, 0, 0, 0);
+      if (tt == 0) bad = !__builtin_isfinite(d[0]);
       const int t = 16 * tt + rq;  // L % 4 == 0: all four columns or none
-      if (t < L) *reinterpret_cast<f32x4*>(o + jj * sk + cb + t) = d;
+      if (t < L) *reinterpret_cast<f32x4*>(orow + t) = d;
+    }
+    if (__builtin_amdgcn_ballot_w64(bad)) {
+      if (bad) {
+#pragma unroll 1
+        for (int q = 0; q < 4 * NT; ++q) {
+          const int t = 16 * (q >> 2) + rq + (q & 3);
+          if (t < L) {
+            float acc = 0.0f;
+#pragma unroll 1
+            for (int j = 0; j < K; ++j) {
+              const int e = DX ? t - j + p : t + j - p;
+              if ((unsigned)e < (unsigned)L) acc = fmaf(row[e], wh[j], acc);
+            }
+            orow[t] = acc;
+          }
+        }
+      }
     }
   };
 

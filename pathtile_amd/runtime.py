@@ -343,7 +343,8 @@ class HipWarpRuntime:
         self._lib = _lib.load()
         self._closed = False
         self._ws_lock = threading.Lock()
-        self._workspace: torch.Tensor | None = None
+        # (device index, stream handle) -> (stream, workspace)
+        self._workspaces: dict[tuple[int, int], tuple[Any, torch.Tensor]] = {}
 
     # ------------------------------------------------------------------ checks
     @staticmethod
@@ -471,14 +472,24 @@ class HipWarpRuntime:
 
     def _get_workspace(self, nbytes: int, device: torch.device) -> torch.Tensor:
         """Reusable byte workspace for the deterministic dK
-        (kernels/warp_tiled_noatomic_optimized.py:1448-1471). Allocated on
-        torch's caching allocator on first use and grown when needed."""
+        (kernels/warp_tiled_noatomic_optimized.py:1448-1471), one per
+        (device, stream): the launch goes to torch's current stream of the
+        device, and each stream keeps its own buffer, so launches on two
+        streams never share partials. The buffer is allocated from torch's
+        caching allocator while that stream is current, so when it is
+        replaced by a larger one, its memory returns to that stream's pool
+        and is reused only by work ordered after the launches that read it."""
+        stream = torch.cuda.current_stream(device)
+        key = (device.index if device.index is not None else torch.cuda.current_device(),
+               int(stream.cuda_stream))
         with self._ws_lock:
-            ws = self._workspace
-            if ws is None or ws.numel() < nbytes or ws.device != device:
-                ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
-                self._workspace = ws
-            return ws
+            entry = self._workspaces.get(key)
+            if entry is None or entry[1].numel() < nbytes:
+                with torch.cuda.stream(stream):
+                    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+                self._workspaces[key] = (stream, ws)
+                return ws
+            return entry[1]
 
     def launch_bwd_weight_deterministic(
         self,
@@ -778,7 +789,7 @@ class HipWarpRuntime:
             return
         if torch.cuda.is_available():
             torch.cuda.synchronize()
-        self._workspace = None
+        self._workspaces.clear()
         self._closed = True
 
 

@@ -156,6 +156,69 @@ def test_fwd_dx_matrix_core_kernel(rt, shape, monkeypatch):
     assert oracle.normalized_max_abs(dx, oracle.dx_f64(dye, we)) < FWD_TOL
 
 
+def _same_bits_or_both_nan(a, b):
+    return bool(np.all((a == b) | (np.isnan(a) & np.isnan(b))))
+
+
+@pytest.mark.parametrize("algo", ["auto", "valu", "mfma"])
+@pytest.mark.parametrize("shape", [
+    (64, 16, 48, 48),     # C1: the matrix-core kernel by default
+    (40, 8, 44, 48),      # L < row bucket
+    (33, 8, 32, 17),      # 32 bucket, ragged last step
+    (50, 16, 48, 4),      # short filter (VALU by default, matrix cores forced)
+])
+def test_nonfinite_values_reach_only_the_reference_window(rt, shape, algo, monkeypatch):
+    """Inf, -Inf and NaN in x / dY (same channel as finite rows) and in one
+    channel's taps. The reference's fmaf chain touches an element only
+    through the taps whose window holds it (kernels/warp_tiled_ampere.py:
+    411-430, 479-498), so non-finite values reach exactly the outputs in that
+    window. On every kernel: every row with a non-finite input equals the
+    oracle's FP32 chain bit for bit (NaN where it has NaN); in the channel
+    with the non-finite tap, the non-finite outputs are exactly the chain's
+    (same NaN positions, same signed infinities) and the finite ones within
+    1e-5 of it; every other row stays within 1e-5 of FP64."""
+    if algo != "auto":
+        monkeypatch.setenv("PATHTILE_ROWS_ALGO", algo)
+    B, H, L, K = shape
+    x, w, dy = _inputs(B, H, L, K, seed=6000 + B + H + L + K)
+    rng = np.random.default_rng(B + L + K)
+    bad_rows = set()
+    for t, v in zip((x, dy), (float("inf"), float("nan"))):
+        for val in (v, -float("inf"), float("nan")):
+            b, h, s = int(rng.integers(B)), int(rng.integers(H)), int(rng.integers(L))
+            t[b, h, s] = val
+            bad_rows.add((b, h))
+    hb = H - 1
+    w[hb, K // 3] = float("inf")
+    xd, wd, dyd = _dev(x, w, dy)
+    y = _fwd(rt, xd, wd).cpu().numpy()
+    dx = _dx(rt, dyd, wd).cpu().numpy()
+    y_ref, dx_ref = oracle.fwd_f32_refchain(x, w), oracle.dx_f32_refchain(dy, w)
+    for got, ref, src in ((y, y_ref, x), (dx, dx_ref, dy)):
+        exact = ~np.isfinite(src.numpy()).all(axis=2)
+        exact[:, hb] = False
+        assert exact.sum() >= 2
+        assert _same_bits_or_both_nan(got[exact], ref[exact])
+        gc, rc = got[:, hb], ref[:, hb]
+        assert np.array_equal(np.isnan(gc), np.isnan(rc))
+        assert np.array_equal(np.where(np.isinf(gc), gc, 0), np.where(np.isinf(rc), rc, 0))
+        fr = np.isfinite(rc)
+        assert fr.any() and (~fr).any()
+        assert oracle.normalized_max_abs(gc[fr], rc[fr]) < FWD_TOL
+        other = ~exact
+        other[:, hb] = False
+        assert np.isfinite(got[other]).all()
+    fin = np.ones((B, H), dtype=bool)
+    fin[:, hb] = False
+    for b, h in bad_rows:
+        fin[b, h] = False
+    xs = x.clone(); xs[~torch.from_numpy(fin)] = 0.0
+    dys = dy.clone(); dys[~torch.from_numpy(fin)] = 0.0
+    ws = w.clone(); ws[hb] = 0.0
+    assert oracle.normalized_max_abs(y[fin], oracle.fwd_f64(xs, ws)[fin]) < FWD_TOL
+    assert oracle.normalized_max_abs(dx[fin], oracle.dx_f64(dys, ws)[fin]) < FWD_TOL
+
+
 @pytest.mark.parametrize("algo", ["auto", "valu", "mfma"])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "B{}H{}L{}K{}".format(*s))
 def test_dk_atomic_and_deterministic(rt, shape, algo, monkeypatch):
