@@ -41,6 +41,10 @@ extern "C" {
 #define PT_ERR_WORKSPACE (-4)  /* workspace missing or too small             */
 #define PT_ERR_HIP (-5)        /* the HIP runtime reported a launch error    */
 #define PT_ERR_ALIGN (-6)      /* pointer not 4-byte aligned                 */
+#define PT_ERR_SCRATCH (-7)    /* the static scratch is too small (noalloc)  */
+
+/* Bytes of the static device scratch of pt_dwconv1d_dk_det_f32_noalloc. */
+#define PT_DK_SCRATCH_BYTES (8u << 20)
 
 #define PT_MAX_L 48
 #define PT_MAX_K 48
@@ -125,6 +129,25 @@ int pt_dwconv1d_dk_det_f32(const float* dy, const float* x, float* dk,
                            void* workspace, size_t workspace_bytes, int B,
                            int H, int L, int K, int threads_per_block,
                            void* stream);
+
+/*
+ * Deterministic weight gradient that allocates nothing and takes no
+ * workspace. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same kernels, partial order and
+ * result bits as pt_dwconv1d_dk_det_f32 with the same threads_per_block;
+ * the partials go to a static device array of PT_DK_SCRATCH_BYTES (8 MiB)
+ * that each device holds until the process ends. A call whose partials
+ * (H * K * 4 bytes per batch range; at most the size
+ * pt_dwconv1d_dk_det_workspace_bytes reports) exceed it returns
+ * PT_ERR_SCRATCH. Every call on a device shares that
+ * device's array: calls that overlap on one device (two streams, two host
+ * threads) race and must be ordered by the caller. Each call overwrites
+ * every partial it reads, so nothing needs clearing between calls.
+ */
+int pt_dwconv1d_dk_det_f32_noalloc(const float* dy, const float* x, float* dk,
+                                   int B, int H, int L, int K,
+                                   int threads_per_block, void* stream);
 
 /*
  * BF16 I/O variants (no counterpart in the reference, which is FP32 only).

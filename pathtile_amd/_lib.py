@@ -24,6 +24,8 @@ PT_ERR_CONFIG = -3
 PT_ERR_WORKSPACE = -4
 PT_ERR_HIP = -5
 PT_ERR_ALIGN = -6
+PT_ERR_SCRATCH = -7
+PT_DK_SCRATCH_BYTES = 8 << 20
 
 PT_KERNEL_FWD = 0
 PT_KERNEL_DX = 1
@@ -48,6 +50,7 @@ SIGNATURES = {
     "pt_dwconv1d_dk_det_f32": (
         _i, [_vp, _vp, _vp, _vp, ctypes.c_size_t, _i, _i, _i, _i, _i, _vp]
     ),
+    "pt_dwconv1d_dk_det_f32_noalloc": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "pt_dwconv1d_fwd_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "pt_dwconv1d_dx_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "pt_dwconv1d_dk_atomic_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
@@ -113,6 +116,6 @@ def check(status: int, what: str) -> None:
         return
     msg = f"{what}: {status_string(status)} (status {status})"
     if status in (PT_ERR_SHAPE, PT_ERR_CONFIG, PT_ERR_NULL, PT_ERR_ALIGN,
-                  PT_ERR_WORKSPACE):
+                  PT_ERR_WORKSPACE, PT_ERR_SCRATCH):
         raise ValueError(msg)
     raise PathTileLibraryError(msg)

@@ -716,6 +716,54 @@ static long long long_dk_ranges(int B, int H) {
   return nr < 1 ? 1 : nr;
 }
 
+// --- static scratch of the no-allocation deterministic DK -----------------
+// The partials of pt_dwconv1d_dk_det_f32_noalloc live in this array instead
+// of a caller's workspace. Each device holds its own copy for the life of
+// the process. In host code `scratch` names a host-side stand-in, not device
+// memory: kernels get the device address that hipGetSymbolAddress returns
+// for the current device, looked up once per device and cached.
+static __device__ __align__(256) float scratch[PT_DK_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static float* g_scratch_ptr[kMaxDevices];
+
+static int scratch_address(float** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return PT_ERR_HIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return PT_ERR_HIP;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return PT_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = (float*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PT_OK;
+}
+
+// Deterministic DK into `partials` (H * K * g.nbt floats), then the
+// fixed-order reduction that overwrites dk. Every partial is written by the
+// first launch, so the buffer needs no clearing.
+static int dk_det_launch(const float* dy, const float* x, float* dk,
+                         float* partials, int B, int H, int L, int K,
+                         int threads, const DkGeom& g, void* stream) {
+  int st = dk_path(true, dy, x, partials, B, H, L, K, threads, g, stream);
+  if (st != PT_OK) return st;
+  int ncoef = H * K;
+  int nbt = g.nbt;
+  const float* cp = partials;
+  void* args[] = {&cp, &dk, &ncoef, &nbt};
+  const uint32_t grid = (uint32_t)((ncoef + 3) / 4);
+  return launch((const void*)&dk_reduce_kernel, grid, 256, 0, stream, args);
+}
+
 static const void* kernel_for(int kernel_id, int L, int K) {
   if (L < 1 || L > kMaxL || K < 1 || K > kMaxK) return nullptr;
   const int li = lbucket_index(L), ki = kbucket_index(K);
@@ -751,6 +799,7 @@ const char* pt_status_string(int status) {
     case PT_ERR_WORKSPACE: return "workspace missing or too small";
     case PT_ERR_HIP: return "HIP runtime launch error";
     case PT_ERR_ALIGN: return "pointer not 4-byte aligned";
+    case PT_ERR_SCRATCH: return "the call needs more partials than the library's static scratch holds (PT_DK_SCRATCH_BYTES); use pt_dwconv1d_dk_det_f32 with a workspace";
     default: return "unknown status";
   }
 }
@@ -827,17 +876,32 @@ int pt_dwconv1d_dk_det_f32(const float* dy, const float* x, float* dk,
   const size_t need = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
   if (!workspace || workspace_bytes < need) return PT_ERR_WORKSPACE;
   if (!pt::aligned(workspace, 4)) return PT_ERR_ALIGN;
-  float* partials = (float*)workspace;
-  st = pt::dk_path(true, dy, x, partials, B, H, L, K, threads_per_block, g,
-                   stream);
+  return pt::dk_det_launch(dy, x, dk, (float*)workspace, B, H, L, K,
+                           threads_per_block, g, stream);
+}
+
+int pt_dwconv1d_dk_det_f32_noalloc(const float* dy, const float* x, float* dk,
+                                   int B, int H, int L, int K,
+                                   int threads_per_block, void* stream) {
+  int st = pt::check_shape(B, H, L, K);
   if (st != PT_OK) return st;
-  int ncoef = H * K;
-  int nbt = g.nbt;
-  const float* cp = partials;
-  void* args[] = {&cp, &dk, &ncoef, &nbt};
-  const uint32_t grid = (uint32_t)((ncoef + 3) / 4);
-  return pt::launch((const void*)&pt::dk_reduce_kernel, grid, 256, 0, stream,
-                    args);
+  if (!pt::valid_dk_threads(threads_per_block)) return PT_ERR_CONFIG;
+  if (H == 0) return PT_OK;  // empty tensors may have NULL data
+  if (!dk) return PT_ERR_NULL;
+  if (!pt::aligned(dk, 4)) return PT_ERR_ALIGN;
+  if (B == 0) return pt::zero_fill(dk, H * K, stream);
+  if (!dy || !x) return PT_ERR_NULL;
+  if (!pt::aligned(dy, 4) || !pt::aligned(x, 4)) return PT_ERR_ALIGN;
+  const pt::DkGeom g = pt::dk_geometry(
+      B, H, L, K, threads_per_block, pt::aligned(dy, 16) && pt::aligned(x, 16));
+  if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
+  const size_t need = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
+  if (need > (size_t)PT_DK_SCRATCH_BYTES) return PT_ERR_SCRATCH;
+  float* partials = nullptr;
+  st = pt::scratch_address(&partials);
+  if (st != PT_OK) return st;
+  return pt::dk_det_launch(dy, x, dk, partials, B, H, L, K, threads_per_block,
+                           g, stream);
 }
 
 int pt_kernel_attributes(int kernel_id, int L, int K, int* regs,

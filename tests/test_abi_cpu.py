@@ -360,3 +360,34 @@ def test_xcd_remap_is_a_bijection():
 
     for n in list(range(1, 130)) + [random.Random(1).randint(1, 50000) for _ in range(20)]:
         assert sorted(remap(p, n) for p in range(n)) == list(range(n))
+
+
+def test_noalloc_dk_validation_and_scratch_limit_before_launch(lib):
+    """pt_dwconv1d_dk_det_f32_noalloc checks shape, config, NULL, alignment
+    and then its static scratch (PT_DK_SCRATCH_BYTES of partials) before any
+    HIP call: a shape whose partials exceed it is refused with
+    PT_ERR_SCRATCH, for 16-byte aligned (channel-group) and 4-byte aligned
+    (per-channel) inputs alike."""
+    from pathtile_amd import _lib
+
+    buf = (ctypes.c_ubyte * 4096)()
+    base = ctypes.addressof(buf)
+    al = base + (-base) % 16
+    pa, pb, pc = (ctypes.c_void_p(al + o) for o in (0, 1024, 2048))
+    mis = [ctypes.c_void_p(al + o) for o in (4, 1028)]
+    fn = lib.pt_dwconv1d_dk_det_f32_noalloc
+    S = None
+    assert fn(pa, pb, pc, 1, 1, 49, 3, 128, S) == _lib.PT_ERR_SHAPE
+    assert fn(pa, pb, pc, 1, 1, 8, 3, 96, S) == _lib.PT_ERR_CONFIG
+    assert fn(pa, pb, None, 1, 1, 8, 3, 128, S) == _lib.PT_ERR_NULL
+    assert fn(None, pb, pc, 1, 1, 8, 3, 128, S) == _lib.PT_ERR_NULL
+    assert fn(ctypes.c_void_p(al + 2), pb, pc, 1, 1, 8, 3, 128, S) == _lib.PT_ERR_ALIGN
+    B, H, L, K = 4096, 8192, 48, 48  # 8192 * 48 taps * 4 bytes * >= 8 ranges > 8 MiB
+    need = ctypes.c_size_t(0)
+    assert lib.pt_dwconv1d_dk_det_workspace_bytes(B, H, L, K, 128, ctypes.byref(need)) == 0
+    assert need.value > _lib.PT_DK_SCRATCH_BYTES
+    assert fn(pa, pb, pc, B, H, L, K, 128, S) == _lib.PT_ERR_SCRATCH
+    assert fn(mis[0], mis[1], pc, B, H, L, K, 128, S) == _lib.PT_ERR_SCRATCH
+    assert "static scratch" in _lib.status_string(_lib.PT_ERR_SCRATCH)
+    with pytest.raises(ValueError, match="static scratch"):
+        _lib.check(_lib.PT_ERR_SCRATCH, "pt_dwconv1d_dk_det_f32_noalloc")
