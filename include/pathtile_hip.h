@@ -72,16 +72,20 @@ const char* pt_status_string(int status);
  * MI355X counterpart of WARPS_PER_BLOCK, kernels/warp_tiled_ampere.py:643-644).
  *
  * Two kernels serve FWD and DX. The lane-per-row VALU kernel reproduces the
- * reference's fmaf chain bit for bit and honours waves_per_block. Where a
- * row needs at least 10.5 (LMAX / L)^2 useful FMAs per output on average
- * (LMAX = 16 ceil(L / 16)) and the layout allows it (L % 4 == 0, H % 8 == 0,
- * x and y 16-byte aligned), the
- * channel-group matrix-core kernel runs instead: eight waves per workgroup
- * whatever waves_per_block says, sums in the matrix cores' order (within
- * FP32 rounding of the reference: about 3e-7 max-abs-scaled against FP64).
- * The environment variable PATHTILE_ROWS_ALGO=valu selects the VALU kernel
- * everywhere, =mfma the matrix-core kernel wherever the layout allows; it is
- * read on every call.
+ * reference's fmaf chain bit for bit and honours waves_per_block; its
+ * workgroup holds a 64-row LDS tile per wave, so 16 waves fit only rows up
+ * to 32 (PT_ERR_CONFIG for longer rows on this kernel). Where a row needs at
+ * least 10.5 (LMAX / L)^2 useful FMAs per output on average (LMAX =
+ * 16 ceil(L / 16)) and the layout allows it (L % 4 == 0, H % 8 == 0, x and
+ * y 16-byte aligned), the channel-group matrix-core kernel runs instead:
+ * eight waves (channels) per workgroup whatever waves_per_block says, so
+ * every value is accepted there and gives the same bits; it sums in the
+ * matrix cores' order (within FP32 rounding of the reference: about 3e-7
+ * max-abs-scaled against FP64). On both kernels an Inf or NaN input or tap
+ * reaches exactly the outputs whose reference window holds it (those
+ * outputs follow the reference's chain). The environment variable
+ * PATHTILE_ROWS_ALGO=valu selects the VALU kernel everywhere, =mfma the
+ * matrix-core kernel wherever the layout allows; it is read on every call.
  */
 int pt_dwconv1d_fwd_f32(const float* x, const float* w, float* y, int B, int H,
                         int L, int K, int waves_per_block, void* stream);

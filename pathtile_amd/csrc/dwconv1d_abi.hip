@@ -338,7 +338,7 @@ static int max_lds_per_block() {
                             dev) != hipSuccess ||
       n <= 0) {
     (void)hipGetLastError();
-    n = 64 * 1024;
+    n = 160 * 1024;  // gfx950, the one target of this library
   }
   if (dev >= 0 && dev < 64) cache[dev] = n;
   return n;
@@ -456,6 +456,11 @@ static int rows_cg_launch(Fn fn, const T* in, const float* w, T* out, int B,
   return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream, args);
 }
 
+// Eight channels (waves) per workgroup whatever the caller's waves per
+// block: measured on MI355X at 1, 2, 4, 8 and 16 channels, 8 was fastest or
+// within 3% everywhere (at P: 227, 171, 156, 140 us for 1 to 8), while the
+// VALU kernel that serves the other shapes wants 1 to 4 waves per workgroup
+// (at S: 553-568 us against 606 at 8), so one knob cannot serve both.
 static int rows_cg_path(bool dx, const float* in, const float* w, float* out,
                         int B, int H, int L, int K, void* stream) {
   return rows_cg_launch(kRowsCgTable[dx ? 1 : 0][mfma_index(L)], in, w, out, B,
@@ -480,6 +485,9 @@ static int rows_path(bool dx, const float* in, const float* w, float* out,
   if (!in || !w || !out) return PT_ERR_NULL;
   if (!aligned(in, 4) || !aligned(w, 4) || !aligned(out, 4))
     return PT_ERR_ALIGN;
+  if (rows_algo(L, K) == kRowsMfma && rows_cg_ok(H, L, in, out))
+    return rows_cg_path(dx, in, w, out, B, H, L, K, stream);
+  // The VALU kernel: one 64-row LDS tile per wave.
   const size_t lds_need = (size_t)wpb * rows_lds_per_wave(L);
   if (lds_need > (size_t)max_lds_per_block()) return PT_ERR_CONFIG;
   const int wpc = rows_waves_per_cu(L, K);
@@ -487,8 +495,6 @@ static int rows_path(bool dx, const float* in, const float* w, float* out,
   const bool vec = (L % 4 == 0) && aligned(in, 16) && aligned(out, 16);
   if (wpb * kWave > rows_max_threads(8 * (lbucket_index(L) + 1), vec))
     return PT_ERR_CONFIG;
-  if (rows_algo(L, K) == kRowsMfma && rows_cg_ok(H, L, in, out))
-    return rows_cg_path(dx, in, w, out, B, H, L, K, stream);
   const int li = lbucket_index(L), ki = kbucket_index(K);
   RowsFn fn = dx ? (vec ? kDxTableV : kDxTableS)[li][ki]
                  : (vec ? kFwdTableV : kFwdTableS)[li][ki];

@@ -319,19 +319,26 @@ def test_golden_edge_fixtures(rt):
 
 
 @pytest.mark.parametrize("algo", ["valu", "auto"])
-@pytest.mark.parametrize("wpb,L", [(1, 48), (2, 48), (4, 48), (8, 48), (16, 32), (8, 37)])
-def test_every_waves_per_block_gives_the_same_bits(wpb, L, algo, monkeypatch):
-    """VALU: every waves_per_block reproduces the reference's fmaf chain.
-    Default: the matrix-core kernel (L % 4 == 0, H % 8 == 0, K = 48) ignores
-    waves_per_block, so every value gives the bits of waves_per_block = 1."""
+@pytest.mark.parametrize("wpb,L,H", [(1, 48, 24), (2, 48, 24), (4, 48, 24), (8, 48, 24),
+                                     (16, 32, 48), (16, 32, 24), (8, 37, 24), (16, 48, 48)])
+def test_every_waves_per_block_gives_the_same_bits(wpb, L, H, algo, monkeypatch):
+    """VALU: every waves_per_block reproduces the reference's fmaf chain
+    (16 waves do not fit rows above 32: refused). Default: the matrix-core
+    kernel (L % 4 == 0, H % 8 == 0, K = 48) runs 8-channel workgroups
+    whatever waves_per_block says (16 included, at every L), so every value
+    gives the bits of waves_per_block = 1."""
     from pathtile_amd import runtime
 
     if algo != "auto":
         monkeypatch.setenv("PATHTILE_ROWS_ALGO", algo)
-    B, H, K = 200, 24, 48
+    B, K = 200, 48
     x, w, dy = _inputs(B, H, L, K, seed=7)
     xd, wd, dyd = _dev(x, w, dy)
     r = runtime.HipWarpRuntime(waves_per_block=wpb)
+    if wpb == 16 and L > 32 and not _mfma_serves(H, L, K, algo):
+        with pytest.raises(ValueError, match="unsupported launch configuration"):
+            _fwd(r, xd, wd)
+        return
     y = _fwd(r, xd, wd).cpu().numpy()
     dx = _dx(r, dyd, wd).cpu().numpy()
     if _mfma_serves(H, L, K, algo):
@@ -361,8 +368,10 @@ def test_every_dk_block_size(threads):
 
 
 def test_oversized_workgroup_is_rejected():
-    """16 waves x a 64-row tile at L=48 needs 213 KiB of LDS: refused before
-    launch with the library's configuration error."""
+    """H = 4 leaves the VALU kernel, where 16 waves x a 64-row tile at L = 48
+    need 213 KiB of LDS: refused before launch with the library's
+    configuration error. At H = 8 the matrix-core kernel serves the same
+    call (its workgroups are 8 waves whatever waves_per_block says)."""
     from pathtile_amd import runtime
 
     r = runtime.HipWarpRuntime(waves_per_block=16)
@@ -370,6 +379,9 @@ def test_oversized_workgroup_is_rejected():
     w = torch.zeros(4, 48, device="cuda:0")
     with pytest.raises(ValueError, match="unsupported launch configuration"):
         r.launch_fwd(x, w, torch.empty_like(x))
+    x8, w8, _ = _inputs(64, 8, 48, 48, seed=12)
+    y8 = _fwd(r, x8.cuda(), w8.cuda()).cpu().numpy()
+    assert oracle.normalized_max_abs(y8, oracle.fwd_f64(x8, w8)) < FWD_TOL
 
 
 def test_atomic_dk_accumulates_into_gk(rt):
