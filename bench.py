@@ -1,18 +1,25 @@
 """Benchmark of the MI355X depthwise Conv1D hot path (one JSON line).
 
 Metric: "FWD+dX+dK ms & HBM GB/s (% peak), B16384 H128 L48
-K48 fp32, 1 GPU". A step is one pass of the hot path over one batch:
-FWD, dX and dK (atomic, zero-init outside the dK event as in the reference's
-protocol, README.md:136-140). Inputs are synthetic, drawn on a CPU
-torch.Generator in the order x, w, dY (x, dY ~ N(0,1), w ~ N(0,1/K)) and
-copied to HBM before timing.
+K48 fp32, 1 GPU". A step is one pass of the hot path over one batch: FWD, dX
+and dK. Inputs are synthetic, drawn on a CPU torch.Generator in the order x,
+w, dY (x, dY ~ N(0,1), w ~ N(0,1/K)) and copied to HBM before timing.
 
-    python bench.py [--gpus 1] [--steps 100] [--warmup 20] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
 
-``value`` = mean FWD + mean dX + mean dK kernel ms over the K timed steps
-(HIP events on the launch stream; the reference sums separately timed path
-means, kernels/warp_tiled_ampere.py:1059-1096). ``ms_per_step`` is the wall
-time of the K steps / K between two device synchronisations.
+``value`` = FWD + dX + dK (atomic, zero-init outside the dK timing as in the
+reference's protocol, README.md:136-140) in ms, each path timed with the
+reference's protocol (artifact/REPRODUCIBILITY.md:81-93): 3 trials, each of
+50 warm-up launches and 100 timed launches per path, path order reversed on
+even trials (benchmark/benchmark_pathtile_candidate_sweep.py:488-501), mean
+of the trial means; the between-trial standard deviation is reported beside
+it. The timed launches run back to back between two HIP events on the launch
+stream. ``ms_per_step`` is the wall time of the contract's ``--steps``
+interleaved FWD/dX/zero+dK steps (after ``--warmup`` steps) between two
+device synchronisations. After timing, the outputs of the timed launches are
+checked against PyTorch FP64 on the GPU: FWD/dX on sampled batch rows (all
+channels), dK over the whole batch. The same protocol and checks run for the
+BASELINE's other configurations (S, E2, E1) as separate legs.
 """
 
 from __future__ import annotations
@@ -34,29 +41,37 @@ METRIC = "FWD+dX+dK ms & HBM GB/s (% peak), B16384 H128 L48 K48 fp32, 1 GPU"
 WORKLOADS = {
     # the metric's workload.
     "primary": (16384, 128, 48, 48),
-    # parity cases, benchmarked only on request.
+    # the other BASELINE configurations (legs).
     "short": (32768, 256, 48, 4),
     "odd_k": (16384, 128, 48, 47),
     "edge": (1000, 96, 37, 48),
 }
 PEAK_HBM_GBPS = 8000.0
-PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense FP32 matrix
+PEAK_BF16_MFMA_TFLOPS = 2500.0  # MI355X dense BF16 matrix
 # Published aggregate of the reference for this metric (README.md:96,
 # A100 PCIe 40 GB): 11.283 ms.
 REFERENCE_AGGREGATE_MS = 11.283
 POLICY = ROOT / "pathtile_amd" / "tune" / "frozen_policy.json"
 PROFILES = ROOT / "profiles"
+FWD_TOL, DK_TOL = 1e-5, 1e-4
 
 
 def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=100)
-    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--workload", choices=sorted(WORKLOADS), default="primary")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--trials", type=int, default=3, help="timing trials per path")
+    p.add_argument("--path-warmup", type=int, default=50, help="warm-up launches per path and trial")
+    p.add_argument("--path-runs", type=int, default=100, help="timed launches per path and trial")
+    p.add_argument("--no-legs", action="store_true",
+                   help="skip the other BASELINE configurations (S, E2, E1)")
+    p.add_argument("--no-extras", action="store_true",
+                   help="skip the BF16, channels-last, long-row and VALU-kernel legs")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-runs", type=int, default=5)
+    p.add_argument("--cpu-runs", type=int, default=10)
     p.add_argument("--gpu-library-steps", type=int, default=0, metavar="N",
                    help="also time N calls per path of PyTorch's GPU convolution (MIOpen) "
                         "on the same tensors")
@@ -102,40 +117,100 @@ def make_inputs(B, H, L, K, seed):
     return x, w, dy
 
 
-def correctness_gate(rt, x, w, dy, rows: int = 512) -> dict:
-    """Refuse to time a wrong kernel (benchmark/benchmark_dk_fairness.py:149-170):
-    compare the HIP paths with PyTorch's own conv1d/autograd on the GPU for the
-    first `rows` batch entries."""
+def mean(v):
+    return sum(v) / len(v) if v else float("nan")
+
+
+def stdev(v):
+    if len(v) < 2:
+        return 0.0
+    m = mean(v)
+    return math.sqrt(sum((a - m) ** 2 for a in v) / (len(v) - 1))
+
+
+# --------------------------------------------------------------------------
+# FP64 references on the GPU (PyTorch), for the checks of the timed outputs
+# --------------------------------------------------------------------------
+def fp64_fwd(x, w):
+    """y[b,h,t] = sum_j w[h,j] x[b,h,t+j-p], p = K // 2, in FP64
+    (benchmark/benchmark_shape_sweep_ampere.py:220-239)."""
+    import torch.nn.functional as F
+
+    K = w.shape[1]
+    p = K // 2
+    return F.conv1d(F.pad(x.double(), (p, K - 1 - p)), w.double().unsqueeze(1),
+                    groups=x.shape[1])
+
+
+def fp64_dx(dy, w):
+    """dx[b,h,s] = sum_j w[h,j] dy[b,h,s-j+p]: a correlation with the
+    flipped taps, padded (K-1-p, p), in FP64."""
+    import torch.nn.functional as F
+
+    K = w.shape[1]
+    p = K // 2
+    return F.conv1d(F.pad(dy.double(), (K - 1 - p, p)), w.double().flip(-1).unsqueeze(1),
+                    groups=dy.shape[1])
+
+
+def fp64_dk(dy, x, K):
+    """dK[h,j] = sum_b sum_t dy[b,h,t] x[b,h,t+j-p] in FP64 over the whole
+    batch (benchmark/check_dk_fp64_comparison.py:29-39)."""
     import torch
     import torch.nn.functional as F
 
-    B, H, L = x.shape
-    K = w.shape[1]
-    xs, dys = x[:rows].contiguous(), dy[:rows].contiguous()
-    y = torch.empty_like(xs)
-    dx = torch.empty_like(xs)
-    gk = torch.empty(H, K, device=x.device)
-    rt.launch_fwd(xs, w, y)
-    rt.launch_bwd_input(dys, w, dx)
-    rt.launch_bwd_weight(dys, xs, gk, K, zero_first=True)
-    xr = xs.double().requires_grad_(True)
-    wr = w.double().requires_grad_(True)
-    left = K // 2
-    yr = F.conv1d(F.pad(xr, (left, K - 1 - left)), wr.unsqueeze(1), groups=H)
-    gx_r, gk_r = torch.autograd.grad(yr, (xr, wr), dys.double())
-
-    def err(a, b):
-        return float((a.double() - b).abs().max() / b.abs().max().clamp_min(1e-12))
-
-    e = {"fwd": err(y, yr.detach()), "dx": err(dx, gx_r), "dk": err(gk, gk_r)}
-    ok = e["fwd"] < 1e-5 and e["dx"] < 1e-5 and e["dk"] < 1e-4
-    if not ok:
-        raise SystemExit(f"correctness gate failed: {e}")
-    return e
+    L = x.shape[2]
+    p = K // 2
+    xp = F.pad(x.double(), (p, K - 1 - p))
+    dyd = dy.double()
+    out = torch.stack([(dyd * xp[..., j:j + L]).sum(dim=(0, 2)) for j in range(K)], dim=1)
+    del xp, dyd
+    return out
 
 
-def mean(v):
-    return sum(v) / len(v) if v else float("nan")
+def nerr(a, ref) -> float:
+    """max |a - ref| / max |ref| (kernels/warp_tiled_ampere.py:182-184)."""
+    return float((a.double() - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+
+
+def device_warmup(fns: dict, seconds: float = 0.3) -> None:
+    """Launch every path round-robin for about `seconds` of wall time before
+    the first timed trial: the first ~0.1 s of launches after the inputs are
+    written run a few percent slow (measured on MI355X: the first trial of
+    the first path 144 us against 135.6 us after), which the per-path warm-up
+    of the protocol alone does not cover."""
+    import torch
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for fn in fns.values():
+            fn()
+        torch.cuda.synchronize()
+
+
+def time_paths(fns: dict, stream, trials: int, warmup: int, runs: int) -> dict:
+    """The reference's protocol per path: `trials` trials, each `warmup`
+    launches then `runs` launches back to back between two events on the
+    launch stream; path order reversed on even trials. Returns per path the
+    trial means (ms per launch), their mean and their standard deviation."""
+    import torch
+
+    per = {k: [] for k in fns}
+    for t in range(1, trials + 1):
+        order = list(fns) if t % 2 else list(reversed(list(fns)))
+        for k in order:
+            fn = fns[k]
+            for _ in range(warmup):
+                fn()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(runs):
+                fn()
+            e1.record(stream)
+            e1.synchronize()
+            per[k].append(e0.elapsed_time(e1) / runs)
+    return {k: {"ms": mean(v), "std_ms": stdev(v), "trials_ms": v} for k, v in per.items()}
 
 
 def rows_kernel_name(H: int, L: int, K: int, dx: bool) -> str:
@@ -168,19 +243,113 @@ def dk_kernel_name(H: int, L: int, threads: int) -> str:
     return "dwconv_dk_mfma_kernel"
 
 
-def read_traffic(kernel_tag: str) -> dict | None:
-    """HBM bytes per launch of `kernel_tag` from the committed rocprofv3 PMC
-    summary (profiles/pmc_traffic_<kernel_tag>.md, lines
-    'FETCH_BYTES_PER_LAUNCH: <n>' and 'WRITE_BYTES_PER_LAUNCH: <n>')."""
-    f = PROFILES / f"pmc_traffic_{kernel_tag}.md"
+def read_profile_numbers(name: str, keys: tuple[str, ...]) -> dict | None:
+    """`KEY: number` lines from a committed rocprofv3 summary under
+    profiles/ (None if the file or a key is missing)."""
+    f = PROFILES / name
     if not f.exists():
         return None
     text = f.read_text()
-    m1 = re.search(r"FETCH_BYTES_PER_LAUNCH:\s*([0-9.eE+]+)", text)
-    m2 = re.search(r"WRITE_BYTES_PER_LAUNCH:\s*([0-9.eE+]+)", text)
-    if not (m1 and m2):
-        return None
-    return {"fetch": float(m1.group(1)), "write": float(m2.group(1))}
+    out = {}
+    for k in keys:
+        m = re.search(rf"{k}:\s*([0-9.eE+]+)", text)
+        if not m:
+            return None
+        out[k] = float(m.group(1))
+    return out
+
+
+def read_traffic(kernel_tag: str) -> dict | None:
+    """HBM bytes per launch of `kernel_tag` from the committed rocprofv3 PMC
+    summary (profiles/pmc_traffic_<kernel_tag>.md)."""
+    r = read_profile_numbers(f"pmc_traffic_{kernel_tag}.md",
+                             ("FETCH_BYTES_PER_LAUNCH", "WRITE_BYTES_PER_LAUNCH"))
+    return None if r is None else {"fetch": r["FETCH_BYTES_PER_LAUNCH"],
+                                   "write": r["WRITE_BYTES_PER_LAUNCH"]}
+
+
+def workload_leg(rt, name: str, args, dev, stream, keep: bool = False) -> dict:
+    """One BASELINE configuration: per-path timing with the reference's
+    protocol, then the checks of the timed outputs against FP64 (sampled
+    batch rows for FWD/dX, the whole batch for dK; the deterministic dK
+    bitwise equal across two runs)."""
+    import torch
+
+    from pathtile_amd import runtime
+
+    B, H, L, K = WORKLOADS[name]
+    log(f"{name}: B={B} H={H} L={L} K={K}")
+    x_cpu, w_cpu, dy_cpu = make_inputs(B, H, L, K, args.seed)
+    x, w, dy = x_cpu.to(dev), w_cpu.to(dev), dy_cpu.to(dev)
+    y = torch.empty_like(x)
+    dx = torch.empty_like(x)
+    gk = torch.zeros(H, K, device=dev)
+    gd = torch.zeros(H, K, device=dev)
+    fns = {
+        "fwd": lambda: rt.launch_fwd(x, w, y),
+        "bwd_input": lambda: rt.launch_bwd_input(dy, w, dx),
+        "bwd_weight": lambda: rt.launch_bwd_weight(dy, x, gk, K),
+        "bwd_weight_zero": lambda: rt.launch_bwd_weight(dy, x, gk, K, zero_first=True),
+        "bwd_weight_det": lambda: rt.launch_bwd_weight_deterministic(dy, x, gd, K),
+    }
+    device_warmup(fns)
+    timing = time_paths(fns, stream, args.trials, args.path_warmup, args.path_runs)
+
+    # Checks of the timed launches' outputs: y and dx hold the last timed
+    # launch's results; dK is launched once more on the same tensors (the
+    # timed atomic launches accumulate into gk).
+    g = torch.Generator().manual_seed(args.seed + 1)
+    idx = torch.randperm(B, generator=g)[: min(B, 256)]
+    idx[0], idx[-1] = 0, B - 1  # first and last sample: the ragged tail steps
+    idx = idx.to(dev)
+    gate = {
+        "fwd": nerr(y[idx], fp64_fwd(x[idx], w)),
+        "bwd_input": nerr(dx[idx], fp64_dx(dy[idx], w)),
+    }
+    ref = fp64_dk(dy, x, K)
+    rt.launch_bwd_weight(dy, x, gk, K, zero_first=True)
+    gate["bwd_weight"] = nerr(gk, ref)
+    gd2 = torch.empty_like(gd)
+    rt.launch_bwd_weight_deterministic(dy, x, gd2, K)
+    gate["bwd_weight_det"] = nerr(gd2, ref)
+    torch.cuda.synchronize()
+    det_bitwise = bool(torch.equal(gd, gd2))
+    ok = (gate["fwd"] < FWD_TOL and gate["bwd_input"] < FWD_TOL and gate["bwd_weight"] < DK_TOL
+          and gate["bwd_weight_det"] < DK_TOL and det_bitwise)
+    if not ok:
+        raise SystemExit(f"{name}: check of the timed outputs failed: {gate}, "
+                         f"deterministic dK bitwise={det_bitwise}")
+    nbytes = runtime.minimum_algorithmic_bytes(B, H, L, K)
+    kernels = {"fwd": rows_kernel_name(H, L, K, False), "bwd_input": rows_kernel_name(H, L, K, True),
+               "bwd_weight": dk_kernel_name(H, L, rt.bwdk_block)}
+    paths = {}
+    for ph, t in timing.items():
+        gbps = runtime.algorithmic_bandwidth_gbps(nbytes, t["ms"])
+        paths[ph] = {"ms": round(t["ms"], 5), "std_ms": round(t["std_ms"], 5),
+                     "trials_ms": [round(v, 5) for v in t["trials_ms"]],
+                     "gbps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_HBM_GBPS, 2),
+                     "kernel": kernels[{"bwd_weight_zero": "bwd_weight",
+                                        "bwd_weight_det": "bwd_weight"}.get(ph, ph)]}
+    agg = paths["fwd"]["ms"] + paths["bwd_input"]["ms"] + paths["bwd_weight"]["ms"]
+    agg_std = math.sqrt(sum(timing[p]["std_ms"] ** 2 for p in ("fwd", "bwd_input", "bwd_weight")))
+    leg = {
+        "config": {"B": B, "H": H, "L": L, "K": K},
+        "fwd_dx_dk_ms": round(agg, 5),
+        "fwd_dx_dk_std_ms": round(agg_std, 5),
+        "aggregate_pct_peak": round(100 * 3 * nbytes / (agg / 1e3) / 1e9 / PEAK_HBM_GBPS, 2),
+        "algorithmic_bytes_per_path": nbytes,
+        "paths": paths,
+        "check_of_timed_outputs": {k: float(f"{v:.3e}") for k, v in gate.items()}
+        | {"deterministic_dk_bitwise_repeat": det_bitwise,
+           "sampled_rows": int(idx.numel()),
+           "bars": "FWD/dX <= 1e-5, dK <= 1e-4 max-abs-scaled vs PyTorch FP64 on the GPU"},
+    }
+    if keep:
+        leg["_tensors"] = (x_cpu, w_cpu, dy_cpu, x, w, dy, y, dx, gk)
+    else:
+        del x, w, dy, y, dx, gk, gd, gd2, ref
+        torch.cuda.empty_cache()
+    return leg
 
 
 def cpu_baseline(x, w, dy, runs: int) -> dict:
@@ -329,6 +498,189 @@ def s4convd_training_steps(steps: int, warmup: int, dev) -> dict:
             "speedup_vs_pytorch": round(out["pytorch"]["ms_per_step"] / out["warp"]["ms_per_step"], 3)}
 
 
+def extras(rt, args, dev, stream, x, w, dy, y, gk) -> dict:
+    """Legs beyond the metric on the primary tensors (no reference
+    counterpart for BF16; the reference's Flash-DWC bridge ABI for
+    channels-last dK; the reference's long-row module at its benchmark
+    shape; the VALU FWD/dX kernel that reproduces the reference's bits)."""
+    import torch
+
+    from pathtile_amd import runtime
+
+    B, H, L = x.shape
+    K = w.shape[1]
+    out = {}
+    prot = dict(stream=stream, trials=args.trials, warmup=args.path_warmup, runs=args.path_runs)
+
+    # BF16 I/O: x, dY and the FWD/dX outputs in bfloat16, taps and dK in
+    # FP32; algorithmic bytes (2 B H L * 2 + H K * 4) per path. Served for
+    # the channel-group layout only.
+    dk_channels = 2 * (rt.bwdk_block // 64)
+    if L % 4 == 0 and H % 8 == 0 and H % dk_channels == 0 and rt.bwdk_block <= 512:
+        xb, dyb = x.to(torch.bfloat16), dy.to(torch.bfloat16)
+        yb, dxb = torch.empty_like(xb), torch.empty_like(dyb)
+        t = time_paths({
+            "fwd": lambda: rt.launch_fwd_bf16(xb, w, yb),
+            "bwd_input": lambda: rt.launch_bwd_input_bf16(dyb, w, dxb),
+            "bwd_weight": lambda: rt.launch_bwd_weight_bf16(dyb, xb, gk, K),
+            "bwd_weight_det": lambda: rt.launch_bwd_weight_deterministic_bf16(dyb, xb, gk, K),
+        }, **prot)
+        rows_b = min(512, B)
+        y32 = torch.empty(rows_b, H, L, device=dev)
+        rt.launch_fwd(xb[:rows_b].float().contiguous(), w, y32)
+        torch.cuda.synchronize()
+        bf16_gate = nerr(yb[:rows_b].float(), y32.double())
+        if not bf16_gate < 2.0 ** -8:
+            raise SystemExit(f"BF16 gate failed: {bf16_gate}")
+        del xb, dyb, yb, dxb, y32
+        nb = 2 * B * H * L * 2 + H * K * 4
+        out["bf16_io"] = {
+            "paths": {ph: {"ms": round(v["ms"], 5), "std_ms": round(v["std_ms"], 5),
+                           "gbps": round(nb / (v["ms"] / 1e3) / 1e9, 1),
+                           "pct_peak": round(100 * nb / (v["ms"] / 1e3) / 1e9 / PEAK_HBM_GBPS, 2)}
+                      for ph, v in t.items()},
+            "fwd_dx_dk_ms": round(t["fwd"]["ms"] + t["bwd_input"]["ms"] + t["bwd_weight"]["ms"], 5),
+            "gate_vs_fp32_path": float(f"{bf16_gate:.3e}"),
+            "note": "x, dY, y, dX bfloat16; taps and dK FP32; FP32 accumulation; "
+                    "algorithmic bytes (2 B H L * 2 + H K * 4) per path",
+        }
+
+    # Channels-last dK through the Flash-DWC bridge ABI (flash_dk_fp32).
+    if B % 16 == 0 and H % 32 == 0:
+        xc = x.permute(0, 2, 1).unsqueeze(1).contiguous()
+        dyc = dy.permute(0, 2, 1).unsqueeze(1).contiguous()
+        dwc = torch.zeros(1, K, H, device=dev)
+        t = time_paths({"dk": lambda: rt.launch_bwd_weight_channels_last(xc, dyc, dwc, 1)}, **prot)
+        rt.launch_bwd_weight_deterministic(dy, x, gk, K)
+        rt.launch_bwd_weight_channels_last(xc, dyc, dwc, 1, zero_first=True)
+        torch.cuda.synchronize()
+        cl_gate = nerr(dwc[0].T, gk.double())
+        if not cl_gate < 1e-5:
+            raise SystemExit(f"channels-last dK gate failed: {cl_gate}")
+        gb = runtime.algorithmic_bandwidth_gbps(runtime.minimum_algorithmic_bytes(B, H, L, K),
+                                                t["dk"]["ms"])
+        out["channels_last_dk"] = {
+            "ms": round(t["dk"]["ms"], 5), "std_ms": round(t["dk"]["std_ms"], 5),
+            "gbps": round(gb, 1), "pct_peak": round(100 * gb / PEAK_HBM_GBPS, 2),
+            "kernel": f"dwconv_dk_cl_kernel<{16 * ((L + 15) // 16)}>",
+            "gate_vs_row_major": float(f"{cl_gate:.3e}"),
+            "note": "flash_dk_fp32 (x, dY [B,1,L,H]; dw [1,K,H] accumulated), GZ=1; "
+                    "algorithmic bytes as the row-major dK"}
+        del xc, dyc, dwc
+
+    # The VALU rows kernel (the reference's lane-per-row structure, bit-exact
+    # with its fmaf chain), forced beside the default FWD/DX kernel.
+    prev = os.environ.get("PATHTILE_ROWS_ALGO")
+    os.environ["PATHTILE_ROWS_ALGO"] = "valu"
+    try:
+        dxv = torch.empty_like(x)
+        t = time_paths({"fwd": lambda: rt.launch_fwd(x, w, y),
+                        "bwd_input": lambda: rt.launch_bwd_input(dy, w, dxv)}, **prot)
+        idx = torch.arange(0, B, max(1, B // 256), device=dev)
+        valu_gate = {"fwd": nerr(y[idx], fp64_fwd(x[idx], w)),
+                     "bwd_input": nerr(dxv[idx], fp64_dx(dy[idx], w))}
+        kern = {"fwd": rows_kernel_name(H, L, K, False), "bwd_input": rows_kernel_name(H, L, K, True)}
+        del dxv
+    finally:
+        if prev is None:
+            del os.environ["PATHTILE_ROWS_ALGO"]
+        else:
+            os.environ["PATHTILE_ROWS_ALGO"] = prev
+    if not all(v < FWD_TOL for v in valu_gate.values()):
+        raise SystemExit(f"VALU rows kernel gate failed: {valu_gate}")
+    nbytes = runtime.minimum_algorithmic_bytes(B, H, L, K)
+    out["rows_valu"] = {
+        ph: {"ms": round(v["ms"], 5), "std_ms": round(v["std_ms"], 5),
+             "pct_peak": round(100 * runtime.algorithmic_bandwidth_gbps(nbytes, v["ms"])
+                               / PEAK_HBM_GBPS, 2), "kernel": kern[ph]}
+        for ph, v in t.items()
+    } | {"check_vs_fp64": {k: float(f"{v:.3e}") for k, v in valu_gate.items()},
+         "note": "PATHTILE_ROWS_ALGO=valu: the bit-exact VALU FWD/DX kernel, same protocol"}
+    return out
+
+
+def long_rows_leg(rt, args, dev, stream) -> dict:
+    """Long rows at the reference's long-row benchmark shape (kernels/
+    shared_l192.py, benchmarked at B16384 H128 L192 K192 by
+    benchmark/benchmark_gmc_vs_shared_l192.py:14-17). The default kernels run
+    on the BF16 matrix cores with three-way split FP32 operands; the FP32
+    matrix-core kernels (PATHTILE_LONG_ALGO=fp32) are timed beside them."""
+    import torch
+
+    from pathtile_amd.tune.baselines import useful_products
+
+    LB, LH, LL, LK = 16384, 128, 192, 192
+    xl = torch.randn(LB, LH, LL, generator=torch.Generator().manual_seed(args.seed + 3)).to(dev)
+    dyl = torch.randn(LB, LH, LL, generator=torch.Generator().manual_seed(args.seed + 4)).to(dev)
+    wl = (torch.randn(LH, LK, generator=torch.Generator().manual_seed(args.seed + 5)) / LK ** 0.5).to(dev)
+    yl, dxl, gkl = torch.empty_like(xl), torch.empty_like(dyl), torch.empty(LH, LK, device=dev)
+    fns = {
+        "fwd": lambda: rt.launch_fwd_long(xl, wl, yl),
+        "bwd_input": lambda: rt.launch_bwd_input_long(dyl, wl, dxl),
+        "bwd_weight": lambda: rt.launch_bwd_weight_long(dyl, xl, gkl, LK),
+    }
+    prot = dict(stream=stream, trials=args.trials, warmup=args.path_warmup, runs=args.path_runs)
+    useful = 2 * useful_products(LB, LH, LL, LK)
+    nbytes = 2 * LB * LH * LL * 4 + LH * LK * 4
+    # Issued BF16 matrix flops per launch of the split kernels, from the
+    # committed rocprofv3 counter summary (SQ_INSTS_VALU_MFMA_MOPS_BF16).
+    issued = read_profile_numbers("pmc_mfma_long_l192_k192.md",
+                                  ("BF16_MFMA_FLOP_FWD", "BF16_MFMA_FLOP_DX", "BF16_MFMA_FLOP_DK"))
+    issued_key = {"fwd": "BF16_MFMA_FLOP_FWD", "bwd_input": "BF16_MFMA_FLOP_DX",
+                  "bwd_weight": "BF16_MFMA_FLOP_DK"}
+
+    def paths(t, split):
+        out = {}
+        for ph, v in t.items():
+            s = v["ms"] / 1e3
+            row = {"ms": round(v["ms"], 5), "std_ms": round(v["std_ms"], 5),
+                   "tflops_useful": round(useful / s / 1e12, 2),
+                   "hbm_pct_peak": round(100 * nbytes / s / 1e9 / PEAK_HBM_GBPS, 2)}
+            if split and issued:
+                f = issued[issued_key[ph]]
+                row["tflops_bf16_issued"] = round(f / s / 1e12, 1)
+                row["frac_bf16_mfma_peak"] = round(f / s / 1e12 / PEAK_BF16_MFMA_TFLOPS, 4)
+            out[ph] = row
+        return out
+
+    prev = os.environ.pop("PATHTILE_LONG_ALGO", None)
+    try:
+        t_split = time_paths(fns, **prot)
+        y_split = yl[:256].clone()
+        os.environ["PATHTILE_LONG_ALGO"] = "fp32"
+        t_fp32 = time_paths(fns, **prot)
+        rt.launch_fwd_long(xl, wl, yl)
+        torch.cuda.synchronize()
+    finally:
+        if prev is None:
+            os.environ.pop("PATHTILE_LONG_ALGO", None)
+        else:
+            os.environ["PATHTILE_LONG_ALGO"] = prev
+    gate = {"split_vs_fp64": nerr(y_split, fp64_fwd(xl[:256], wl)),
+            "fp32_vs_fp64": nerr(yl[:256], fp64_fwd(xl[:256], wl))}
+    if not all(v < FWD_TOL for v in gate.values()):
+        raise SystemExit(f"long-row gate failed: {gate}")
+    del xl, dyl, wl, yl, dxl, gkl
+    torch.cuda.empty_cache()
+    return {
+        "config": {"B": LB, "H": LH, "L": LL, "K": LK},
+        "paths": paths(t_split, True),
+        "fwd_dx_dk_ms": round(sum(v["ms"] for v in t_split.values()), 5),
+        "kernels": {"fwd": "dwconv_rows_long_s3_kernel<192, 192, false, true>",
+                    "bwd_input": "dwconv_rows_long_s3_kernel<192, 192, true, true>",
+                    "bwd_weight": "dwconv_dk_long_s3_kernel<192, true>"},
+        "fp32_mfma_kernels": {"paths": paths(t_fp32, False),
+                              "fwd_dx_dk_ms": round(sum(v["ms"] for v in t_fp32.values()), 5)},
+        "check_fwd_first_256_samples": {k: float(f"{v:.3e}") for k, v in gate.items()},
+        "note": "pt_dwconv1d_{fwd,dx,dk}_long_f32; default = BF16 matrix cores on three-way split "
+                "FP32 operands (FP32-accurate), fp32_mfma_kernels = PATHTILE_LONG_ALGO=fp32; "
+                "tflops_useful = 2 * real multiply-adds / time; frac_bf16_mfma_peak = BF16 matrix "
+                "flops the split kernels issue (rocprofv3 SQ_INSTS_VALU_MFMA_MOPS_BF16, "
+                "profiles/pmc_mfma_long_l192_k192.md) / time / 2.5 PFLOP/s; HBM bytes "
+                "2 B H L 4 + H K 4 per path",
+    }
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
@@ -346,19 +698,16 @@ def main(argv=None) -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
     B, H, L, K = WORKLOADS[args.workload]
     cfg = frozen_config()
     rt = runtime.HipWarpRuntime(waves_per_block=cfg["fwd_waves_per_block"],
                                 dx_waves_per_block=cfg["dx_waves_per_block"],
                                 bwdk_block=cfg["dk_threads_per_block"])
-    log(f"workload B={B} H={H} L={L} K={K} config={cfg}")
-    x_cpu, w_cpu, dy_cpu = make_inputs(B, H, L, K, args.seed)
-    x, w, dy = x_cpu.to(dev), w_cpu.to(dev), dy_cpu.to(dev)
-    y = torch.empty_like(x)
-    dx = torch.empty_like(x)
-    gk = torch.zeros(H, K, device=dev)
-    gate = correctness_gate(rt, x, w, dy)
-    log(f"correctness gate vs torch (first 512 rows): {gate}")
+    log(f"workload {args.workload} config={cfg}")
+    main_leg = workload_leg(rt, args.workload, args, dev, stream, keep=True)
+    x_cpu, w_cpu, dy_cpu, x, w, dy, y, dx, gk = main_leg.pop("_tensors")
+    log(f"{args.workload}: {main_leg['fwd_dx_dk_ms']:.4f} ms, checks {main_leg['check_of_timed_outputs']}")
 
     def step():
         rt.launch_fwd(x, w, y)
@@ -366,219 +715,38 @@ def main(argv=None) -> int:
         gk.zero_()
         rt.launch_bwd_weight(dy, x, gk, K)
 
+    # The contract's steps: `warmup` untimed, then exactly `steps` interleaved
+    # FWD / dX / zero + dK steps, wall-clocked between two synchronisations.
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    # The contract's K steps (FWD, dX, zero + dK interleaved), wall-clocked
-    # between two synchronisations.
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
 
-    # Per-path loops: `steps` back-to-back launches of one path between two
-    # events recorded on the launch stream (torch's current stream, where the
-    # runtime enqueues), mean = elapsed / steps. The atomic dK loop does not
-    # re-zero gk (the kernel's work is the same; the zero-init is timed as its
-    # own path, "bwd_weight_zero", where it is part of the call).
-    stream = torch.cuda.current_stream(dev)
-    loops = {
-        "fwd": lambda: rt.launch_fwd(x, w, y),
-        "bwd_input": lambda: rt.launch_bwd_input(dy, w, dx),
-        "bwd_weight": lambda: rt.launch_bwd_weight(dy, x, gk, K),
-        "bwd_weight_zero": lambda: rt.launch_bwd_weight(dy, x, gk, K, zero_first=True),
-        "bwd_weight_det": lambda: rt.launch_bwd_weight_deterministic(dy, x, gk, K),
-    }
-    def time_loop(fn):
-        for _ in range(max(1, args.warmup // 4)):
-            fn()
-        ev0 = torch.cuda.Event(enable_timing=True)
-        ev1 = torch.cuda.Event(enable_timing=True)
-        ev0.record(stream)
-        for _ in range(args.steps):
-            fn()
-        ev1.record(stream)
-        ev1.synchronize()
-        return ev0.elapsed_time(ev1) / args.steps
-
-    loop_ms = {ph: time_loop(fn) for ph, fn in loops.items()}
-
-    # BF16 I/O (no reference counterpart): the same workload with x, dY and
-    # the FWD/dX outputs in bfloat16, taps and dK in FP32, same loops. Its
-    # algorithmic bytes are (2 B H L * 2 + H K * 4) per path. The BF16 entry
-    # points serve the channel-group layout only (L % 4 == 0, H % 8 == 0 and
-    # the dK block's channel rule), so other shapes skip the leg.
-    bf16_leg = None
-    dk_channels = 2 * (rt.bwdk_block // 64)
-    if L % 4 == 0 and H % 8 == 0 and H % dk_channels == 0 and rt.bwdk_block <= 512:
-        xb, dyb = x.to(torch.bfloat16), dy.to(torch.bfloat16)
-        yb, dxb = torch.empty_like(xb), torch.empty_like(dyb)
-        bf16_loops = {
-            "fwd": lambda: rt.launch_fwd_bf16(xb, w, yb),
-            "bwd_input": lambda: rt.launch_bwd_input_bf16(dyb, w, dxb),
-            "bwd_weight": lambda: rt.launch_bwd_weight_bf16(dyb, xb, gk, K),
-            "bwd_weight_det": lambda: rt.launch_bwd_weight_deterministic_bf16(dyb, xb, gk, K),
-        }
-        bf16_ms = {ph: time_loop(fn) for ph, fn in bf16_loops.items()}
-        # gate: BF16 FWD against the FP32 path on the same (BF16-valued) input
-        rows_b = min(512, B)
-        y32 = torch.empty(rows_b, H, L, device=dev)
-        rt.launch_fwd(xb[:rows_b].float().contiguous(), w, y32)
-        torch.cuda.synchronize()
-        bf16_gate = float((yb[:rows_b].float() - y32).abs().max() / y32.abs().max().clamp_min(1e-30))
-        if not bf16_gate < 2.0 ** -8:
-            raise SystemExit(f"BF16 gate failed: {bf16_gate}")
-        del xb, dyb, yb, dxb, y32
-        bf16_bytes = 2 * B * H * L * 2 + H * K * 4
-        bf16_leg = {
-            "paths": {
-                ph: {"ms": round(ms, 5),
-                     "gbps": round(bf16_bytes / (ms / 1e3) / 1e9, 1),
-                     "pct_peak": round(100 * bf16_bytes / (ms / 1e3) / 1e9 / PEAK_HBM_GBPS, 2)}
-                for ph, ms in bf16_ms.items()
-            },
-            "fwd_dx_dk_ms": round(bf16_ms["fwd"] + bf16_ms["bwd_input"] + bf16_ms["bwd_weight"], 5),
-            "gate_vs_fp32_path": float(f"{bf16_gate:.3e}"),
-            "note": "x, dY, y, dX bfloat16; taps and dK FP32; FP32 accumulation; "
-                    "algorithmic bytes (2 B H L * 2 + H K * 4) per path",
-        }
-
-    # Channels-last dK through the Flash-DWC bridge ABI (flash_dk_fp32): x and
-    # dY permuted to [B, 1, L, H] outside the timed region, dw [1, K, H]
-    # accumulated into, same loop; GZ = 1 (B % 16 == 0 and H % 32 == 0 are the
-    # bridge's own rules, so other shapes skip the leg). Gate: the row-major
-    # deterministic dK of the same data.
-    cl_leg = None
-    if B % 16 == 0 and H % 32 == 0:
-        xc = x.permute(0, 2, 1).unsqueeze(1).contiguous()
-        dyc = dy.permute(0, 2, 1).unsqueeze(1).contiguous()
-        dwc = torch.zeros(1, K, H, device=dev)
-        cl_ms = time_loop(lambda: rt.launch_bwd_weight_channels_last(xc, dyc, dwc, 1))
-        rt.launch_bwd_weight_deterministic(dy, x, gk, K)
-        rt.launch_bwd_weight_channels_last(xc, dyc, dwc, 1, zero_first=True)
-        torch.cuda.synchronize()
-        cl_gate = float((dwc[0].T - gk).abs().max() / gk.abs().max().clamp_min(1e-30))
-        if not cl_gate < 1e-5:
-            raise SystemExit(f"channels-last dK gate failed: {cl_gate}")
-        cl_gbps = runtime.algorithmic_bandwidth_gbps(runtime.minimum_algorithmic_bytes(B, H, L, K), cl_ms)
-        cl_leg = {"ms": round(cl_ms, 5), "gbps": round(cl_gbps, 1),
-                  "pct_peak": round(100 * cl_gbps / PEAK_HBM_GBPS, 2),
-                  "kernel": f"dwconv_dk_cl_kernel<{16 * ((L + 15) // 16)}>",
-                  "gate_vs_row_major": float(f"{cl_gate:.3e}"),
-                  "note": "flash_dk_fp32 (x, dY [B,1,L,H]; dw [1,K,H] accumulated), GZ=1; "
-                          "algorithmic bytes as the row-major dK"}
-        del xc, dyc, dwc
-
-    # Long rows at the reference's long-row benchmark shape (kernels/
-    # shared_l192.py, benchmarked at B16384 H128 L192 K192 by
-    # benchmark/benchmark_gmc_vs_shared_l192.py:14-17). The default kernels
-    # run on the BF16 matrix cores with three-way split FP32 operands (six
-    # part products); the FP32 matrix-core kernels (PATHTILE_LONG_ALGO=fp32)
-    # are timed beside them. Useful flops: 2 per multiply-add that touches a
-    # real element. Same loop.
-    LB, LH, LL, LK = 16384, 128, 192, 192
-    xl = torch.randn(LB, LH, LL, generator=torch.Generator().manual_seed(args.seed + 3)).to(dev)
-    dyl = torch.randn(LB, LH, LL, generator=torch.Generator().manual_seed(args.seed + 4)).to(dev)
-    wl = (torch.randn(LH, LK, generator=torch.Generator().manual_seed(args.seed + 5)) / LK ** 0.5).to(dev)
-    yl, dxl, gkl = torch.empty_like(xl), torch.empty_like(dyl), torch.empty(LH, LK, device=dev)
-    long_loops = {
-        "fwd": lambda: rt.launch_fwd_long(xl, wl, yl),
-        "bwd_input": lambda: rt.launch_bwd_input_long(dyl, wl, dxl),
-        "bwd_weight": lambda: rt.launch_bwd_weight_long(dyl, xl, gkl, LK),
-    }
-    from pathtile_amd.tune.baselines import useful_products
-    long_flops = 2 * useful_products(LB, LH, LL, LK)
-    long_bytes = 2 * LB * LH * LL * 4 + LH * LK * 4
-
-    def long_paths(ms_by_path):
-        return {ph: {"ms": round(ms, 5),
-                     "tflops_useful": round(long_flops / (ms / 1e3) / 1e12, 2),
-                     "frac_fp32_mfma_peak": round(long_flops / (ms / 1e3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
-                     "hbm_pct_peak": round(100 * long_bytes / (ms / 1e3) / 1e9 / PEAK_HBM_GBPS, 2)}
-                for ph, ms in ms_by_path.items()}
-
-    prev_long = os.environ.pop("PATHTILE_LONG_ALGO", None)
-    long_ms = {ph: time_loop(fn) for ph, fn in long_loops.items()}
-    # gate on the first 256 samples (a small copy: the profiles' copy probe
-    # is the largest plain copy of the run)
-    y_split = yl[:256].clone()
-    os.environ["PATHTILE_LONG_ALGO"] = "fp32"
-    long_ms_fp32 = {ph: time_loop(fn) for ph, fn in long_loops.items()}
-    rt.launch_fwd_long(xl, wl, yl)
-    torch.cuda.synchronize()
-    long_gate = float((y_split - yl[:256]).abs().max() / yl[:256].abs().max())
-    if prev_long is None:
-        del os.environ["PATHTILE_LONG_ALGO"]
-    else:
-        os.environ["PATHTILE_LONG_ALGO"] = prev_long
-    if not long_gate < 1e-5:
-        raise SystemExit(f"long-row split vs FP32 gate failed: {long_gate}")
-    long_leg = {
-        "config": {"B": LB, "H": LH, "L": LL, "K": LK},
-        "paths": long_paths(long_ms),
-        "fwd_dx_dk_ms": round(sum(long_ms.values()), 5),
-        "kernels": {"fwd": "dwconv_rows_long_s3_kernel<192, 192, false, true>",
-                    "bwd_input": "dwconv_rows_long_s3_kernel<192, 192, true, true>",
-                    "bwd_weight": "dwconv_dk_long_s3_kernel<192, true>"},
-        "fp32_mfma_kernels": {"paths": long_paths(long_ms_fp32),
-                              "fwd_dx_dk_ms": round(sum(long_ms_fp32.values()), 5)},
-        "gate_split_vs_fp32_fwd": float(f"{long_gate:.3e}"),
-        "note": "pt_dwconv1d_{fwd,dx,dk}_long_f32; default = BF16 matrix cores on three-way split "
-                "FP32 operands (FP32-accurate), fp32_mfma_kernels = PATHTILE_LONG_ALGO=fp32; useful "
-                "flops 2 * sum over rows of real multiply-adds; FP32 matrix peak 157.3 TFLOP/s; "
-                "HBM bytes 2 B H L 4 + H K 4 per path",
-    }
-    del xl, dyl, wl, yl, dxl, gkl
-
-    # The VALU rows kernel (the reference's lane-per-row structure, bit-exact
-    # with its fmaf chain) timed beside the default FWD/DX kernel, same loops.
-    prev = os.environ.get("PATHTILE_ROWS_ALGO")
-    os.environ["PATHTILE_ROWS_ALGO"] = "valu"
-    valu_gate = correctness_gate(rt, x, w, dy)
-    valu_ms = {"fwd": time_loop(loops["fwd"]), "bwd_input": time_loop(loops["bwd_input"])}
-    valu_kernels = {"fwd": rows_kernel_name(H, L, K, False), "bwd_input": rows_kernel_name(H, L, K, True)}
-    if prev is None:
-        del os.environ["PATHTILE_ROWS_ALGO"]
-    else:
-        os.environ["PATHTILE_ROWS_ALGO"] = prev
-
     # The reference's per-launch protocol (kernels/warp_tiled_ampere.py:
-    # 1059-1070; benchmark/benchmark_pathtile_candidate_sweep.py:274-317):
-    # an event pair around every launch; dK re-zeroed outside the events.
+    # 1059-1070): an event pair around every launch; dK re-zeroed outside.
     coll = runtime.KernelEventCollector()
     coll.enabled = True
-    for _ in range(args.steps):
+    n_ev = args.path_runs
+    for _ in range(n_ev):
         rt.launch_fwd(x, w, y, coll)
-    for _ in range(args.steps):
+    for _ in range(n_ev):
         rt.launch_bwd_input(dy, w, dx, coll)
-    for _ in range(args.steps):
+    for _ in range(n_ev):
         gk.zero_()
         rt.launch_bwd_weight(dy, x, gk, K, coll)
-    for _ in range(args.steps):
-        rt.launch_bwd_weight(dy, x, gk, K, coll, zero_first=True)
-    for _ in range(args.steps):
-        rt.launch_bwd_weight_deterministic(dy, x, gk, K, coll)
-    rows = coll.rows(synchronize=True)
-    per = {ph: [r["runtime_ms"] for r in rows if r["phase"] == ph]
-           for ph in ("fwd", "bwd_input", "bwd_weight", "bwd_weight_zero", "bwd_weight_det")}
-    assert all(len(v) == args.steps for v in per.values())
+    ev = {}
+    for r in coll.rows(synchronize=True):
+        ev.setdefault(r["phase"], []).append(r["runtime_ms"])
+    for ph, v in ev.items():
+        main_leg["paths"][ph]["per_launch_event_ms"] = round(mean(v), 5)
 
-    nbytes = runtime.minimum_algorithmic_bytes(B, H, L, K)
-    paths = {}
-    for ph, v in per.items():
-        ms = loop_ms[ph]
-        gbps = runtime.algorithmic_bandwidth_gbps(nbytes, ms)
-        paths[ph] = {"ms": round(ms, 5),
-                     "gbps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_HBM_GBPS, 2),
-                     "per_launch_event_ms": round(mean(v), 5),
-                     "per_launch_event_min_ms": round(min(v), 5)}
-    agg = paths["fwd"]["ms"] + paths["bwd_input"]["ms"] + paths["bwd_weight"]["ms"]
-    kernels = {"fwd": rows_kernel_name(H, L, K, False), "bwd_input": rows_kernel_name(H, L, K, True),
-               "bwd_weight": dk_kernel_name(H, L, cfg["dk_threads_per_block"])}
-    for ph in paths:
-        paths[ph]["kernel"] = kernels[{"bwd_weight_zero": "bwd_weight",
-                                       "bwd_weight_det": "bwd_weight"}.get(ph, ph)]
+    paths = main_leg["paths"]
+    agg = main_leg["fwd_dx_dk_ms"]
+    nbytes = main_leg["algorithmic_bytes_per_path"]
     dominant = max(("fwd", "bwd_input", "bwd_weight"), key=lambda k: paths[k]["ms"])
     tag = {"fwd": "fwd", "bwd_input": "dx", "bwd_weight": "dk"}[dominant]
     ach = paths[dominant]["gbps"]
@@ -606,28 +774,20 @@ def main(argv=None) -> int:
             "dk_threads_per_block": cfg["dk_threads_per_block"],
             "launch_config_source": cfg["source"],
         },
-        "protocol": ("value = FWD + dX + dK (atomic, excl. zero-init) mean launch times; "
-                     "each path runs `steps` back-to-back launches between two HIP events on "
-                     "the launch stream; paths.*.per_launch_event_ms = the reference's "
-                     "protocol (an event pair per launch); ms_per_step = wall time of "
+        "protocol": (f"value = FWD + dX + dK (atomic, excl. zero-init); each path: {args.trials} "
+                     f"trials x ({args.path_warmup} warm-up + {args.path_runs} timed launches back "
+                     "to back between two HIP events on the launch stream), path order reversed "
+                     "on even trials, mean of trial means (std_ms = between-trial std); "
+                     "per_launch_event_ms = an event pair per launch; ms_per_step = wall time of "
                      "`steps` interleaved FWD/dX/zero+dK steps"),
+        "value_std_ms": main_leg["fwd_dx_dk_std_ms"],
         "aggregate_gbps": round(3 * nbytes / (agg / 1e3) / 1e9, 1),
-        "aggregate_pct_peak": round(100 * 3 * nbytes / (agg / 1e3) / 1e9 / PEAK_HBM_GBPS, 2),
+        "aggregate_pct_peak": main_leg["aggregate_pct_peak"],
         "algorithmic_bytes_per_path": nbytes,
         "paths": paths,
-        "correctness_gate": {k: float(f"{v:.3e}") for k, v in gate.items()},
-        "bf16_io": bf16_leg,
-        "channels_last_dk": cl_leg,
-        "long_rows": long_leg,
-        "rows_valu": {
-            ph: {"ms": round(ms, 5), "pct_peak": round(100 * runtime.algorithmic_bandwidth_gbps(nbytes, ms)
-                                                     / PEAK_HBM_GBPS, 2),
-                 "kernel": valu_kernels[ph]}
-            for ph, ms in valu_ms.items()
-        } | {"correctness_gate": {k: float(f"{v:.3e}") for k, v in valu_gate.items()},
-             "note": "PATHTILE_ROWS_ALGO=valu: the bit-exact VALU FWD/DX kernel, same loops"},
+        "check_of_timed_outputs": main_leg["check_of_timed_outputs"],
         "roofline": {
-            "kernel": kernels[dominant],
+            "kernel": paths[dominant]["kernel"],
             "bound": "hbm",
             "achieved": ach,
             "peak": PEAK_HBM_GBPS,
@@ -637,18 +797,33 @@ def main(argv=None) -> int:
             "algorithmic_bytes": nbytes,
         },
     }
+    if not args.no_extras:
+        log("extras: BF16, channels-last, VALU FWD/dX ...")
+        line.update(extras(rt, args, dev, stream, x, w, dy, y, gk))
     if args.gpu_library_steps:
         log("GPU library baseline ...")
         line["gpu_library_baseline"] = gpu_library_baseline(x, w, dy, args.gpu_library_steps)
-    if args.s4convd_steps:
-        log("S4ConvD training steps ...")
-        line["s4convd"] = s4convd_training_steps(args.s4convd_steps, max(3, args.warmup // 4), dev)
     if args.copy_probe:
         for _ in range(args.copy_probe):
             y.copy_(x)
         torch.cuda.synchronize()
         line["copy_probe"] = {"copies": args.copy_probe, "bytes_read_per_copy": x.numel() * 4,
                               "bytes_written_per_copy": x.numel() * 4}
+    del x, w, dy, y, dx, gk
+    torch.cuda.empty_cache()
+    if not args.no_legs:
+        legs = {}
+        for name in WORKLOADS:
+            if name != args.workload:
+                legs[name] = workload_leg(rt, name, args, dev, stream)
+                log(f"{name}: {legs[name]['fwd_dx_dk_ms']:.4f} ms")
+        line["baseline_configs"] = legs
+    if not args.no_extras:
+        log("long rows ...")
+        line["long_rows"] = long_rows_leg(rt, args, dev, stream)
+    if args.s4convd_steps:
+        log("S4ConvD training steps ...")
+        line["s4convd"] = s4convd_training_steps(args.s4convd_steps, max(3, args.warmup), dev)
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         line["cpu_baseline"] = cpu_baseline(x_cpu, w_cpu, dy_cpu, args.cpu_runs)

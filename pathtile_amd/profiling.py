@@ -13,8 +13,14 @@ Three reports, each written for one workload:
             of the bytes a copy loads, ``WRITE_SIZE`` reads them exactly.
 ``valu``    VALU instruction counts and the VALU-busy fraction from
             ``SQ_INSTS_VALU`` / ``SQ_ACTIVE_INST_VALU`` / ``SQ_BUSY_CYCLES`` /
-            ``GRBM_GUI_ACTIVE``, and the MFMA-busy fraction from
-            ``SQ_VALU_MFMA_BUSY_CYCLES`` when collected.
+            ``GRBM_GUI_ACTIVE``, the MFMA-busy fraction from
+            ``SQ_VALU_MFMA_BUSY_CYCLES`` when collected, and the useful
+            FP32 work as a fraction of the vector and of the matrix FP32
+            peaks.
+``mfma``    Matrix flops each kernel issues per dispatch, from
+            ``SQ_INSTS_VALU_MFMA_MOPS_F32`` / ``..._BF16`` (units of 512
+            flops), beside its useful flops; ``--emit SUBSTR=KEY`` writes a
+            ``KEY: flops`` line per kernel for bench.py.
 
 Only the dispatches with the largest grid of each kernel, and none below a
 quarter of its median duration or counter value, are kept, so the small
@@ -26,7 +32,9 @@ Usage::
     python -m pathtile_amd.profiling traffic FETCH_DB WRITE_DB --kernel SUBSTR \
         --tag fwd --algorithmic-bytes N --copy-bytes N --command CMD --out FILE
     python -m pathtile_amd.profiling valu    DB --command CMD --out FILE \
-        --useful-fma N --clock-mhz F
+        --useful-fma SUBSTR=N --clock-mhz F
+    python -m pathtile_amd.profiling mfma    DB --command CMD --out FILE \
+        --useful-fma SUBSTR=N --emit SUBSTR=KEY
 """
 
 from __future__ import annotations
@@ -37,6 +45,8 @@ import statistics
 from pathlib import Path
 
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
+PEAK_FP32_VECTOR = 78.6e12   # MI355X, non-packed FP32 FMA on the SIMDs
+PEAK_FP32_MATRIX = 157.3e12  # MI355X dense FP32 matrix cores
 # MI355X: 256 CUs x 4 SIMDs; a wave64 VALU op occupies its SIMD16 for 4 cycles.
 NUM_SIMDS = 1024
 CYCLES_PER_WAVE_VALU = 4
@@ -182,13 +192,15 @@ def valu_report(db: str, command: str, useful_fma: dict[str, int], clock_mhz: fl
             per.setdefault(r["name"], {}).setdefault(c, []).append(r["value"])
     out = ["Command:", "", "```", command, "```", "",
            f"VALU-busy = SQ_ACTIVE_INST_VALU x {CYCLES_PER_WAVE_VALU} / ({NUM_SIMDS} SIMDs x "
-           f"GRBM_GUI_ACTIVE / {NUM_XCD} XCDs). FP32 fraction = useful FP32 FLOPs / "
-           f"(duration x 78.6 TFLOP/s non-packed vector FP32 peak; packed FP32 is off in this "
-           f"build), duration = GRBM_GUI_ACTIVE / {NUM_XCD} / {clock_mhz:.0f} MHz.", "",
+           f"GRBM_GUI_ACTIVE / {NUM_XCD} XCDs). Useful FP32 work = 2 x useful FMAs (multiply-adds "
+           f"that touch a real element) / duration, as a fraction of the 78.6 TFLOP/s "
+           f"non-packed vector FP32 peak (packed FP32 is off in this build) and of the "
+           f"157.3 TFLOP/s dense FP32 matrix peak; duration = GRBM_GUI_ACTIVE / {NUM_XCD} / "
+           f"{clock_mhz:.0f} MHz.", "",
            f"MFMA-busy = SQ_VALU_MFMA_BUSY_CYCLES / ({NUM_SIMDS} SIMDs x GRBM_GUI_ACTIVE / "
            f"{NUM_XCD} XCDs) (n/a when that counter was not collected).", "",
-           "| kernel | dispatches | waves | VALU insts | VALU insts / wave | VALU-busy | MFMA-busy | useful FMA | FP32 fraction |",
-           "|---|---|---|---|---|---|---|---|---|"]
+           "| kernel | dispatches | waves | VALU insts | VALU insts / wave | VALU-busy | MFMA-busy | useful FMA | of vector FP32 peak | of matrix FP32 peak |",
+           "|---|---|---|---|---|---|---|---|---|---|"]
     for name, cs in per.items():
         m = {c: statistics.mean(v) for c, v in cs.items()}
         n = len(cs.get("SQ_INSTS_VALU", []))
@@ -197,15 +209,52 @@ def valu_report(db: str, command: str, useful_fma: dict[str, int], clock_mhz: fl
         fma = next((v for k, v in useful_fma.items() if k in name), None)
         if fma is not None:
             secs = gui / (clock_mhz * 1e6)
-            frac = f"{2 * fma / secs / 78.6e12:.3f}"
+            frac = f"{2 * fma / secs / PEAK_FP32_VECTOR:.3f}"
+            frac_m = f"{2 * fma / secs / PEAK_FP32_MATRIX:.3f}"
             fma_s = str(fma)
         else:
-            frac, fma_s = "n/a", "n/a"
+            frac, frac_m, fma_s = "n/a", "n/a", "n/a"
         mfma = (f"{m['SQ_VALU_MFMA_BUSY_CYCLES'] / (NUM_SIMDS * gui):.3f}"
                 if "SQ_VALU_MFMA_BUSY_CYCLES" in m else "n/a")
         out.append(f"| `{short_name(name)}` | {n} | {m['SQ_WAVES']:.0f} | {m['SQ_INSTS_VALU']:.0f} | "
-                   f"{m['SQ_INSTS_VALU'] / max(m['SQ_WAVES'], 1):.0f} | {busy:.3f} | {mfma} | {fma_s} | {frac} |")
+                   f"{m['SQ_INSTS_VALU'] / max(m['SQ_WAVES'], 1):.0f} | {busy:.3f} | {mfma} | {fma_s} | "
+                   f"{frac} | {frac_m} |")
     return "\n".join(out) + "\n"
+
+
+def mfma_report(db: str, command: str, useful_fma: dict[str, int], emit: dict[str, str],
+                match: str = "pt::") -> str:
+    """Matrix flops issued per dispatch (MOPS counters x 512) per kernel."""
+    counters = ("SQ_INSTS_VALU_MFMA_MOPS_F32", "SQ_INSTS_VALU_MFMA_MOPS_BF16")
+    per = {}
+    for c in counters:
+        rows = _largest_dispatches(
+            [r for r in counter_rows(db, c) if match in r["name"]], "grid", "value")
+        for r in rows:
+            per.setdefault(r["name"], {}).setdefault(c, []).append(r["value"])
+    out = ["Command:", "", "```", command, "```", "",
+           "Issued matrix flops per dispatch = SQ_INSTS_VALU_MFMA_MOPS_<type> x 512 (mean over "
+           "the dispatches with each kernel's largest grid). Useful flops = 2 x multiply-adds "
+           "that touch a real element.", "",
+           "| kernel | dispatches | FP32 matrix flops | BF16 matrix flops | useful flops | issued / useful |",
+           "|---|---|---|---|---|---|"]
+    lines = []
+    for name, cs in per.items():
+        m = {c: statistics.mean(v) for c, v in cs.items()}
+        f32 = m.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0.0) * 512
+        bf16 = m.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0) * 512
+        if f32 == 0 and bf16 == 0:
+            continue
+        fma = next((v for k, v in useful_fma.items() if k in name), None)
+        useful = 2 * fma if fma is not None else None
+        ratio = f"{(f32 + bf16) / useful:.2f}" if useful else "n/a"
+        n = max(len(v) for v in cs.values())
+        out.append(f"| `{short_name(name)}` | {n} | {f32:.4g} | {bf16:.4g} | "
+                   f"{useful if useful is not None else 'n/a'} | {ratio} |")
+        for sub, key in emit.items():
+            if sub in name:
+                lines.append(f"{key}: {bf16 if bf16 > 0 else f32:.0f}")
+    return "\n".join(out + [""] + sorted(lines)) + "\n"
 
 
 def main(argv=None) -> int:
@@ -233,18 +282,35 @@ def main(argv=None) -> int:
     v.add_argument("--clock-mhz", type=float, default=2400.0)
     v.add_argument("--title", default="VALU utilisation")
     v.add_argument("--out", required=True)
+    m = sub.add_parser("mfma")
+    m.add_argument("db")
+    m.add_argument("--command", required=True)
+    m.add_argument("--useful-fma", action="append", default=[],
+                   help="KERNEL_SUBSTR=N useful FMAs per dispatch (repeatable)")
+    m.add_argument("--emit", action="append", default=[],
+                   help="KERNEL_SUBSTR=KEY: write 'KEY: flops' for that kernel (repeatable)")
+    m.add_argument("--title", default="Issued matrix flops")
+    m.add_argument("--out", required=True)
     a = p.parse_args(argv)
+
+    def pairs(items, conv):
+        d = {}
+        for item in items:
+            k, _, n = item.rpartition("=")
+            d[k] = conv(n)
+        return d
+
     if a.cmd == "trace":
         text = f"# {a.title}\n\n" + trace_report(a.db, a.command)
     elif a.cmd == "traffic":
         text = traffic_report(a.fetch_db, a.write_db, a.kernel, a.tag, a.algorithmic_bytes,
                               a.copy_bytes, a.command)
+    elif a.cmd == "valu":
+        text = f"# {a.title}\n\n" + valu_report(a.db, a.command, pairs(a.useful_fma, int),
+                                                a.clock_mhz)
     else:
-        fma = {}
-        for item in a.useful_fma:
-            k, _, n = item.rpartition("=")
-            fma[k] = int(n)
-        text = f"# {a.title}\n\n" + valu_report(a.db, a.command, fma, a.clock_mhz)
+        text = f"# {a.title}\n\n" + mfma_report(a.db, a.command, pairs(a.useful_fma, int),
+                                                pairs(a.emit, str))
     Path(a.out).parent.mkdir(parents=True, exist_ok=True)
     Path(a.out).write_text(text)
     print(text)
