@@ -73,6 +73,7 @@ def _run_phase(name, cases, args, out: Path, log) -> list[dict]:
     for trial in range(1, args.trials + 1):
         res = run_trial(cases, trial, args.warmup, args.runs, args.seed, log=log)
         _write_csv(out / f"{name}_trial{trial}.csv", res["summary"])
+        _write_csv(out / f"{name}_control_trial{trial}.csv", res["control"])
         rows += res["summary"]
         validation += res["validation"]
         metas.append(res["metadata"])
@@ -81,21 +82,36 @@ def _run_phase(name, cases, args, out: Path, log) -> list[dict]:
     return rows
 
 
+def _phase_rows(out: Path, name: str) -> tuple[list[dict], list[dict]]:
+    rows = sum((_read_csv(p) for p in sorted(out.glob(f"{name}_trial*.csv"))), [])
+    ctrl = sum((_read_csv(p) for p in sorted(out.glob(f"{name}_control_trial*.csv"))), [])
+    return select.mean_of_trials(rows), select.mean_of_trials(ctrl)
+
+
 def build_report(out: Path, policy: dict) -> dict:
-    """Regret tables from the CSVs in `out` (no device needed)."""
-    train = select.mean_of_trials(sum((_read_csv(p) for p in sorted(out.glob("train_trial*.csv"))), []))
-    hold = select.mean_of_trials(sum((_read_csv(p) for p in sorted(out.glob("holdout_trial*.csv"))), []))
+    """Regret tables from the CSVs in `out` (no device needed): the
+    reference's summary per phase, per-path regret, the (shape, path) pairs
+    where the FWD/dX knob cannot change the kernel, the regret over the
+    knobs that can, and the noise floor from the duplicate control."""
+    train, train_ctrl = _phase_rows(out, "train")
+    hold, hold_ctrl = _phase_rows(out, "holdout")
     recomputed = select.select_policy(train)
     if recomputed != policy["selected"]:
         raise AssertionError(f"frozen policy {policy['selected']} != training-only reconstruction {recomputed}")
     metas = json.loads((out / "holdout_metadata.json").read_text())
     select.verify_frozen_before_holdout(policy, [m["created_at_utc"] for m in metas])
-    train_per, train_sum = select.holdout_regret(train, recomputed)
-    hold_per, hold_sum = select.holdout_regret(hold, recomputed)
-    _write_csv(out / "train_per_shape.csv", train_per)
-    _write_csv(out / "holdout_per_shape.csv", hold_per)
-    report = {"policy": recomputed, "train": train_sum, "holdout": hold_sum,
-              "device_name": policy.get("device_name")}
+    report = {"policy": recomputed, "device_name": policy.get("device_name"),
+              "knob_inert_rule": select.KNOB_INERT_RULE}
+    for name, rows, ctrl in (("train", train, train_ctrl), ("holdout", hold, hold_ctrl)):
+        per, summary = select.holdout_regret(rows, recomputed)
+        for r in per:
+            r["fwd_dx_knob_inert"] = select.fwd_dx_knob_inert(r["H"], r["L"], r["K"])
+        _write_csv(out / f"{name}_per_shape.csv", per)
+        summary["per_path"] = select.path_regret(rows, recomputed)
+        summary["knob_active_paths"] = select.active_knob_regret(rows, recomputed)
+        if ctrl:
+            summary["noise_floor"] = select.noise_floor(rows, ctrl)
+        report[name] = summary
     (out / "report.json").write_text(json.dumps(report, indent=2))
     return report
 

@@ -187,3 +187,102 @@ def verify_frozen_before_holdout(policy: dict, holdout_created_at: Iterable[str]
     for stamp in holdout_created_at:
         if not frozen_at < datetime.fromisoformat(str(stamp)):
             raise AssertionError(f"Policy timestamp {frozen_at} is not before holdout trial {stamp}")
+
+
+# --------------------------------------------------------------------------
+# Additions on MI355X: per-path regret, the pairs where a knob cannot act,
+# and the noise floor of two measurements of one configuration.
+# --------------------------------------------------------------------------
+KNOB_INERT_RULE = (
+    "FWD/dX waves per workgroup cannot change the kernel where the matrix-core "
+    "FWD/dX kernel serves (L % 4 == 0, H % 8 == 0 and >= 10.5 (LMAX / L)^2 useful "
+    "FMAs per output, LMAX = 16 ceil(L / 16)): it always runs 8-wave workgroups. "
+    "There the FWD/dX candidates differ only by measurement noise.")
+
+
+def _useful_fma_per_row(L: int, K: int) -> int:
+    p = K // 2
+    return sum(max(0, min(L, L - (j - p)) - max(0, p - j)) for j in range(K))
+
+
+def fwd_dx_knob_inert(H: int, L: int, K: int) -> bool:
+    """True where the FWD/dX knob cannot change the kernel (the library's
+    matrix-core rule for 16-byte aligned rows, as the tuner allocates)."""
+    H, L, K = int(H), int(L), int(K)
+    lmax = 16 * ((L + 15) // 16)
+    return L % 4 == 0 and H % 8 == 0 and 2 * _useful_fma_per_row(L, K) * L >= 21 * lmax * lmax
+
+
+def path_regret(rows: list[dict], policy: dict[str, int]) -> dict[str, dict]:
+    """Per path: sum over shapes of the frozen candidate's time against the
+    per-shape fastest, and the mean of the per-shape path regrets."""
+    orc = oracle(rows)
+    out = {}
+    for phase, key in POLICY_KEYS.items():
+        shapes = sorted({c for (c, ph) in orc if ph == phase})
+        frozen = [selected_time(rows, c, phase, policy[key]) for c in shapes]
+        best = [orc[(c, phase)]["winner_mean_ms"] for c in shapes]
+        regs = [(f / b - 1.0) * 100.0 for f, b in zip(frozen, best)]
+        out[phase] = {
+            "shapes": len(shapes),
+            "sum_regret_pct": normalize_roundoff((sum(frozen) / sum(best) - 1.0) * 100.0),
+            "mean_regret_pct": normalize_roundoff(sum(regs) / len(regs)),
+            "max_regret_pct": normalize_roundoff(max(regs)),
+        }
+        if phase != "bwd_weight":
+            inert = [c for c in shapes if fwd_dx_knob_inert(*_hlk(rows, c))]
+            out[phase]["shapes_knob_inert"] = len(inert)
+    return out
+
+
+def _hlk(rows: list[dict], config_id: str) -> tuple[int, int, int]:
+    r = next(r for r in rows if r["config_id"] == config_id)
+    return int(r["H"]), int(r["L"]), int(r["K"])
+
+
+def active_knob_regret(rows: list[dict], policy: dict[str, int]) -> dict:
+    """Regret of the frozen policy when the FWD/dX paths whose knob cannot
+    act count at the frozen candidate's time on both sides (their spread is
+    measurement noise, not a choice the policy could improve)."""
+    orc = oracle(rows)
+    regs = []
+    for cid in sorted({r["config_id"] for r in rows}):
+        inert = fwd_dx_knob_inert(*_hlk(rows, cid))
+        frozen = best = 0.0
+        for phase, key in POLICY_KEYS.items():
+            f = selected_time(rows, cid, phase, policy[key])
+            frozen += f
+            best += f if (inert and phase != "bwd_weight") else orc[(cid, phase)]["winner_mean_ms"]
+        regs.append((frozen / best - 1.0) * 100.0)
+    return {"shapes": len(regs), "mean_regret_pct": normalize_roundoff(sum(regs) / len(regs)),
+            "max_regret_pct": normalize_roundoff(max(regs))}
+
+
+def noise_floor(rows: list[dict], control: list[dict]) -> dict:
+    """Two measurements of one configuration per (shape, path): the control
+    rows repeat a candidate that the sweep also measured. Reported: the mean
+    relative difference per path, and the regret that the repeated
+    configuration shows against the faster of its two measurements (a policy
+    can show this much regret from noise alone)."""
+    per_path: dict[str, list[float]] = {}
+    regs = []
+    shapes = sorted({r["config_id"] for r in control})
+    for cid in shapes:
+        first = second = 0.0
+        for phase in PHASES:
+            c = next(r for r in control if r["config_id"] == cid and r["phase"] == phase)
+            a = selected_time(rows, cid, phase, int(c["candidate_value"]))
+            b = float(c["mean_ms"])
+            per_path.setdefault(phase, []).append(abs(a - b) / a * 100.0)
+            first += a
+            second += min(a, b)
+        regs.append((first / second - 1.0) * 100.0)
+    return {
+        "control_values": {ph: int(next(r for r in control if r["phase"] == ph)["candidate_value"])
+                           for ph in PHASES},
+        "shapes": len(shapes),
+        "mean_abs_diff_pct": {ph: normalize_roundoff(sum(v) / len(v)) for ph, v in per_path.items()},
+        "mean_regret_pct": normalize_roundoff(sum(regs) / len(regs)),
+        "max_regret_pct": normalize_roundoff(max(regs)),
+    }
+

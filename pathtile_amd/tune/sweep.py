@@ -39,6 +39,16 @@ FWD_DX_CANDIDATES = (1, 2, 4, 8)
 DK_CANDIDATES = (64, 128, 192, 256, 384, 512)
 
 
+def control_specs() -> list[tuple[str, int]]:
+    """Duplicate control: the runtime's current launch values (the installed
+    frozen policy), timed a second time per shape after every candidate, so
+    two measurements of one configuration give the regret's noise floor
+    (scripts/aggregate_pathtile_results.py:223-240 reads regret against such
+    a floor). Their rows never enter the selection."""
+    return [(FWD_DX_KIND, int(rt.DEFAULT_WAVES_PER_BLOCK)),
+            (DK_KIND, int(rt.DEFAULT_BWDK_BLOCK))]
+
+
 def utc_now() -> str:
     return datetime.now(timezone.utc).isoformat()
 
@@ -201,8 +211,9 @@ def run_trial(cases: list[ShapeCase], trial_id: int, warmup: int, runs: int,
     created = utc_now()
     order = list(reversed(cases)) if trial_id % 2 == 0 else list(cases)
     specs = candidate_specs(trial_id)
+    controls = control_specs()
     runtimes = {(k, v): make_runtime(k, v) for k, v in specs}
-    summary, validation = [], []
+    summary, control, validation = [], [], []
     t0 = time.time()
     for case in order:
         seed = case_seed(base_seed, case)
@@ -214,6 +225,12 @@ def run_trial(cases: list[ShapeCase], trial_id: int, warmup: int, runs: int,
             times = measure_candidate(runtimes[(kind, value)], kind, sets, k, warmup, runs)
             for phase, vals in times.items():
                 summary.append({**case.as_dict(), "trial_id": trial_id, "candidate_kind": kind,
+                                "candidate_value": value, "phase": phase,
+                                "buffer_sets": len(sets), **stats(vals)})
+        for kind, value in controls:
+            times = measure_candidate(runtimes[(kind, value)], kind, sets, k, warmup, runs)
+            for phase, vals in times.items():
+                control.append({**case.as_dict(), "trial_id": trial_id, "candidate_kind": kind,
                                 "candidate_value": value, "phase": phase,
                                 "buffer_sets": len(sets), **stats(vals)})
         del x, k, gy, sets
@@ -233,4 +250,5 @@ def run_trial(cases: list[ShapeCase], trial_id: int, warmup: int, runs: int,
                                 "stream, cycling buffer sets past the 256 MiB MALL; dK "
                                 "zero-fill outside the event; mean of trial means",
     }
-    return {"summary": summary, "validation": validation, "metadata": meta}
+    meta["control"] = {kind: value for kind, value in controls}
+    return {"summary": summary, "control": control, "validation": validation, "metadata": meta}

@@ -194,3 +194,67 @@ def test_baselines_on_the_committed_tuner_results():
     assert out["coverage_budget_sweep"][-1]["policy"] == frozen
     for name, r in out["policies"].items():
         assert r["holdout"]["shapes"] == 10 and r["train"]["shapes"] == 20, name
+
+
+def _shape_rows(cid, H, L, K, times):
+    """times: {phase: {value: ms}} for one shape."""
+    out = []
+    for phase, by_value in times.items():
+        for v, ms in by_value.items():
+            out.append({"config_id": cid, "B": 64, "H": H, "L": L, "K": K, "phase": phase,
+                        "candidate_value": v, "mean_ms": ms})
+    return out
+
+
+def test_fwd_dx_knob_inert_follows_the_library_rule():
+    # matrix cores: L % 4 == 0, H % 8 == 0 and >= 10.5 (LMAX / L)^2 useful FMAs per output
+    assert select.fwd_dx_knob_inert(128, 48, 48)      # P
+    assert select.fwd_dx_knob_inert(128, 48, 47)      # E2
+    assert not select.fwd_dx_knob_inert(256, 48, 4)   # S: short chain, VALU kernel
+    assert not select.fwd_dx_knob_inert(96, 37, 48)   # E1: L % 4 != 0
+    assert not select.fwd_dx_knob_inert(12, 48, 48)   # H % 8 != 0
+    # the useful-FMA threshold against a brute-force count: L = 40 (LMAX 48)
+    L, K = 40, 32
+    p = K // 2
+    useful = sum(1 for t in range(L) for j in range(K) if 0 <= t + j - p < L)
+    assert select._useful_fma_per_row(L, K) == useful
+    assert select.fwd_dx_knob_inert(64, L, K) == (2 * useful * L >= 21 * 48 * 48)
+
+
+def test_per_path_and_active_knob_regret():
+    pol = {"fwd_waves_per_block": 2, "dx_waves_per_block": 2, "dk_threads_per_block": 128}
+    rows = []
+    # shape a: FWD/dX knob inert (P-like); fwd candidate 4 is 10% faster by noise
+    rows += _shape_rows("a", 128, 48, 48, {"fwd": {2: 1.1, 4: 1.0}, "bwd_input": {2: 1.0, 4: 1.0},
+                                           "bwd_weight": {128: 2.0, 256: 2.0}})
+    # shape b: VALU shapes (knob active); dk candidate 256 is 25% faster
+    rows += _shape_rows("b", 256, 48, 4, {"fwd": {2: 1.0, 4: 1.5}, "bwd_input": {2: 1.0, 4: 1.0},
+                                          "bwd_weight": {128: 2.5, 256: 2.0}})
+    per = select.path_regret(rows, pol)
+    assert per["fwd"]["sum_regret_pct"] == pytest.approx((2.1 / 2.0 - 1) * 100)
+    assert per["fwd"]["mean_regret_pct"] == pytest.approx(5.0)
+    assert per["fwd"]["shapes_knob_inert"] == 1 and "shapes_knob_inert" not in per["bwd_weight"]
+    assert per["bwd_weight"]["max_regret_pct"] == pytest.approx(25.0)
+    _, total = select.holdout_regret(rows, pol)
+    act = select.active_knob_regret(rows, pol)
+    # a: the inert FWD noise no longer counts -> 0; b: 4.5 / 4.0 -> 12.5%
+    assert act["mean_regret_pct"] == pytest.approx(6.25)
+    assert total["mean_regret_pct"] == pytest.approx(((4.1 / 4.0 - 1) + (4.5 / 4.0 - 1)) * 50)
+
+
+def test_noise_floor_from_the_duplicate_control():
+    rows = _shape_rows("a", 128, 48, 48, {"fwd": {2: 1.0}, "bwd_input": {2: 1.0},
+                                          "bwd_weight": {128: 2.0}})
+    rows += _shape_rows("b", 128, 48, 48, {"fwd": {2: 1.0}, "bwd_input": {2: 1.0},
+                                           "bwd_weight": {128: 2.0}})
+    ctrl = _shape_rows("a", 128, 48, 48, {"fwd": {2: 0.9}, "bwd_input": {2: 1.1},
+                                          "bwd_weight": {128: 2.0}})
+    ctrl += _shape_rows("b", 128, 48, 48, {"fwd": {2: 1.0}, "bwd_input": {2: 1.0},
+                                           "bwd_weight": {128: 2.2}})
+    nf = select.noise_floor(rows, ctrl)
+    assert nf["control_values"] == {"fwd": 2, "bwd_input": 2, "bwd_weight": 128}
+    assert nf["mean_abs_diff_pct"]["fwd"] == pytest.approx(5.0)
+    assert nf["mean_abs_diff_pct"]["bwd_weight"] == pytest.approx(5.0)
+    # a: 4.0 against 3.9 (the faster of each pair); b: 4.0 against 4.0
+    assert nf["mean_regret_pct"] == pytest.approx((4.0 / 3.9 - 1) * 50)
+    assert nf["max_regret_pct"] == pytest.approx((4.0 / 3.9 - 1) * 100)
