@@ -78,8 +78,9 @@ const char* pt_status_string(int status);
  * least 10.5 (LMAX / L)^2 useful FMAs per output on average (LMAX =
  * 16 ceil(L / 16)) and the layout allows it (L % 4 == 0, H % 8 == 0, x and
  * y 16-byte aligned), the channel-group matrix-core kernel runs instead:
- * eight waves (channels) per workgroup whatever waves_per_block says, so
- * every value is accepted there and gives the same bits; it sums in the
+ * 8 waves (channels) per workgroup, or 16 for rows of 33-48 columns when
+ * H % 16 == 0, whatever waves_per_block says, so every value is accepted
+ * there and gives the same bits; it sums in the
  * matrix cores' order (within FP32 rounding of the reference: about 3e-7
  * max-abs-scaled against FP64). On both kernels an Inf or NaN input or tap
  * reaches exactly the outputs whose reference window holds it (those

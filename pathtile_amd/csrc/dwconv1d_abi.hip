@@ -431,8 +431,8 @@ static RowsAlgo rows_algo(int L, int K) {
 
 // Launch of the channel-group kernel: one workgroup per (channel group,
 // sample range), the ranges interleaved in 16-sample steps. As many ranges as
-// fill the CUs with min(2, resident) workgroups each (two measured best where
-// the LDS allows them, L <= 32; at L = 48 one fits).
+// fill the CUs with min(max_per_cu, resident) workgroups each (two 8-channel
+// workgroups measured best where the LDS allows them, L <= 32; one above).
 // hc: channels (= waves) per workgroup; lds: dynamic LDS per workgroup;
 // max_per_cu: workgroups per CU the range count is sized for (at most what
 // fits).
@@ -456,13 +456,25 @@ static int rows_cg_launch(Fn fn, const T* in, const float* w, T* out, int B,
   return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream, args);
 }
 
-// Eight channels (waves) per workgroup whatever the caller's waves per
-// block: measured on MI355X at 1, 2, 4, 8 and 16 channels, 8 was fastest or
-// within 3% everywhere (at P: 227, 171, 156, 140 us for 1 to 8), while the
-// VALU kernel that serves the other shapes wants 1 to 4 waves per workgroup
-// (at S: 553-568 us against 606 at 8), so one knob cannot serve both.
+// Channels (waves) per workgroup, whatever the caller's waves per block:
+//  * rows of 33-48 columns with H % 16 == 0: 16, one per CU, with one input
+//    and two output stages in LDS (148 KB at L = 48). Each step then moves
+//    16 segments of 3 KB instead of 1.5 KB; a copy kernel with the same
+//    access pattern ran in 129.8 us at P against 136.4 us for 1.5 KB
+//    segments, and the kernel itself 3-6% faster on every such shape tried
+//    (P: 133.7 against 142.4 us FWD);
+//  * otherwise 8, two per CU where the LDS allows (two input and two output
+//    stages). Measured on MI355X at 1, 2, 4 and 8 channels, 8 was fastest
+//    (at P: 227, 171, 156, 140 us).
+// The VALU kernel that serves the other shapes wants 1 to 4 waves per
+// workgroup (at S: 553-568 us against 606 at 8), so one knob cannot serve
+// both kernels.
 static int rows_cg_path(bool dx, const float* in, const float* w, float* out,
                         int B, int H, int L, int K, void* stream) {
+  if (mfma_index(L) == 2 && H % 16 == 0 &&
+      rows_cg_lds_bytes(L, 16, 1) <= (size_t)max_lds_per_block())
+    return rows_cg_launch(kRowsCg16Table[dx ? 1 : 0], in, w, out, B, H, L, K, stream, 16,
+                          rows_cg_lds_bytes(L, 16, 1), 1);
   return rows_cg_launch(kRowsCgTable[dx ? 1 : 0][mfma_index(L)], in, w, out, B,
                         H, L, K, stream, kRowsCgWaves, rows_cg_lds_bytes(L), 2);
 }

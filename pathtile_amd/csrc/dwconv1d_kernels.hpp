@@ -892,13 +892,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_t(const T* base) {
   return make_rsrc(reinterpret_cast<const float*>(base));
 }
 
-__host__ __device__ constexpr size_t rows_cg_lds_bytes(int L, int hc = kRowsCgWaves) {
-  // two input + two output stages of 16 samples x (HC * L + 4) floats
-  return (size_t)4 * kRowsCgStep * (hc * L + 4) * sizeof(float);
+__host__ __device__ constexpr size_t rows_cg_lds_bytes(int L, int hc = kRowsCgWaves,
+                                                       int nin = 2) {
+  // nin input + two output stages of 16 samples x (HC * L + 4) floats
+  return (size_t)(nin + 2) * kRowsCgStep * (hc * L + 4) * sizeof(float);
 }
 
 // kDepth: steps in flight in registers; HC: channels (= waves) per
-// workgroup.
+// workgroup; NIN: input stages in LDS. With two, one barrier per step
+// separates the MFMAs of step s (and the input store of step s + 1) from
+// the output flush of step s. With one (16 channels at L = 48, whose two
+// input and two output stages would not fit), a second barrier per step
+// keeps the input store of step s + 1 after every wave's reads of step s.
 //
 // Non-finite values. The band matrix multiplies every input column of a
 // sample by every output column's taps, zeros included, so one Inf or NaN
@@ -915,7 +920,7 @@ __host__ __device__ constexpr size_t rows_cg_lds_bytes(int L, int hc = kRowsCgWa
 // terms of which some are infinite or NaN has the same non-finite value in
 // any order (sums that overflow FP32 aside). A wave whose lanes all see
 // finite first outputs skips the chain.
-template <int LMAX, bool DX, int kDepth, int HC = kRowsCgWaves>
+template <int LMAX, bool DX, int kDepth, int HC = kRowsCgWaves, int NIN = 2>
 __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
     const float* __restrict__ in, const float* __restrict__ w,
     float* __restrict__ out, int B, int H, int L, int K, int nranges,
@@ -941,8 +946,8 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
   const int per = kRowsCgStep * segc;     // chunks per stage
   const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
   const uint32_t grp_bytes = (uint32_t)g * (uint32_t)seg * 4u;
-  float* inl = lds;                       // input stages 0, 1
-  float* outl = lds + 2 * sz;             // output stages 0, 1
+  float* inl = lds;                       // input stage(s)
+  float* outl = lds + NIN * sz;           // output stages 0, 1
 
   // Loop-invariant part of each staged chunk (as in the DK kernel).
   int ek[kNpt];
@@ -1002,7 +1007,7 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
   const int rq = 4 * kk;
   const int cb = wave * L;
   auto mfma_step = [&](int s) {
-    const float* row = inl + (s & 1) * sz + jj * sk + cb;  // sample jj, this channel
+    const float* row = inl + (NIN == 2 ? (s & 1) : 0) * sz + jj * sk + cb;  // sample jj, this channel
     const float* src = row + NU * kk;
     float* orow = outl + (s & 1) * sz + jj * sk + cb;
     float a[NU];
@@ -1051,7 +1056,7 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
     }
   };
 
-  if (nsteps > 0) {
+  if (nsteps > 0 && NIN == 2) {
 #pragma unroll
     for (int d = 0; d < kDepth; ++d)
       if (d < nsteps) load_step(d, stg[d]);
@@ -1071,6 +1076,28 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
             if (s + 1 + kDepth < nsteps)
               load_step(s + 1 + kDepth, stg[(d + 1) % kDepth]);
           }
+          __syncthreads();
+          flush_out(s);
+        }
+      }
+    }
+  } else if (nsteps > 0) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d)
+      if (d < nsteps) load_step(d, stg[d]);
+    for (int s0 = 0; s0 < nsteps; s0 += kDepth) {
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) {
+        const int s = s0 + d;
+        if (s < nsteps) {
+          // The input stage was last read by mfma_step(s - 1), which every
+          // thread finished before the second barrier of step s - 1; output
+          // stage s & 1 was last read by flush_out(s - 2), finished before
+          // the first barrier of step s - 1.
+          store_stage(0, stg[d]);
+          if (s + kDepth < nsteps) load_step(s + kDepth, stg[d]);
+          __syncthreads();
+          mfma_step(s);
           __syncthreads();
           flush_out(s);
         }

@@ -38,6 +38,8 @@ using RowsCgFn = void (*)(const float*, const float*, float*, int, int, int,
                           int, int, uint32_t);
 // channel-group matrix-core FWD / DX: [0 = FWD, 1 = DX][row bucket 16, 32, 48]
 extern const RowsCgFn kRowsCgTable[2][3];
+// 16-channel workgroups with one input stage, row bucket 48: [0 = FWD, 1 = DX]
+extern const RowsCgFn kRowsCg16Table[2];
 // BF16 I/O (uint16_t bit patterns; FP32 taps, FP32 accumulation)
 using RowsCgBf16Fn = void (*)(const uint16_t*, const float*, uint16_t*, int,
                               int, int, int, int, uint32_t);

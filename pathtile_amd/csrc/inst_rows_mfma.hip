@@ -8,4 +8,6 @@ const RowsCgFn kRowsCgTable[2][3] = {
      &dwconv_rows_cg_kernel<48, false, 2>},
     {&dwconv_rows_cg_kernel<16, true, 2>, &dwconv_rows_cg_kernel<32, true, 2>,
      &dwconv_rows_cg_kernel<48, true, 2>}};
+const RowsCgFn kRowsCg16Table[2] = {&dwconv_rows_cg_kernel<48, false, 2, 16, 1>,
+                                    &dwconv_rows_cg_kernel<48, true, 2, 16, 1>};
 }  // namespace pt

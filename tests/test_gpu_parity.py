@@ -137,6 +137,12 @@ def test_fwd_dx_bit_exact_and_fp64(rt, shape, algo, monkeypatch):
     (513, 8, 8, 3),       # short filter, forced onto the matrix cores
     (4096, 8, 48, 48),    # one channel group, many interleaved ranges
     (40, 4800, 16, 16),   # 600 channel groups, more than two per CU: one range each
+    # 16-channel workgroups (rows of 33-48 columns, H % 16 == 0), one input stage
+    (1, 16, 48, 48),      # a single ragged step
+    (33, 32, 36, 32),     # L below the bucket, ragged last step
+    (4096, 16, 48, 48),   # one channel group, many interleaved ranges
+    (100, 48, 40, 24),    # three channel groups, odd-ish K
+    (257, 16, 44, 47),    # odd K, ragged
 ])
 def test_fwd_dx_matrix_core_kernel(rt, shape, monkeypatch):
     """The channel-group matrix-core kernel (forced) against FP64 on the
