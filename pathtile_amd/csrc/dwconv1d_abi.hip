@@ -163,10 +163,13 @@ struct DkGeom {
 };
 
 // Channel-group DK: whole 16-byte aligned rows (L % 4 == 0) in groups of
-// kCgChannelsPerWave channels per wave, at most 8 waves per workgroup.
-static bool dk_cg_ok(int H, int L, int threads) {
+// dk_cpw(L) channels per wave (one in the 48-column row bucket, two below;
+// BF16 DK: two), at most 8 waves per workgroup.
+static int dk_cpw(int L) { return dk_cg_cpw(16 * (mfma_index(L) + 1)); }
+
+static bool dk_cg_ok(int H, int L, int threads, int cpw) {
   const int wpb = threads / kWave;
-  return L % 4 == 0 && wpb <= 8 && H % (kCgChannelsPerWave * wpb) == 0;
+  return L % 4 == 0 && wpb <= 8 && H % (cpw * wpb) == 0;
 }
 
 // Tensors of at least the 256 MiB MALL stream differently from smaller ones
@@ -253,10 +256,10 @@ static DkGeom dk_geometry(int B, int H, int L, int K, int threads, bool vec16,
   g.wpb = threads / kWave;
   const long long wpb = g.wpb;
   const long long rows = (long long)B * H;
-  g.cg = g.algo == kDkMfma && vec16 && dk_cg_ok(H, L, threads);
+  g.cg = g.algo == kDkMfma && vec16 && dk_cg_ok(H, L, threads, dk_cpw(L));
   g.nt = g.cg && cg_large(B, H, L);
   if (g.cg) {
-    const long long ngroups = (long long)H / (kCgChannelsPerWave * wpb);
+    const long long ngroups = (long long)H / (dk_cpw(L) * wpb);
     const long long nr = cg_ranges(B, H, L);
     g.rows_per_wave = 0;
     g.nbt = (int)nr;
@@ -539,7 +542,7 @@ static int dk_path(bool det, const float* gy, const float* x, float* dst,
   int rpw = g.rows_per_wave, nbt = g.nbt, d = det ? 1 : 0;
   if (g.cg) {
     DkCgFn fn = (g.nt ? kDkCgTableNT : kDkCgTable)[mfma_index(L)];
-    const size_t lds = cg_lds_bytes(16 * (mfma_index(L) + 1), g.wpb, L);
+    const size_t lds = cg_lds_bytes(16 * (mfma_index(L) + 1), g.wpb, L, dk_cpw(L));
     void* args[] = {&gy, &x, &dst, &B, &H, &L, &K, &nbt, &nblocks, &d};
     return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream,
                   args);
@@ -599,7 +602,8 @@ static int bf16_rows_path(bool dx, const void* in, const float* w, void* out,
 static int bf16_dk_check(int B, int H, int L, int K, int threads) {
   int st = check_shape(B, H, L, K);
   if (st != PT_OK) return st;
-  if (!valid_dk_threads(threads) || !dk_cg_ok(H, L, threads)) return PT_ERR_CONFIG;
+  if (!valid_dk_threads(threads) || !dk_cg_ok(H, L, threads, kCgChannelsPerWave))
+    return PT_ERR_CONFIG;
   return PT_OK;
 }
 
@@ -962,7 +966,7 @@ int pt_dynamic_lds_bytes(int kernel_id, int L, int K, int block_config,
       if (!pt::valid_dk_threads(block_config) || block_config > 8 * pt::kWave)
         return PT_ERR_CONFIG;
       *lds_bytes = (int)pt::cg_lds_bytes(16 * (pt::mfma_index(L) + 1),
-                                         block_config / pt::kWave, L);
+                                         block_config / pt::kWave, L, pt::dk_cpw(L));
       return PT_OK;
     case PT_KERNEL_FWD_CG:
     case PT_KERNEL_DX_CG:

@@ -1293,7 +1293,8 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_bf16mma_kernel(
 // one 192-byte row per channel: full cache lines, and no line shared with a
 // channel that another workgroup reads.
 //
-// Workgroup (g, r) owns channel group g of HC = kCgChannelsPerWave * wpb
+// Workgroup (g, r) owns channel group g of HC = CPW * wpb (CPW channels per
+// wave: dk_cg_cpw(LMAX))
 // channels and the interleaved steps r, r + nranges, r + 2 nranges, ... of
 // 4 samples each. At any moment the running workgroups therefore cover one
 // compact window of nranges steps of the whole [b, :, :] tensor; the host
@@ -1311,6 +1312,12 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_bf16mma_kernel(
 // channel per workgroup.
 // ---------------------------------------------------------------------------
 constexpr int kCgChannelsPerWave = 2;
+
+// Channels per wave of the FP32 row-major DK for a row bucket: one in the
+// 48-column bucket (16 resident waves per CU with half the matrix work each,
+// 3-7% faster at L = 40-48 with 256 or more threads per workgroup), two
+// below (one per wave was 5-25% slower at L = 24 and H = 256).
+__host__ __device__ constexpr int dk_cg_cpw(int lmax) { return lmax >= 48 ? 1 : 2; }
 constexpr int kCgStep = 4;      // samples per stage (the MFMA K)
 constexpr int kCgPad = 16;      // floats between the samples of a stage
 constexpr int kCgDepth = 2;     // steps in flight in registers
@@ -1324,11 +1331,12 @@ struct CgGeo {
 
 // Dynamic LDS of the channel-group DK kernel: two stages of both tensors,
 // or, for the epilogue, one D tile per wave plus the workgroup's tap sums.
-__host__ __device__ constexpr size_t cg_lds_bytes(int lmax, int wpb, int L) {
+__host__ __device__ constexpr size_t cg_lds_bytes(int lmax, int wpb, int L,
+                                                  int cpw) {
   const size_t stages =
-      (size_t)2 * 2 * kCgStep * (kCgChannelsPerWave * wpb * L + kCgPad);
+      (size_t)2 * 2 * kCgStep * (cpw * wpb * L + kCgPad);
   const size_t dtile = (size_t)wpb * (16 * (lmax / 16)) * (16 * (lmax / 16) + 1) +
-                       (size_t)kCgChannelsPerWave * wpb * kMaxK;
+                       (size_t)cpw * wpb * kMaxK;
   return (stages > dtile ? stages : dtile) * sizeof(float);
 }
 
@@ -1343,14 +1351,13 @@ __host__ __device__ constexpr size_t cg_lds_bytes(int lmax, int wpb, int L) {
 // and channel, which contended badly at small K). det: write the sums as
 // partials [h][j][nranges] instead. CL: dk is [K][H] (the channels-last
 // layout's dw), whose hc channels of one tap are contiguous; atomics only.
-template <int LMAX, bool CL = false>
+template <int LMAX, bool CL = false, int CPW = kCgChannelsPerWave>
 __device__ __forceinline__ void dk_cg_epilogue(
-    const f32x4 (&acc)[kCgChannelsPerWave][LMAX / 16][LMAX / 16], float* lds,
+    const f32x4 (&acc)[CPW][LMAX / 16][LMAX / 16], float* lds,
     float* __restrict__ dst, int wave, int wpb, int g, int r, int hc, int L,
     int K, int nranges, int det, int H = 0) {
   using G = CgGeo<LMAX>;
   constexpr int NT = G::nt;
-  constexpr int CPW = kCgChannelsPerWave;
   const int lane = threadIdx.x & (kWave - 1);
   const int nthreads = blockDim.x;
   float* dt = lds + wave * (G::dim * G::dstride);
@@ -1406,14 +1413,13 @@ __device__ __forceinline__ void dk_cg_epilogue(
   }
 }
 
-template <int LMAX, int LOAD_CPOL = kCpolNone>
+template <int LMAX, int LOAD_CPOL = kCpolNone, int CPW = dk_cg_cpw(LMAX)>
 __global__ __launch_bounds__(512) void dwconv_dk_cg_kernel(
     const float* __restrict__ gy, const float* __restrict__ x,
     float* __restrict__ dst, int B, int H, int L, int K, int nranges,
     uint32_t nblocks, int det) {
   using G = CgGeo<LMAX>;
   constexpr int NT = G::nt;
-  constexpr int CPW = kCgChannelsPerWave;
   constexpr int DEPTH = kCgDepth;
   extern __shared__ float lds[];
 
@@ -1542,7 +1548,7 @@ __global__ __launch_bounds__(512) void dwconv_dk_cg_kernel(
     }
   }
 
-  dk_cg_epilogue<LMAX>(acc, lds, dst, wave, wpb, g, r, hc, L, K, nranges, det);
+  dk_cg_epilogue<LMAX, false, CPW>(acc, lds, dst, wave, wpb, g, r, hc, L, K, nranges, det);
 }
 
 // ---------------------------------------------------------------------------
