@@ -57,6 +57,10 @@ extern "C" {
 #define PT_KERNEL_DK_CG 4      /* channel-group DK (L % 4 == 0, H % (2 * waves) == 0) */
 #define PT_KERNEL_FWD_CG 5     /* channel-group matrix-core FWD (L % 4 == 0, H % 8 == 0) */
 #define PT_KERNEL_DX_CG 6      /* channel-group matrix-core DX  (L % 4 == 0, H % 8 == 0) */
+#define PT_KERNEL_FWD_STREAM 7 /* short-tap streaming FWD (K <= 9, L % 4 == 0) */
+#define PT_KERNEL_DX_STREAM 8  /* short-tap streaming DX  (K <= 9, L % 4 == 0) */
+#define PT_KERNEL_FWD_CG16 9   /* 16-channel matrix-core FWD (33 <= L <= 48, L % 4 == 0, H % 16 == 0) */
+#define PT_KERNEL_DX_CG16 10   /* 16-channel matrix-core DX  (33 <= L <= 48, L % 4 == 0, H % 16 == 0) */
 
 /* Version of this ABI (PT_ABI_VERSION). */
 int pt_abi_version(void);

@@ -34,6 +34,10 @@ PT_KERNEL_DK_REDUCE = 3
 PT_KERNEL_DK_CG = 4
 PT_KERNEL_FWD_CG = 5
 PT_KERNEL_DX_CG = 6
+PT_KERNEL_FWD_STREAM = 7
+PT_KERNEL_DX_STREAM = 8
+PT_KERNEL_FWD_CG16 = 9
+PT_KERNEL_DX_CG16 = 10
 
 # Every symbol include/pathtile_hip.h declares, with (restype, argtypes).
 _vp = ctypes.c_void_p

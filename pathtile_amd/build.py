@@ -26,6 +26,7 @@ SOURCES = [
     "inst_fwd_s.hip",
     "inst_dx_v.hip",
     "inst_dx_s.hip",
+    "inst_stream.hip",
     "inst_dk_v.hip",
     "inst_dk_s.hip",
     "inst_dk_mfma.hip",

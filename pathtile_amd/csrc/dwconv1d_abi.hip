@@ -411,9 +411,15 @@ static int rows_waves_per_cu(int L, int K) {
 // the row bucket 16, 32 or 48: rows that fill their bucket partly pay for
 // the matrix work they waste); below that the VALU kernel (bit-exact with the
 // reference's fmaf chain) is as fast or faster.
-// PATHTILE_ROWS_ALGO=valu forces the VALU kernel everywhere; =mfma forces the
-// matrix cores wherever the layout allows them.
-enum RowsAlgo { kRowsValu = 0, kRowsMfma = 1 };
+// Where the VALU serves, the tile kernel (a lane per row through an LDS
+// transpose) runs, or the streaming kernel (float4 lanes, no LDS; rows of
+// L % 4 == 0 floats, at most 9 taps) where the channel period would idle
+// the tile kernel's grid (rows_path); both run the reference's chain bit
+// for bit.
+// PATHTILE_ROWS_ALGO=valu forces the VALU kernels everywhere (=tile: the
+// tile kernel only, =stream: the streaming kernel wherever it can serve);
+// =mfma forces the matrix cores wherever the layout allows them.
+enum RowsAlgo { kRowsValu = 0, kRowsMfma = 1, kRowsTile = 2, kRowsStream = 3 };
 
 // The matrix-core kernel stages whole float4 rows of kRowsCgWaves channels.
 static bool rows_cg_ok(int H, int L, const void* in, const void* out) {
@@ -425,6 +431,8 @@ static bool rows_cg_ok(int H, int L, const void* in, const void* out) {
 static RowsAlgo rows_algo(int L, int K) {
   const char* env = getenv("PATHTILE_ROWS_ALGO");
   if (env && strcmp(env, "valu") == 0) return kRowsValu;
+  if (env && strcmp(env, "tile") == 0) return kRowsTile;
+  if (env && strcmp(env, "stream") == 0) return kRowsStream;
   if (env && strcmp(env, "mfma") == 0) return kRowsMfma;
   const long long lmax = 16LL * (mfma_index(L) + 1);
   // useful / L >= 10.5 (lmax / L)^2, in integers
@@ -491,6 +499,41 @@ static long long gcd_ll(long long a, long long b) {
   return a;
 }
 
+// The streaming kernel serves K <= 9 on whole float4 rows (16-byte aligned
+// tensors), while a channel period H * L fits the 32-bit lane arithmetic.
+static bool stream_ok(int H, int L, int K, const void* in, const void* out) {
+  return K <= kStreamMaxK && L % 4 == 0 && aligned(in, 16) && aligned(out, 16) &&
+         (long long)H * L < (1LL << 31);
+}
+
+// Grid of the streaming kernel: the resident waves, rounded to whole channel
+// periods. Round r moves NW spans of 64 U float4s; when NW * 64 U is a
+// multiple of H L / 4 every lane keeps its column and channel (and taps)
+// from span to span. A period longer than the resident waves takes more
+// workgroups than fit at once; if that is more waves than there are spans,
+// every span gets its own wave instead.
+static int stream_path(bool dx, const float* in, const float* w, float* out,
+                       int B, int H, int L, int K, int wpb, void* stream) {
+  const StreamFn fn = kStreamTable[dx ? 1 : 0][K - 1];
+  const int threads = wpb * kWave;
+  const unsigned long long nf4 = (unsigned long long)B * H * L / 4;
+  const long long span = 64LL * kStreamU;
+  const long long nspans = (long long)((nf4 + span - 1) / span);
+  const long long need = (nspans + wpb - 1) / wpb;  // blocks for one span per wave
+  const long long period = (long long)H * L / 4;
+  const long long q = period / gcd_ll(period, span);  // waves per channel period
+  const long long rq = q / gcd_ll(q, wpb);            // workgroups per period
+  long long nb = (long long)blocks_per_cu((const void*)fn, threads, 0) * num_cus();
+  nb = nb / rq * rq;
+  if (nb < rq) nb = rq;
+  if (nb > need) nb = need;
+  if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
+  uint32_t nblocks = (uint32_t)nb;
+  uint64_t unf4 = nf4, uns = (uint64_t)nspans;
+  void* args[] = {&in, &w, &out, &H, &L, &unf4, &uns};
+  return launch((const void*)fn, nblocks, (uint32_t)threads, 0, stream, args);
+}
+
 static int rows_path(bool dx, const float* in, const float* w, float* out,
                      int B, int H, int L, int K, int wpb, void* stream) {
   int st = check_shape(B, H, L, K);
@@ -500,16 +543,21 @@ static int rows_path(bool dx, const float* in, const float* w, float* out,
   if (!in || !w || !out) return PT_ERR_NULL;
   if (!aligned(in, 4) || !aligned(w, 4) || !aligned(out, 4))
     return PT_ERR_ALIGN;
-  if (rows_algo(L, K) == kRowsMfma && rows_cg_ok(H, L, in, out))
+  const RowsAlgo algo = rows_algo(L, K);
+  if (algo == kRowsMfma && rows_cg_ok(H, L, in, out))
     return rows_cg_path(dx, in, w, out, B, H, L, K, stream);
-  // The VALU kernel: one 64-row LDS tile per wave.
+  // The VALU tile kernel: one 64-row LDS tile per wave. Its limits on the
+  // waves per workgroup hold for the streaming kernel too, so both VALU
+  // kernels accept the same launch configurations.
   const size_t lds_need = (size_t)wpb * rows_lds_per_wave(L);
   if (lds_need > (size_t)max_lds_per_block()) return PT_ERR_CONFIG;
-  const int wpc = rows_waves_per_cu(L, K);
-  const size_t lds = lds_for_blocks_per_cu(lds_need, 0, wpb >= wpc ? 1 : wpc / wpb);
   const bool vec = (L % 4 == 0) && aligned(in, 16) && aligned(out, 16);
   if (wpb * kWave > rows_max_threads(8 * (lbucket_index(L) + 1), vec))
     return PT_ERR_CONFIG;
+  if (algo == kRowsStream && stream_ok(H, L, K, in, out))
+    return stream_path(dx, in, w, out, B, H, L, K, wpb, stream);
+  const int wpc = rows_waves_per_cu(L, K);
+  const size_t lds = lds_for_blocks_per_cu(lds_need, 0, wpb >= wpc ? 1 : wpc / wpb);
   const int li = lbucket_index(L), ki = kbucket_index(K);
   RowsFn fn = dx ? (vec ? kDxTableV : kDxTableS)[li][ki]
                  : (vec ? kFwdTableV : kFwdTableS)[li][ki];
@@ -517,14 +565,24 @@ static int rows_path(bool dx, const float* in, const float* w, float* out,
   const long long ntiles = (R + kWave - 1) / kWave;
   // Persistent grid: one round of resident workgroups, no more than there
   // are tiles. Wave g takes tiles g, g + G, ...; lane i's channel stays
-  // fixed when G is a multiple of P = H / gcd(H, 64), so prefer such G.
+  // fixed when G is a multiple of P = H / gcd(H, 64), i.e. the workgroup
+  // count a multiple of Q = P / gcd(P, wpb). Rounding down to that idles
+  // nb % Q workgroups; a lane whose channel changes reloads its taps every
+  // tile, which measured 16% slower than idling 13% of the waves
+  // (B30000 H37 L32 K8) and 25% faster than idling 49% (B2000 H131 L44 K9).
+  // So: round when that idles at most a quarter of the workgroups; else the
+  // streaming kernel (keeps its taps for any period, 33.6 -> 18.4 us at
+  // B2000 H131 L44 K9) where it can serve, or tiles with tap reloads.
   long long nb = (long long)blocks_per_cu((const void*)fn, wpb * kWave, lds) *
                  num_cus();
   const long long need = (ntiles + wpb - 1) / wpb;
   if (nb > need) nb = need;
   const long long P = (long long)H / gcd_ll(H, kWave);
   const long long Q = P / gcd_ll(P, wpb);  // blocks per channel period
-  if (Q > 1 && nb >= Q) nb = nb / Q * Q;
+  const bool periodic = nb == need || Q <= 1 || (nb >= Q && 4 * (nb % Q) <= nb);
+  if (!periodic && algo != kRowsTile && stream_ok(H, L, K, in, out))
+    return stream_path(dx, in, w, out, B, H, L, K, wpb, stream);
+  if (periodic && nb < need && Q > 1) nb = nb / Q * Q;
   if (nb < 1) nb = 1;
   if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
   uint32_t nblocks = (uint32_t)nb;
@@ -799,6 +857,14 @@ static const void* kernel_for(int kernel_id, int L, int K) {
     case PT_KERNEL_DK_CG: return (const void*)kDkCgTable[mfma_index(L)];
     case PT_KERNEL_FWD_CG: return (const void*)kRowsCgTable[0][mfma_index(L)];
     case PT_KERNEL_DX_CG: return (const void*)kRowsCgTable[1][mfma_index(L)];
+    case PT_KERNEL_FWD_STREAM:
+    case PT_KERNEL_DX_STREAM:
+      if (K > kStreamMaxK || L % 4 != 0) return nullptr;
+      return (const void*)kStreamTable[kernel_id == PT_KERNEL_DX_STREAM ? 1 : 0][K - 1];
+    case PT_KERNEL_FWD_CG16:
+    case PT_KERNEL_DX_CG16:
+      if (mfma_index(L) != 2 || L % 4 != 0) return nullptr;
+      return (const void*)kRowsCg16Table[kernel_id == PT_KERNEL_DX_CG16 ? 1 : 0];
     default: return nullptr;
   }
 }
@@ -973,6 +1039,17 @@ int pt_dynamic_lds_bytes(int kernel_id, int L, int K, int block_config,
       // always kRowsCgWaves waves per workgroup, whatever the caller's config
       if (!pt::valid_wpb(block_config)) return PT_ERR_CONFIG;
       *lds_bytes = (int)pt::rows_cg_lds_bytes(L);
+      return PT_OK;
+    case PT_KERNEL_FWD_CG16:
+    case PT_KERNEL_DX_CG16:
+      // always 16 waves per workgroup, one input stage
+      if (!pt::valid_wpb(block_config)) return PT_ERR_CONFIG;
+      *lds_bytes = (int)pt::rows_cg_lds_bytes(L, 16, 1);
+      return PT_OK;
+    case PT_KERNEL_FWD_STREAM:
+    case PT_KERNEL_DX_STREAM:
+      if (!pt::valid_wpb(block_config)) return PT_ERR_CONFIG;
+      *lds_bytes = 0;
       return PT_OK;
     default:
       return PT_ERR_CONFIG;

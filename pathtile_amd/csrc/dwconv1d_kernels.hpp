@@ -391,7 +391,11 @@ __global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kerne
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t wpb = blockDim.x / kWave;
-  const uint32_t gwave = blockIdx.x * wpb + (uint32_t)wave;
+  // Wave-major numbering: consecutive tiles go to consecutive workgroups
+  // (different CUs), whatever the workgroup size. Block-major numbering put
+  // a workgroup's waves on adjacent tiles and measured 3-8% slower at 4 and
+  // 8 waves per workgroup (B32768 H256 L48 K4: 573 against 555 us at 4).
+  const uint32_t gwave = (uint32_t)wave * gridDim.x + blockIdx.x;
   const uint32_t nwaves = gridDim.x * wpb;
   const uint32_t uL = (uint32_t)L;
   const uint32_t tile_elems = (uint32_t)kWave * uL;
@@ -563,6 +567,143 @@ __global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kerne
       }
     }
     wave_lds_sync();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// FWD / DX for short taps (K <= 9, so p = K/2 <= 4 and K-1-p <= 4) on rows of
+// L % 4 == 0 floats, 16-byte aligned: a streaming kernel with no LDS.
+//
+// The tensor is read as F = B*H*L/4 float4s (a float4 never straddles two
+// rows). A wave owns spans of 64*U consecutive float4s: lane i, register u
+// holds float4 64u + i of the span, so every load and store instruction of
+// the wave moves 1 KiB of contiguous memory, and U of them are in flight
+// per wave. Each output needs at most 4 elements on either side, which lie
+// in the neighbouring float4s: the lane to the left / right in the same
+// register (DPP wave_shr:1 / wave_shl:1), lane 63 of register u-1 / lane 0
+// of register u+1 at the register edges (readlane), and one float4 before
+// and after the span at its edges (one load by lanes 0 and 1).
+//
+// A neighbouring float4 lies wholly inside or wholly outside the lane's row
+// (column c0 of the lane's float4 is a multiple of 4): terms that reach
+// into it are taken iff c0 >= 4 (left) or c0 + 4 < L (right), and skipped
+// otherwise, exactly as the reference skips them; terms inside the lane's
+// own float4 are always taken. Each output thus runs the reference's fmaf
+// chain (start 0.0f, taps j = 0 .. K-1 ascending, the same skipped terms)
+// bit for bit, for any values, non-finite ones included.
+//
+// The grid advances by NW spans per round (NW = waves in the grid); the host
+// makes NW * 64U a multiple of H*L/4 float4s (or gives every span its own
+// wave), so a lane's column and channel are the same in every span it takes:
+// both, and the lane's U sets of K taps, are computed once per wave.
+// ---------------------------------------------------------------------------
+constexpr int kStreamMaxK = 9;
+constexpr int kStreamU = 4;  // float4s per lane per span (spans of 4 KiB)
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_shift(float v, float old) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(
+      __float_as_int(old), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_of(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ float f4c(const float4& v, int c) {
+  return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w;
+}
+
+template <int K, bool DX, int U = kStreamU>
+__global__ __launch_bounds__(1024) void dwconv_stream_kernel(
+    const float* __restrict__ in, const float* __restrict__ w,
+    float* __restrict__ out, int H, int L, uint64_t nf4, uint64_t nspans) {
+  static_assert(K >= 1 && K <= kStreamMaxK, "stream kernel: K <= 9");
+  constexpr int P = K / 2;
+  // Window offsets d (output column - input column) of the chain: FWD
+  // d = j - p, DX d = p - j; the left neighbour supplies d in [-4, -1],
+  // the right one d in [4, 7] relative to the lane's first column.
+  constexpr int NL = DX ? K - 1 - P : P;   // elements needed from the left
+  constexpr int NR = DX ? P : K - 1 - P;   // elements needed from the right
+  constexpr uint32_t kSpanBytes = 64u * U * 16u;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const uint32_t wpb = blockDim.x / kWave;
+  const uint64_t gw = (uint64_t)blockIdx.x * wpb + threadIdx.x / kWave;
+  const uint64_t nw = (uint64_t)gridDim.x * wpb;
+  if (gw >= nspans) return;
+
+  // Column and channel of each of the lane's float4s (the same in every
+  // span of this wave), and that channel's taps.
+  const uint32_t HL = (uint32_t)H * (uint32_t)L;
+  const uint32_t bmod = (uint32_t)((gw * (uint64_t)(64 * U) * 4u) % HL);
+  int col[U];
+  float wt[U][K];
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t r = (bmod + 4u * (uint32_t)(64 * u + lane)) % HL;
+    const uint32_t h = r / (uint32_t)L;
+    col[u] = (int)(r - h * (uint32_t)L);
+#pragma unroll
+    for (int j = 0; j < K; ++j) wt[u][j] = buf_load1(rw, (h * (uint32_t)K + (uint32_t)j) * 4u, 0);
+  }
+
+  for (uint64_t s = gw; s < nspans; s += nw) {
+    const uint64_t f0 = s * (uint64_t)(64 * U);           // first float4 of the span
+    const uint64_t hb = f0 ? f0 - 1 : 0;                  // first float4 the resource covers
+    const uint32_t lead = (uint32_t)(f0 - hb) * 16u;      // bytes before the span (0 or 16)
+    const uint64_t left = (nf4 - hb) * 16u;
+    const uint32_t nrec = left < (uint64_t)(kSpanBytes + 32u) ? (uint32_t)left : kSpanBytes + 32u;
+    const __amdgpu_buffer_rsrc_t rin = make_rsrc_n(in + 4 * hb, nrec);
+    const uint64_t oleft = (nf4 - f0) * 16u;
+    const __amdgpu_buffer_rsrc_t rout =
+        make_rsrc_n(out + 4 * f0, oleft < (uint64_t)kSpanBytes ? (uint32_t)oleft : kSpanBytes);
+
+    float4 x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      x[u] = buf_load4<kCpolNT>(rin, lead + (uint32_t)(64 * u + lane) * 16u, 0);
+    // Lane 0: the float4 before the span (none for the first span); lane 1:
+    // the float4 after it (past the tensor's end it reads 0 and is unused).
+    const uint32_t hoff = lane == 0 ? (f0 ? 0u : kOob) : lane == 1 ? lead + kSpanBytes : kOob;
+    const float4 halo = buf_load4(rin, hoff, 0);
+
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      // win[4 + d] = element d of the row relative to the float4's column 0,
+      // d in [-NL, 3 + NR].
+      float win[12];
+      win[4] = x[u].x;
+      win[5] = x[u].y;
+      win[6] = x[u].z;
+      win[7] = x[u].w;
+#pragma unroll
+      for (int q = 0; q < NL; ++q) {   // left: component 3 - q of float4 - 1
+        const int c = 3 - q;
+        const float edge = u == 0 ? lane_of(f4c(halo, c), 0) : lane_of(f4c(x[u - 1], c), 63);
+        win[c] = dpp_shift<0x138>(f4c(x[u], c), edge);       // wave_shr:1
+      }
+#pragma unroll
+      for (int q = 0; q < NR; ++q) {   // right: component q of float4 + 1
+        const float edge = u == U - 1 ? lane_of(f4c(halo, q), 1) : lane_of(f4c(x[u + 1], q), 0);
+        win[8 + q] = dpp_shift<0x130>(f4c(x[u], q), edge);   // wave_shl:1
+      }
+      const bool lok = col[u] >= 4;
+      const bool rok = col[u] + 4 < L;
+      float acc[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+          const int idx = 4 + c + (DX ? P - j : j - P);
+          const float f = fmaf(win[idx], wt[u][j], a);
+          a = idx < 4 ? (lok ? f : a) : idx >= 8 ? (rok ? f : a) : f;
+        }
+        acc[c] = a;
+      }
+      buf_store4<kCpolNT>(make_float4(acc[0], acc[1], acc[2], acc[3]), rout,
+                          (uint32_t)(64 * u + lane) * 16u);
+    }
   }
 }
 

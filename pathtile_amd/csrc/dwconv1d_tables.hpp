@@ -24,6 +24,10 @@ extern const RowsFn kFwdTableV[kNumLB][kNumKB];
 extern const RowsFn kFwdTableS[kNumLB][kNumKB];
 extern const RowsFn kDxTableV[kNumLB][kNumKB];
 extern const RowsFn kDxTableS[kNumLB][kNumKB];
+// short-tap streaming FWD / DX: [0 = FWD, 1 = DX][K - 1], K = 1 .. 9
+using StreamFn = void (*)(const float*, const float*, float*, int, int, uint64_t,
+                          uint64_t);
+extern const StreamFn kStreamTable[2][9];
 extern const DkFn kDkTableV[kNumLB][kNumKB];
 extern const DkFn kDkTableS[kNumLB][kNumKB];
 // matrix-core DK by row bucket 16, 32, 48

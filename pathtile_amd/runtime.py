@@ -760,22 +760,34 @@ class HipWarpRuntime:
     def resource_report(self, L: int = DEFAULT_L, K: int = DEFAULT_K):
         """Registers, LDS, scratch and estimated occupancy of the kernels that
         serve (L, K) (the reference's resource_report, :814-833). FWD and dX
-        list both kernels: the VALU rows kernel at this runtime's waves per
-        block, and the channel-group matrix-core kernel (8 waves), which
-        serves long FMA chains on 16-byte aligned rows with L % 4 == 0 and
-        H % 8 == 0."""
+        list every kernel that can serve them: the VALU tile kernel and, for
+        K <= 9 on rows of L % 4 == 0, the VALU streaming kernel, both at this
+        runtime's waves per block; the channel-group matrix-core kernel (8
+        waves; long FMA chains on 16-byte aligned rows with L % 4 == 0 and
+        H % 8 == 0) and, for 33 <= L <= 48, its 16-channel variant (16 waves,
+        H % 16 == 0)."""
         import pandas as pd
 
         rows = []
         cg_block = 8 * WAVE_SIZE
-        for name, kid, block, cfg in (
-            ("fwd", _lib.PT_KERNEL_FWD, self.fwd_block, self.waves_per_block),
-            ("fwd_matrix_cores", _lib.PT_KERNEL_FWD_CG, cg_block, self.waves_per_block),
-            ("bwd_input", _lib.PT_KERNEL_DX, self.dx_waves_per_block * WAVE_SIZE,
-             self.dx_waves_per_block),
-            ("bwd_input_matrix_cores", _lib.PT_KERNEL_DX_CG, cg_block, self.dx_waves_per_block),
-            ("bwd_weight", _lib.PT_KERNEL_DK, self.bwdk_block, self.bwdk_block),
-        ):
+        cg16_block = 16 * WAVE_SIZE
+        stream = K <= 9 and L % 4 == 0
+        cg16 = 33 <= L <= 48 and L % 4 == 0
+        fwd_wpb, dx_wpb = self.waves_per_block, self.dx_waves_per_block
+        kernels = [("fwd", _lib.PT_KERNEL_FWD, self.fwd_block, fwd_wpb)]
+        if stream:
+            kernels.append(("fwd_stream", _lib.PT_KERNEL_FWD_STREAM, self.fwd_block, fwd_wpb))
+        kernels.append(("fwd_matrix_cores", _lib.PT_KERNEL_FWD_CG, cg_block, fwd_wpb))
+        if cg16:
+            kernels.append(("fwd_matrix_cores_16", _lib.PT_KERNEL_FWD_CG16, cg16_block, fwd_wpb))
+        kernels.append(("bwd_input", _lib.PT_KERNEL_DX, dx_wpb * WAVE_SIZE, dx_wpb))
+        if stream:
+            kernels.append(("bwd_input_stream", _lib.PT_KERNEL_DX_STREAM, dx_wpb * WAVE_SIZE, dx_wpb))
+        kernels.append(("bwd_input_matrix_cores", _lib.PT_KERNEL_DX_CG, cg_block, dx_wpb))
+        if cg16:
+            kernels.append(("bwd_input_matrix_cores_16", _lib.PT_KERNEL_DX_CG16, cg16_block, dx_wpb))
+        kernels.append(("bwd_weight", _lib.PT_KERNEL_DK, self.bwdk_block, self.bwdk_block))
+        for name, kid, block, cfg in kernels:
             a = self.kernel_attributes(kid, L, K)
             lds = a["static_lds"] + self.dynamic_lds_bytes(kid, L, K, cfg)
             row = {"kernel": name, "L": L, "K": K}

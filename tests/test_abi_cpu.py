@@ -325,6 +325,15 @@ def test_workspace_bytes(lib):
             assert lib.pt_dynamic_lds_bytes(kid, L, 48, 1, ctypes.byref(lds)) == 0
             assert lds.value == 4 * 16 * (8 * L + 4) * 4
         assert lib.pt_dynamic_lds_bytes(kid, 48, 48, 3, ctypes.byref(lds)) == _lib.PT_ERR_CONFIG
+    # 16-channel matrix-core FWD/DX: one input + two output stages
+    for kid in (_lib.PT_KERNEL_FWD_CG16, _lib.PT_KERNEL_DX_CG16):
+        assert lib.pt_dynamic_lds_bytes(kid, 48, 48, 4, ctypes.byref(lds)) == 0
+        assert lds.value == 3 * 16 * (16 * 48 + 4) * 4
+    # short-tap streaming FWD/DX: no LDS
+    for kid in (_lib.PT_KERNEL_FWD_STREAM, _lib.PT_KERNEL_DX_STREAM):
+        assert lib.pt_dynamic_lds_bytes(kid, 48, 4, 16, ctypes.byref(lds)) == 0
+        assert lds.value == 0
+        assert lib.pt_dynamic_lds_bytes(kid, 48, 4, 3, ctypes.byref(lds)) == _lib.PT_ERR_CONFIG
 
 
 def test_library_is_not_linked_to_the_oracle():

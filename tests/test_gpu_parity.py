@@ -99,13 +99,13 @@ def _mfma_serves(H, L, K, algo):
     aligned call: the layout must allow it (L % 4 == 0, H % 8 == 0) and,
     unless forced, the row must need >= 10.5 (LMAX / L)^2 useful FMAs per
     output (LMAX = 16 ceil(L / 16))."""
-    if algo == "valu" or L % 4 or H % 8:
+    if algo in ("valu", "tile", "stream") or L % 4 or H % 8:
         return False
     lmax = 16 * ((L + 15) // 16)
     return algo == "mfma" or 2 * oracle.useful_fma_per_row(L, K) * L >= 21 * lmax * lmax
 
 
-@pytest.mark.parametrize("algo", ["auto", "valu", "mfma"])
+@pytest.mark.parametrize("algo", ["auto", "valu", "tile", "stream", "mfma"])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "B{}H{}L{}K{}".format(*s))
 def test_fwd_dx_bit_exact_and_fp64(rt, shape, algo, monkeypatch):
     """Both FWD/DX kernels; the library reads PATHTILE_ROWS_ALGO on every
@@ -166,7 +166,7 @@ def _same_bits_or_both_nan(a, b):
     return bool(np.all((a == b) | (np.isnan(a) & np.isnan(b))))
 
 
-@pytest.mark.parametrize("algo", ["auto", "valu", "mfma"])
+@pytest.mark.parametrize("algo", ["auto", "valu", "tile", "stream", "mfma"])
 @pytest.mark.parametrize("shape", [
     (64, 16, 48, 48),     # C1: the matrix-core kernel by default
     (40, 8, 44, 48),      # L < row bucket
@@ -224,6 +224,81 @@ def test_nonfinite_values_reach_only_the_reference_window(rt, shape, algo, monke
     ws = w.clone(); ws[hb] = 0.0
     assert oracle.normalized_max_abs(y[fin], oracle.fwd_f64(xs, ws)[fin]) < FWD_TOL
     assert oracle.normalized_max_abs(dx[fin], oracle.dx_f64(dys, ws)[fin]) < FWD_TOL
+
+
+def _sprinkle_nonfinite(t, n, seed):
+    """n non-finite values (Inf, -Inf, NaN in turn) at seeded positions."""
+    rng = np.random.default_rng(seed)
+    flat = t.view(-1)
+    for i, pos in enumerate(rng.integers(0, flat.numel(), size=n)):
+        flat[int(pos)] = (float("inf"), -float("inf"), float("nan"))[i % 3]
+
+
+STREAM_SHAPES = [
+    (3, 1, 4, None),        # L = 4: every neighbour float4 is another row
+    (70, 5, 16, None),      # one partial span
+    (257, 8, 48, None),     # S family
+    (33, 9, 24, None),
+    (100, 131, 44, None),   # H prime: a channel period of 1441 float4s
+    (40, 3, 12, None),      # period of 9 float4s, many per span
+]
+
+
+@pytest.mark.parametrize("K", list(range(1, 10)))
+@pytest.mark.parametrize("shape", STREAM_SHAPES, ids=lambda s: "B{}H{}L{}".format(*s[:3]))
+def test_stream_kernel_is_the_reference_chain_for_any_values(rt, shape, K, monkeypatch):
+    """The short-tap streaming kernel (forced; K <= 9, L % 4 == 0): its
+    neighbour float4s come from other lanes, other registers and the span's
+    halo loads, and the terms that reach past the row are skipped, so every
+    output is the reference's fmaf chain bit for bit, non-finite inputs and
+    taps included (NaN where the chain gives NaN)."""
+    monkeypatch.setenv("PATHTILE_ROWS_ALGO", "stream")
+    B, H, L, _ = shape
+    x, w, dy = _inputs(B, H, L, K, seed=9000 + B + H + L + K)
+    _sprinkle_nonfinite(x, 5, seed=K)
+    _sprinkle_nonfinite(dy, 5, seed=K + 50)
+    w[H // 2, (K - 1) // 2] = float("inf")
+    xd, wd, dyd = _dev(x, w, dy)
+    y = _fwd(rt, xd, wd).cpu().numpy()
+    dx = _dx(rt, dyd, wd).cpu().numpy()
+    assert _same_bits_or_both_nan(y, oracle.fwd_f32_refchain(x, w))
+    assert _same_bits_or_both_nan(dx, oracle.dx_f32_refchain(dy, w))
+
+
+@pytest.mark.parametrize("K", [1, 4, 9])
+@pytest.mark.parametrize("shape", [
+    (2048, 256, 48),   # S family: 6144 spans, a 12-wave channel period, several spans per wave
+    (2000, 131, 44),   # H prime: more workgroups than fit at once
+    (9000, 37, 32),    # period of 296 float4s
+], ids=lambda s: "B{}H{}L{}".format(*s))
+def test_stream_kernel_multi_span_grids(rt, shape, K, monkeypatch):
+    """Grids whose waves take several spans: every lane keeps its column and
+    channel from span to span (the grid advances by whole channel periods),
+    so the outputs are still the reference's chain bit for bit."""
+    monkeypatch.setenv("PATHTILE_ROWS_ALGO", "stream")
+    B, H, L = shape
+    x, w, dy = _inputs(B, H, L, K, seed=9500 + B + H + L + K)
+    xd, wd, dyd = _dev(x, w, dy)
+    assert np.array_equal(_fwd(rt, xd, wd).cpu().numpy(), oracle.fwd_f32_refchain(x, w))
+    assert np.array_equal(_dx(rt, dyd, wd).cpu().numpy(), oracle.dx_f32_refchain(dy, w))
+
+
+@pytest.mark.parametrize("wpb,L", [(1, 48), (2, 48), (4, 48), (8, 48), (16, 32)])
+@pytest.mark.parametrize("algo", ["stream", "valu"])
+def test_stream_kernel_every_waves_per_block(wpb, L, algo, monkeypatch):
+    """Every waves_per_block gives the reference's bits on the streaming
+    kernel (forced) and on the VALU choice at H = 131, whose channel period
+    idles a quarter or more of the tile kernel's grid at some waves per
+    block (there the streaming kernel serves) and less at others."""
+    from pathtile_amd import runtime
+
+    monkeypatch.setenv("PATHTILE_ROWS_ALGO", algo)
+    B, H, K = 1500, 131, 5
+    x, w, dy = _inputs(B, H, L, K, seed=31 + wpb)
+    xd, wd, dyd = _dev(x, w, dy)
+    r = runtime.HipWarpRuntime(waves_per_block=wpb, dx_waves_per_block=wpb)
+    assert np.array_equal(_fwd(r, xd, wd).cpu().numpy(), oracle.fwd_f32_refchain(x, w))
+    assert np.array_equal(_dx(r, dyd, wd).cpu().numpy(), oracle.dx_f32_refchain(dy, w))
 
 
 @pytest.mark.parametrize("algo", ["auto", "valu", "mfma"])
@@ -550,8 +625,14 @@ def test_resource_report_lists_every_kernel(rt):
     one row per kernel that can serve (L, K), with registers, LDS and an
     occupancy estimate; no kernel spills to scratch."""
     df = rt.resource_report(48, 48)
-    assert list(df["kernel"]) == ["fwd", "fwd_matrix_cores", "bwd_input",
-                                  "bwd_input_matrix_cores", "bwd_weight"]
+    assert list(df["kernel"]) == ["fwd", "fwd_matrix_cores", "fwd_matrix_cores_16",
+                                  "bwd_input", "bwd_input_matrix_cores",
+                                  "bwd_input_matrix_cores_16", "bwd_weight"]
     assert (df["scratch_bytes"] == 0).all()
-    for L, K in ((16, 3), (37, 48), (8, 8)):
-        assert len(rt.resource_report(L, K)) == 5
+    df = rt.resource_report(48, 4)
+    assert list(df["kernel"]) == ["fwd", "fwd_stream", "fwd_matrix_cores", "fwd_matrix_cores_16",
+                                  "bwd_input", "bwd_input_stream", "bwd_input_matrix_cores",
+                                  "bwd_input_matrix_cores_16", "bwd_weight"]
+    assert (df["scratch_bytes"] == 0).all()
+    for L, K, n in ((16, 3, 7), (37, 48, 5), (8, 8, 7), (36, 9, 9)):
+        assert len(rt.resource_report(L, K)) == n
