@@ -391,14 +391,18 @@ static long long useful_fma_per_row(int L, int K) {
   return n;
 }
 
-// Resident waves per CU for the FWD/DX kernel, measured on MI355X over every
-// (row bucket, tap bucket) at B16384 H128: two waves per SIMD when the FMA
-// chain is long (at least 0.7 L FMAs per element) so one wave's FMAs hide
-// the other's memory time, or when tiles are small (L <= 16); one wave per
-// SIMD otherwise, which streams HBM best. Waves per workgroup do not change
-// this count, so they barely change the time.
-static int rows_waves_per_cu(int L, int K) {
-  if (L <= 16) return 8;
+// Resident waves per CU for the FWD/DX tile kernel, measured on MI355X over
+// every (row bucket, tap bucket) at B16384 H128: two waves per SIMD when the
+// FMA chain is long (at least 0.7 L FMAs per element) so one wave's FMAs
+// hide the other's memory time, or when tiles are small (L <= 16); one wave
+// per SIMD otherwise, which streams HBM best. Waves per workgroup do not
+// change this count, so they barely change the time. Small calls (at most
+// eight tiles per CU) take two waves per SIMD whatever the chain, so every
+// tile gets a wave in one round: B1000 H96 L37 K8 (1500 tiles) 16.4 against
+// 11.1 us; at 4096 tiles the two counts tie, and from 8192 up one wave per
+// SIMD stays faster (B8192 H128 L48 K4: 66.4 against 70.5 us).
+static int rows_waves_per_cu(int L, int K, long long ntiles) {
+  if (L <= 16 || ntiles <= 8LL * num_cus()) return 8;
   return 10 * useful_fma_per_row(L, K) >= 7LL * L * L ? 8 : 4;
 }
 
@@ -556,13 +560,13 @@ static int rows_path(bool dx, const float* in, const float* w, float* out,
     return PT_ERR_CONFIG;
   if (algo == kRowsStream && stream_ok(H, L, K, in, out))
     return stream_path(dx, in, w, out, B, H, L, K, wpb, stream);
-  const int wpc = rows_waves_per_cu(L, K);
+  const long long R = (long long)B * H;
+  const long long ntiles = (R + kWave - 1) / kWave;
+  const int wpc = rows_waves_per_cu(L, K, ntiles);
   const size_t lds = lds_for_blocks_per_cu(lds_need, 0, wpb >= wpc ? 1 : wpc / wpb);
   const int li = lbucket_index(L), ki = kbucket_index(K);
   RowsFn fn = dx ? (vec ? kDxTableV : kDxTableS)[li][ki]
                  : (vec ? kFwdTableV : kFwdTableS)[li][ki];
-  const long long R = (long long)B * H;
-  const long long ntiles = (R + kWave - 1) / kWave;
   // Persistent grid: one round of resident workgroups, no more than there
   // are tiles. Wave g takes tiles g, g + G, ...; lane i's channel stays
   // fixed when G is a multiple of P = H / gcd(H, 64), i.e. the workgroup
