@@ -23,8 +23,10 @@ CSRC = PKG / "csrc"
 SOURCES = [
     "dwconv1d_abi.hip",
     "inst_fwd_v.hip",
+    "inst_fwd_vp.hip",
     "inst_fwd_s.hip",
     "inst_dx_v.hip",
+    "inst_dx_vp.hip",
     "inst_dx_s.hip",
     "inst_stream.hip",
     "inst_dk_v.hip",

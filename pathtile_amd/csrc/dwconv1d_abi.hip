@@ -425,6 +425,21 @@ static int rows_waves_per_cu(int L, int K, long long ntiles) {
 // =mfma forces the matrix cores wherever the layout allows them.
 enum RowsAlgo { kRowsValu = 0, kRowsMfma = 1, kRowsTile = 2, kRowsStream = 3 };
 
+// Input loads of the FWD / DX kernels: plain (cached) for tensors of at most
+// 256 MiB, non-temporal above. Repeated calls on a tensor that small find
+// part of it still in the 256 MiB MALL; measured on MI355X with
+// back-to-back calls, plain loads were 8-14% faster there (matrix cores:
+// B16384 H128 L32 K32 78.8 against 87.5 us, B8192 H128 L48 K48 61.8
+// against 70.2; tile kernel: B16384 H128 L32 K8 78.1 against 87.4, B8192
+// H128 L48 K4 60.3 against 67.7) and 2-7% slower from 320 MiB up (P 143.3
+// against 136.1 us). Stores stay non-temporal: plain stores on top of plain
+// loads were 1-25% slower at every size measured.
+constexpr double kRowsPlainLoadBytes = 256.0 * 1024 * 1024;
+
+static bool rows_plain_loads(int B, int H, int L) {
+  return 4.0 * (double)B * (double)H * (double)L <= kRowsPlainLoadBytes;
+}
+
 // The matrix-core kernel stages whole float4 rows of kRowsCgWaves channels.
 static bool rows_cg_ok(int H, int L, const void* in, const void* out) {
   return L % 4 == 0 && H % kRowsCgWaves == 0 && aligned(in, 16) &&
@@ -447,7 +462,11 @@ static RowsAlgo rows_algo(int L, int K) {
 // Launch of the channel-group kernel: one workgroup per (channel group,
 // sample range), the ranges interleaved in 16-sample steps. As many ranges as
 // fill the CUs with min(max_per_cu, resident) workgroups each (two 8-channel
-// workgroups measured best where the LDS allows them, L <= 32; one above).
+// workgroups measured best where the LDS allows them, L <= 32; one above),
+// rounded down: a grid a few workgroups past one round runs those few in a
+// second round and nearly doubles the time (B16384 H160 L48 K48, 10
+// channel groups: 26 ranges, 260 workgroups on 256 CUs, 276 us; 25 ranges
+// fit one round).
 // hc: channels (= waves) per workgroup; lds: dynamic LDS per workgroup;
 // max_per_cu: workgroups per CU the range count is sized for (at most what
 // fits).
@@ -460,7 +479,7 @@ static int rows_cg_launch(Fn fn, const T* in, const float* w, T* out, int B,
   if (per_cu > max_per_cu) per_cu = max_per_cu;
   const long long ngroups = (long long)H / hc;
   const long long tsteps = ((long long)B + kRowsCgStep - 1) / kRowsCgStep;
-  long long nr = ((long long)num_cus() * per_cu + ngroups / 2) / ngroups;
+  long long nr = (long long)num_cus() * per_cu / ngroups;
   if (nr > tsteps) nr = tsteps;
   if (nr < 1) nr = 1;
   const long long nb = ngroups * nr;
@@ -486,12 +505,14 @@ static int rows_cg_launch(Fn fn, const T* in, const float* w, T* out, int B,
 // both kernels.
 static int rows_cg_path(bool dx, const float* in, const float* w, float* out,
                         int B, int H, int L, int K, void* stream) {
+  const bool plain = rows_plain_loads(B, H, L);
   if (mfma_index(L) == 2 && H % 16 == 0 &&
       rows_cg_lds_bytes(L, 16, 1) <= (size_t)max_lds_per_block())
-    return rows_cg_launch(kRowsCg16Table[dx ? 1 : 0], in, w, out, B, H, L, K, stream, 16,
-                          rows_cg_lds_bytes(L, 16, 1), 1);
-  return rows_cg_launch(kRowsCgTable[dx ? 1 : 0][mfma_index(L)], in, w, out, B,
-                        H, L, K, stream, kRowsCgWaves, rows_cg_lds_bytes(L), 2);
+    return rows_cg_launch((plain ? kRowsCg16TablePL : kRowsCg16Table)[dx ? 1 : 0], in, w,
+                          out, B, H, L, K, stream, 16, rows_cg_lds_bytes(L, 16, 1), 1);
+  return rows_cg_launch((plain ? kRowsCgTablePL : kRowsCgTable)[dx ? 1 : 0][mfma_index(L)],
+                        in, w, out, B, H, L, K, stream, kRowsCgWaves,
+                        rows_cg_lds_bytes(L), 2);
 }
 
 static long long gcd_ll(long long a, long long b) {
@@ -518,7 +539,8 @@ static bool stream_ok(int H, int L, int K, const void* in, const void* out) {
 // every span gets its own wave instead.
 static int stream_path(bool dx, const float* in, const float* w, float* out,
                        int B, int H, int L, int K, int wpb, void* stream) {
-  const StreamFn fn = kStreamTable[dx ? 1 : 0][K - 1];
+  const StreamFn fn =
+      (rows_plain_loads(B, H, L) ? kStreamTablePL : kStreamTable)[dx ? 1 : 0][K - 1];
   const int threads = wpb * kWave;
   const unsigned long long nf4 = (unsigned long long)B * H * L / 4;
   const long long span = 64LL * kStreamU;
@@ -565,8 +587,9 @@ static int rows_path(bool dx, const float* in, const float* w, float* out,
   const int wpc = rows_waves_per_cu(L, K, ntiles);
   const size_t lds = lds_for_blocks_per_cu(lds_need, 0, wpb >= wpc ? 1 : wpc / wpb);
   const int li = lbucket_index(L), ki = kbucket_index(K);
-  RowsFn fn = dx ? (vec ? kDxTableV : kDxTableS)[li][ki]
-                 : (vec ? kFwdTableV : kFwdTableS)[li][ki];
+  const bool plain = rows_plain_loads(B, H, L);
+  RowsFn fn = dx ? (vec ? (plain ? kDxTableVP : kDxTableV) : kDxTableS)[li][ki]
+                 : (vec ? (plain ? kFwdTableVP : kFwdTableV) : kFwdTableS)[li][ki];
   // Persistent grid: one round of resident workgroups, no more than there
   // are tiles. Wave g takes tiles g, g + G, ...; lane i's channel stays
   // fixed when G is a multiple of P = H / gcd(H, 64), i.e. the workgroup

@@ -612,7 +612,8 @@ __device__ __forceinline__ float f4c(const float4& v, int c) {
   return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w;
 }
 
-template <int K, bool DX, int U = kStreamU>
+// LOAD_CPOL: cache policy of the span loads (stores are non-temporal).
+template <int K, bool DX, int LOAD_CPOL = kCpolNT, int U = kStreamU>
 __global__ __launch_bounds__(1024) void dwconv_stream_kernel(
     const float* __restrict__ in, const float* __restrict__ w,
     float* __restrict__ out, int H, int L, uint64_t nf4, uint64_t nspans) {
@@ -661,7 +662,7 @@ __global__ __launch_bounds__(1024) void dwconv_stream_kernel(
     float4 x[U];
 #pragma unroll
     for (int u = 0; u < U; ++u)
-      x[u] = buf_load4<kCpolNT>(rin, lead + (uint32_t)(64 * u + lane) * 16u, 0);
+      x[u] = buf_load4<LOAD_CPOL>(rin, lead + (uint32_t)(64 * u + lane) * 16u, 0);
     // Lane 0: the float4 before the span (none for the first span); lane 1:
     // the float4 after it (past the tensor's end it reads 0 and is unused).
     const uint32_t hoff = lane == 0 ? (f0 ? 0u : kOob) : lane == 1 ? lead + kSpanBytes : kOob;
@@ -1061,7 +1062,10 @@ __host__ __device__ constexpr size_t rows_cg_lds_bytes(int L, int hc = kRowsCgWa
 // terms of which some are infinite or NaN has the same non-finite value in
 // any order (sums that overflow FP32 aside). A wave whose lanes all see
 // finite first outputs skips the chain.
-template <int LMAX, bool DX, int kDepth, int HC = kRowsCgWaves, int NIN = 2>
+//
+// LOAD_CPOL: cache policy of the input loads (stores are non-temporal).
+template <int LMAX, bool DX, int kDepth, int HC = kRowsCgWaves, int NIN = 2,
+          int LOAD_CPOL = kCpolNT>
 __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
     const float* __restrict__ in, const float* __restrict__ w,
     float* __restrict__ out, int B, int H, int L, int K, int nranges,
@@ -1109,7 +1113,7 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
     const int klim = min(kRowsCgStep, B - bs);
 #pragma unroll
     for (int i = 0; i < kNpt; ++i)
-      st[i] = buf_load_chunk<kCpolNT>(rs, ek[i] < klim ? eoff[i] : kOob);
+      st[i] = buf_load_chunk<LOAD_CPOL>(rs, ek[i] < klim ? eoff[i] : kOob);
   };
   auto store_stage = [&](int buf, const u32x4 (&st)[kNpt]) {
 #pragma unroll

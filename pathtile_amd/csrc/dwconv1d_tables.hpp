@@ -24,10 +24,14 @@ extern const RowsFn kFwdTableV[kNumLB][kNumKB];
 extern const RowsFn kFwdTableS[kNumLB][kNumKB];
 extern const RowsFn kDxTableV[kNumLB][kNumKB];
 extern const RowsFn kDxTableS[kNumLB][kNumKB];
+// the V tables with plain (not non-temporal) input loads
+extern const RowsFn kFwdTableVP[kNumLB][kNumKB];
+extern const RowsFn kDxTableVP[kNumLB][kNumKB];
 // short-tap streaming FWD / DX: [0 = FWD, 1 = DX][K - 1], K = 1 .. 9
 using StreamFn = void (*)(const float*, const float*, float*, int, int, uint64_t,
                           uint64_t);
 extern const StreamFn kStreamTable[2][9];
+extern const StreamFn kStreamTablePL[2][9];  // plain input loads
 extern const DkFn kDkTableV[kNumLB][kNumKB];
 extern const DkFn kDkTableS[kNumLB][kNumKB];
 // matrix-core DK by row bucket 16, 32, 48
@@ -44,6 +48,9 @@ using RowsCgFn = void (*)(const float*, const float*, float*, int, int, int,
 extern const RowsCgFn kRowsCgTable[2][3];
 // 16-channel workgroups with one input stage, row bucket 48: [0 = FWD, 1 = DX]
 extern const RowsCgFn kRowsCg16Table[2];
+// the same with plain (not non-temporal) input loads
+extern const RowsCgFn kRowsCgTablePL[2][3];
+extern const RowsCgFn kRowsCg16TablePL[2];
 // BF16 I/O (uint16_t bit patterns; FP32 taps, FP32 accumulation)
 using RowsCgBf16Fn = void (*)(const uint16_t*, const float*, uint16_t*, int,
                               int, int, int, int, uint32_t);
