@@ -249,8 +249,11 @@ static long long bm_ranges(int B, int H, int L) {
   return nr < 1 ? 1 : nr;
 }
 
+// device_cap: size the channel-group DK's ranges for the current device (a
+// launch); without it the geometry depends on the shape alone and its
+// range count bounds every launch's (the deterministic workspace size).
 static DkGeom dk_geometry(int B, int H, int L, int K, int threads, bool vec16,
-                          int esize = 4) {
+                          int esize = 4, bool device_cap = false) {
   DkGeom g;
   g.algo = dk_algo(L, K);
   g.wpb = threads / kWave;
@@ -260,7 +263,22 @@ static DkGeom dk_geometry(int B, int H, int L, int K, int threads, bool vec16,
   g.nt = g.cg && cg_large(B, H, L);
   if (g.cg) {
     const long long ngroups = (long long)H / (dk_cpw(L) * wpb);
-    const long long nr = cg_ranges(B, H, L);
+    long long nr = cg_ranges(B, H, L);
+    // The stride rule was measured where its workgroups fill the resident
+    // slots exactly (H a power of two). Where they overflow them, the few
+    // left over run in a second round: B16384 H96 L48 K48 takes 128.8 us at
+    // the rule's 48 ranges (2304 workgroups, 2048 slots) and 94.6 us at 42
+    // (2016); B32768 H96 L48 K4 249 against 186 us. Cap at one round.
+    if (device_cap) {
+      const int mi = mfma_index(L);
+      const DkCgFn fn = (g.nt ? kDkCgTableNT : kDkCgTable)[mi];
+      const long long resident =
+          (long long)blocks_per_cu((const void*)fn, threads,
+                                   cg_lds_bytes(16 * (mi + 1), (int)wpb, L, dk_cpw(L))) *
+          num_cus();
+      if (ngroups * nr > resident) nr = resident / ngroups;
+      if (nr < 1) nr = 1;
+    }
     g.rows_per_wave = 0;
     g.nbt = (int)nr;
     g.nblocks = ngroups * nr;
@@ -693,16 +711,30 @@ static int bf16_dk_check(int B, int H, int L, int K, int threads) {
 }
 
 // Geometry of the BF16 DK (one kernel: the shape checks of bf16_dk_check
-// admit exactly the layouts it serves).
-static DkGeom bm_geometry(int B, int H, int L, int threads) {
+// admit exactly the layouts it serves). device_cap: a launch, whose ranges
+// are capped at one round of resident workgroups as in dk_geometry; the
+// uncapped count bounds them (the deterministic workspace size).
+static DkGeom bm_geometry(int B, int H, int L, int threads, bool device_cap = false) {
   DkGeom g;
   g.algo = kDkMfma;
   g.cg = true;
   g.nt = bm_nt(B, H, L);
   g.wpb = threads / kWave;
   g.rows_per_wave = 0;
-  g.nbt = (int)bm_ranges(B, H, L);
-  g.nblocks = (long long)H / (kCgChannelsPerWave * g.wpb) * g.nbt;
+  const long long ngroups = (long long)H / (kCgChannelsPerWave * g.wpb);
+  long long nr = bm_ranges(B, H, L);
+  if (device_cap) {
+    const int mi = mfma_index(L);
+    const DkBf16Fn fn = (g.nt ? kDkBf16mmaTableNT : kDkBf16mmaTable)[mi];
+    const long long resident =
+        (long long)blocks_per_cu((const void*)fn, threads,
+                                 dk_bf16mma_lds_bytes(16 * (mi + 1), g.wpb)) *
+        num_cus();
+    if (ngroups * nr > resident) nr = resident / ngroups;
+    if (nr < 1) nr = 1;
+  }
+  g.nbt = (int)nr;
+  g.nblocks = ngroups * nr;
   return g;
 }
 
@@ -721,7 +753,8 @@ static int bf16_dk_launch(bool det, const void* gy, const void* x, float* dst,
 
 // Channels-last DK: 32-channel workgroups of 16 waves, one resident pass of
 // them over the GPU (the sample ranges are the resident workgroups per
-// channel group), at most one range per 4-sample step.
+// channel group, rounded down so no workgroup waits for a second round),
+// at most one range per 4-sample step.
 static int dk_cl_launch(const float* x, const float* dy, float* dw, int B,
                         int H, int L, int K, void* stream) {
   const DkClFn fn = kDkClTable[mfma_index(L)];
@@ -731,7 +764,7 @@ static int dk_cl_launch(const float* x, const float* dy, float* dw, int B,
   const long long ngroups = (long long)H / kClChannels;
   const long long tsteps = ((long long)B + kCgStep - 1) / kCgStep;
   const long long slots = (long long)num_cus() * blocks_per_cu((const void*)fn, threads, lds);
-  long long nr = (slots + ngroups - 1) / ngroups;
+  long long nr = slots / ngroups;
   if (nr > tsteps) nr = tsteps;
   if (nr < 1) nr = 1;
   const long long nb = ngroups * nr;
@@ -946,8 +979,9 @@ int pt_dwconv1d_dk_atomic_f32(const float* dy, const float* x, float* dk,
   if (B == 0) return PT_OK;
   if (!dy || !x) return PT_ERR_NULL;
   if (!pt::aligned(dy, 4) || !pt::aligned(x, 4)) return PT_ERR_ALIGN;
-  const pt::DkGeom g = pt::dk_geometry(
-      B, H, L, K, threads_per_block, pt::aligned(dy, 16) && pt::aligned(x, 16));
+  const pt::DkGeom g =
+      pt::dk_geometry(B, H, L, K, threads_per_block,
+                      pt::aligned(dy, 16) && pt::aligned(x, 16), 4, true);
   if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
   return pt::dk_path(false, dy, x, dk, B, H, L, K, threads_per_block, g,
                      stream);
@@ -985,8 +1019,9 @@ int pt_dwconv1d_dk_det_f32(const float* dy, const float* x, float* dk,
   if (B == 0) return pt::zero_fill(dk, H * K, stream);
   if (!dy || !x) return PT_ERR_NULL;
   if (!pt::aligned(dy, 4) || !pt::aligned(x, 4)) return PT_ERR_ALIGN;
-  const pt::DkGeom g = pt::dk_geometry(
-      B, H, L, K, threads_per_block, pt::aligned(dy, 16) && pt::aligned(x, 16));
+  const pt::DkGeom g =
+      pt::dk_geometry(B, H, L, K, threads_per_block,
+                      pt::aligned(dy, 16) && pt::aligned(x, 16), 4, true);
   if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
   const size_t need = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
   if (!workspace || workspace_bytes < need) return PT_ERR_WORKSPACE;
@@ -1007,8 +1042,9 @@ int pt_dwconv1d_dk_det_f32_noalloc(const float* dy, const float* x, float* dk,
   if (B == 0) return pt::zero_fill(dk, H * K, stream);
   if (!dy || !x) return PT_ERR_NULL;
   if (!pt::aligned(dy, 4) || !pt::aligned(x, 4)) return PT_ERR_ALIGN;
-  const pt::DkGeom g = pt::dk_geometry(
-      B, H, L, K, threads_per_block, pt::aligned(dy, 16) && pt::aligned(x, 16));
+  const pt::DkGeom g =
+      pt::dk_geometry(B, H, L, K, threads_per_block,
+                      pt::aligned(dy, 16) && pt::aligned(x, 16), 4, true);
   if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
   const size_t need = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
   if (need > (size_t)PT_DK_SCRATCH_BYTES) return PT_ERR_SCRATCH;
@@ -1108,7 +1144,7 @@ int pt_dwconv1d_dk_atomic_bf16(const void* dy, const void* x, float* dk, int B,
   if (B == 0) return PT_OK;
   if (!dy || !x) return PT_ERR_NULL;
   if (!pt::aligned(dy, 16) || !pt::aligned(x, 16)) return PT_ERR_ALIGN;
-  const pt::DkGeom g = pt::bm_geometry(B, H, L, threads_per_block);
+  const pt::DkGeom g = pt::bm_geometry(B, H, L, threads_per_block, true);
   if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
   return pt::bf16_dk_launch(false, dy, x, dk, B, H, L, K, threads_per_block, g,
                             stream);
@@ -1141,7 +1177,7 @@ int pt_dwconv1d_dk_det_bf16(const void* dy, const void* x, float* dk,
   if (B == 0) return pt::zero_fill(dk, H * K, stream);
   if (!dy || !x) return PT_ERR_NULL;
   if (!pt::aligned(dy, 16) || !pt::aligned(x, 16)) return PT_ERR_ALIGN;
-  const pt::DkGeom g = pt::bm_geometry(B, H, L, threads_per_block);
+  const pt::DkGeom g = pt::bm_geometry(B, H, L, threads_per_block, true);
   if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
   const size_t need = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
   if (!workspace || workspace_bytes < need) return PT_ERR_WORKSPACE;

@@ -374,9 +374,9 @@ def test_xcd_remap_is_a_bijection():
 def test_noalloc_dk_validation_and_scratch_limit_before_launch(lib):
     """pt_dwconv1d_dk_det_f32_noalloc checks shape, config, NULL, alignment
     and then its static scratch (PT_DK_SCRATCH_BYTES of partials) before any
-    HIP call: a shape whose partials exceed it is refused with
-    PT_ERR_SCRATCH, for 16-byte aligned (channel-group) and 4-byte aligned
-    (per-channel) inputs alike."""
+    launch: a shape whose partials exceed it even at one sample range
+    (H * K * 4 bytes > 8 MiB) is refused with PT_ERR_SCRATCH, for 16-byte
+    aligned (channel-group) and 4-byte aligned (per-channel) inputs alike."""
     from pathtile_amd import _lib
 
     buf = (ctypes.c_ubyte * 4096)()
@@ -391,7 +391,7 @@ def test_noalloc_dk_validation_and_scratch_limit_before_launch(lib):
     assert fn(pa, pb, None, 1, 1, 8, 3, 128, S) == _lib.PT_ERR_NULL
     assert fn(None, pb, pc, 1, 1, 8, 3, 128, S) == _lib.PT_ERR_NULL
     assert fn(ctypes.c_void_p(al + 2), pb, pc, 1, 1, 8, 3, 128, S) == _lib.PT_ERR_ALIGN
-    B, H, L, K = 4096, 8192, 48, 48  # 8192 * 48 taps * 4 bytes * >= 8 ranges > 8 MiB
+    B, H, L, K = 64, 65536, 48, 48  # 65536 * 48 taps * 4 bytes = 12 MiB per range
     need = ctypes.c_size_t(0)
     assert lib.pt_dwconv1d_dk_det_workspace_bytes(B, H, L, K, 128, ctypes.byref(need)) == 0
     assert need.value > _lib.PT_DK_SCRATCH_BYTES
