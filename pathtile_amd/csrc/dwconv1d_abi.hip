@@ -846,11 +846,12 @@ static int rows_long_path(bool dx, const float* in, const float* w, float* out,
 // steps); the range count aims at kLongDkTarget workgroups (two per CU of
 // MI355X), at most one per 32 samples (the split kernel's step; the FP32
 // kernel's 16-sample steps then number at least two per range), and depends
-// on the shape only, so the workspace size does too.
+// on the shape only, so the workspace size does too. It is rounded down: a
+// few workgroups past the target run in another round of their own.
 constexpr long long kLongDkTarget = 512;
 
 static long long long_dk_ranges(int B, int H) {
-  long long nr = (kLongDkTarget + H - 1) / (H > 0 ? H : 1);
+  long long nr = kLongDkTarget / (H > 0 ? H : 1);
   const long long tsteps = ((long long)B + 31) / 32;
   if (nr > tsteps) nr = tsteps;
   return nr < 1 ? 1 : nr;
