@@ -215,8 +215,8 @@ def time_paths(fns: dict, stream, trials: int, warmup: int, runs: int) -> dict:
 
 def rows_kernel_name(H: int, L: int, K: int, dx: bool) -> str:
     """The FWD/DX kernel the library picks for 16-byte aligned rows: the
-    channel-group matrix-core kernel where the layout allows it (L % 4 == 0,
-    H % 8 == 0) and a row needs >= 10.5 (LMAX / L)^2 useful FMAs per output
+    channel-group matrix-core kernel where the layout allows it (H % 8 == 0)
+    and a row needs >= 10.5 (LMAX / L)^2 useful FMAs per output
     (LMAX = 16 ceil(L / 16)), else the VALU rows kernel (or either on
     request through PATHTILE_ROWS_ALGO)."""
     tag = "DX" if dx else "FWD"
@@ -225,7 +225,7 @@ def rows_kernel_name(H: int, L: int, K: int, dx: bool) -> str:
     useful = sum(max(0, min(L, L - (j - p)) - max(0, p - j)) for j in range(K))
     lmax = 16 * ((L + 15) // 16)
     mfma = algo == "mfma" or (algo != "valu" and 2 * useful * L >= 21 * lmax * lmax)
-    if mfma and L % 4 == 0 and H % 8 == 0:
+    if mfma and H % 8 == 0:
         return f"dwconv_rows_cg_kernel<{tag}>"
     return f"dwconv_rows_kernel<{tag}>"
 

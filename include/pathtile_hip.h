@@ -55,12 +55,12 @@ extern "C" {
 #define PT_KERNEL_DK 2
 #define PT_KERNEL_DK_REDUCE 3
 #define PT_KERNEL_DK_CG 4      /* channel-group DK (L % 4 == 0, H % (2 * waves) == 0) */
-#define PT_KERNEL_FWD_CG 5     /* channel-group matrix-core FWD (L % 4 == 0, H % 8 == 0) */
-#define PT_KERNEL_DX_CG 6      /* channel-group matrix-core DX  (L % 4 == 0, H % 8 == 0) */
+#define PT_KERNEL_FWD_CG 5     /* channel-group matrix-core FWD (H % 8 == 0) */
+#define PT_KERNEL_DX_CG 6      /* channel-group matrix-core DX  (H % 8 == 0) */
 #define PT_KERNEL_FWD_STREAM 7 /* short-tap streaming FWD (K <= 9, L % 4 == 0) */
 #define PT_KERNEL_DX_STREAM 8  /* short-tap streaming DX  (K <= 9, L % 4 == 0) */
-#define PT_KERNEL_FWD_CG16 9   /* 16-channel matrix-core FWD (33 <= L <= 48, L % 4 == 0, H % 16 == 0) */
-#define PT_KERNEL_DX_CG16 10   /* 16-channel matrix-core DX  (33 <= L <= 48, L % 4 == 0, H % 16 == 0) */
+#define PT_KERNEL_FWD_CG16 9   /* 16-channel matrix-core FWD (33 <= L <= 48, H % 16 == 0) */
+#define PT_KERNEL_DX_CG16 10   /* 16-channel matrix-core DX  (33 <= L <= 48, H % 16 == 0) */
 
 /* Version of this ABI (PT_ABI_VERSION). */
 int pt_abi_version(void);
@@ -80,17 +80,20 @@ const char* pt_status_string(int status);
  * workgroup holds a 64-row LDS tile per wave, so 16 waves fit only rows up
  * to 32 (PT_ERR_CONFIG for longer rows on this kernel). Where a row needs at
  * least 10.5 (LMAX / L)^2 useful FMAs per output on average (LMAX =
- * 16 ceil(L / 16)) and the layout allows it (L % 4 == 0, H % 8 == 0, x and
- * y 16-byte aligned), the channel-group matrix-core kernel runs instead:
+ * 16 ceil(L / 16)) and the layout allows it (H % 8 == 0, x and y 16-byte
+ * aligned; any L), the channel-group matrix-core kernel runs instead:
  * 8 waves (channels) per workgroup, or 16 for rows of 33-48 columns when
- * H % 16 == 0, whatever waves_per_block says, so every value is accepted
- * there and gives the same bits; it sums in the
+ * H % 16 == 0 and the call is large (tensors above 256 MiB or at least 24
+ * 16-sample steps per CU), whatever waves_per_block says, so every value is
+ * accepted there and gives the same bits; it sums in the
  * matrix cores' order (within FP32 rounding of the reference: about 3e-7
  * max-abs-scaled against FP64). On both kernels an Inf or NaN input or tap
  * reaches exactly the outputs whose reference window holds it (those
  * outputs follow the reference's chain). The environment variable
  * PATHTILE_ROWS_ALGO=valu selects the VALU kernel everywhere, =mfma the
- * matrix-core kernel wherever the layout allows; it is read on every call.
+ * matrix-core kernel wherever the layout allows; PATHTILE_ROWS_CHANNELS=8
+ * or =16 forces the matrix-core kernel's channels per workgroup where the
+ * layout allows; both are read on every call.
  */
 int pt_dwconv1d_fwd_f32(const float* x, const float* w, float* y, int B, int H,
                         int L, int K, int waves_per_block, void* stream);

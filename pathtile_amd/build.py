@@ -33,6 +33,7 @@ SOURCES = [
     "inst_dk_s.hip",
     "inst_dk_mfma.hip",
     "inst_rows_mfma.hip",
+    "inst_rows_mfma_u.hip",
     "inst_bf16.hip",
     "inst_dk_cl.hip",
     "inst_long.hip",

@@ -458,10 +458,12 @@ static bool rows_plain_loads(int B, int H, int L) {
   return 4.0 * (double)B * (double)H * (double)L <= kRowsPlainLoadBytes;
 }
 
-// The matrix-core kernel stages whole float4 rows of kRowsCgWaves channels.
+// The matrix-core kernel stages the contiguous segments of kRowsCgWaves (or
+// 16) channels in 16-byte chunks: with H % 8 == 0 a segment (HC L floats)
+// and a sample (H L floats) are whole chunks at any L, so 16-byte aligned
+// tensors are all it needs (rows of L % 4 != 0 take its A4 = false form).
 static bool rows_cg_ok(int H, int L, const void* in, const void* out) {
-  return L % 4 == 0 && H % kRowsCgWaves == 0 && aligned(in, 16) &&
-         aligned(out, 16) &&
+  return H % kRowsCgWaves == 0 && aligned(in, 16) && aligned(out, 16) &&
          rows_cg_lds_bytes(L) <= (size_t)max_lds_per_block();
 }
 
@@ -509,28 +511,53 @@ static int rows_cg_launch(Fn fn, const T* in, const float* w, T* out, int B,
 }
 
 // Channels (waves) per workgroup, whatever the caller's waves per block:
-//  * rows of 33-48 columns with H % 16 == 0: 16, one per CU, with one input
-//    and two output stages in LDS (148 KB at L = 48). Each step then moves
-//    16 segments of 3 KB instead of 1.5 KB; a copy kernel with the same
-//    access pattern ran in 129.8 us at P against 136.4 us for 1.5 KB
-//    segments, and the kernel itself 3-6% faster on every such shape tried
-//    (P: 133.7 against 142.4 us FWD);
+//  * rows of 33-48 columns with H % 16 == 0, on tensors above 256 MiB or
+//    with at least 24 steps per CU: 16, one per CU, with one input and two
+//    output stages in LDS (148 KB at L = 48). Each step then moves 16
+//    segments of 3 KB instead of 1.5 KB; a copy kernel with the same access
+//    pattern ran in 129.8 us at P against 136.4 us for 1.5 KB segments, and
+//    the kernel itself 3-6% faster there (P: 133.7 against 142.4 us FWD;
+//    B16384 H96 L37 K48 92.2 against 95.9 us);
 //  * otherwise 8, two per CU where the LDS allows (two input and two output
 //    stages). Measured on MI355X at 1, 2, 4 and 8 channels, 8 was fastest
-//    (at P: 227, 171, 156, 140 us).
+//    (at P: 227, 171, 156, 140 us). On tensors of at most 256 MiB (plain
+//    loads) with fewer steps per CU the 16-channel grid gives the CUs
+//    uneven step counts and fewer steps to overlap, and 8 channels measured
+//    as fast or 2-20% faster (B16384 H64 L40 K40 55.8 against 58.7 us,
+//    B4096 H128 L48 K48 33.4 against 35.8, B1000 H96 L37 K48 11.1 against
+//    13.2; B4096 H256 L48 K48, 16 steps per CU, 63.4 against 62.3).
 // The VALU kernel that serves the other shapes wants 1 to 4 waves per
 // workgroup (at S: 553-568 us against 606 at 8), so one knob cannot serve
 // both kernels.
+// PATHTILE_ROWS_CHANNELS=8 or =16 forces the channel count where the layout
+// allows it (16: rows of 33-48 columns, H % 16 == 0); the library reads the
+// variable on every call.
+static int rows_cg_channels_env() {
+  const char* env = getenv("PATHTILE_ROWS_CHANNELS");
+  if (env && strcmp(env, "8") == 0) return 8;
+  if (env && strcmp(env, "16") == 0) return 16;
+  return 0;
+}
+
 static int rows_cg_path(bool dx, const float* in, const float* w, float* out,
                         int B, int H, int L, int K, void* stream) {
   const bool plain = rows_plain_loads(B, H, L);
-  if (mfma_index(L) == 2 && H % 16 == 0 &&
-      rows_cg_lds_bytes(L, 16, 1) <= (size_t)max_lds_per_block())
-    return rows_cg_launch((plain ? kRowsCg16TablePL : kRowsCg16Table)[dx ? 1 : 0], in, w,
-                          out, B, H, L, K, stream, 16, rows_cg_lds_bytes(L, 16, 1), 1);
-  return rows_cg_launch((plain ? kRowsCgTablePL : kRowsCgTable)[dx ? 1 : 0][mfma_index(L)],
-                        in, w, out, B, H, L, K, stream, kRowsCgWaves,
-                        rows_cg_lds_bytes(L), 2);
+  const bool a4 = L % 4 == 0;
+  const long long tsteps = ((long long)B + kRowsCgStep - 1) / kRowsCgStep;
+  const int forced = rows_cg_channels_env();
+  const bool want16 = forced ? forced == 16
+                             : !plain || tsteps * (H / 16) >= 24LL * num_cus();
+  if (mfma_index(L) == 2 && H % 16 == 0 && want16 &&
+      rows_cg_lds_bytes(L, 16, 1) <= (size_t)max_lds_per_block()) {
+    const RowsCgFn* t16 = a4 ? (plain ? kRowsCg16TablePL : kRowsCg16Table)
+                             : (plain ? kRowsCg16TableUPL : kRowsCg16TableU);
+    return rows_cg_launch(t16[dx ? 1 : 0], in, w, out, B, H, L, K, stream, 16,
+                          rows_cg_lds_bytes(L, 16, 1), 1);
+  }
+  const RowsCgFn(*t8)[3] = a4 ? (plain ? kRowsCgTablePL : kRowsCgTable)
+                              : (plain ? kRowsCgTableUPL : kRowsCgTableU);
+  return rows_cg_launch(t8[dx ? 1 : 0][mfma_index(L)], in, w, out, B, H, L, K,
+                        stream, kRowsCgWaves, rows_cg_lds_bytes(L), 2);
 }
 
 static long long gcd_ll(long long a, long long b) {
@@ -916,16 +943,19 @@ static const void* kernel_for(int kernel_id, int L, int K) {
                                       : (const void*)kDkTableV[li][ki];
     case PT_KERNEL_DK_REDUCE: return (const void*)&dk_reduce_kernel;
     case PT_KERNEL_DK_CG: return (const void*)kDkCgTable[mfma_index(L)];
-    case PT_KERNEL_FWD_CG: return (const void*)kRowsCgTable[0][mfma_index(L)];
-    case PT_KERNEL_DX_CG: return (const void*)kRowsCgTable[1][mfma_index(L)];
+    case PT_KERNEL_FWD_CG:
+    case PT_KERNEL_DX_CG:
+      return (const void*)(L % 4 == 0 ? kRowsCgTable : kRowsCgTableU)
+          [kernel_id == PT_KERNEL_DX_CG ? 1 : 0][mfma_index(L)];
     case PT_KERNEL_FWD_STREAM:
     case PT_KERNEL_DX_STREAM:
       if (K > kStreamMaxK || L % 4 != 0) return nullptr;
       return (const void*)kStreamTable[kernel_id == PT_KERNEL_DX_STREAM ? 1 : 0][K - 1];
     case PT_KERNEL_FWD_CG16:
     case PT_KERNEL_DX_CG16:
-      if (mfma_index(L) != 2 || L % 4 != 0) return nullptr;
-      return (const void*)kRowsCg16Table[kernel_id == PT_KERNEL_DX_CG16 ? 1 : 0];
+      if (mfma_index(L) != 2) return nullptr;
+      return (const void*)(L % 4 == 0 ? kRowsCg16Table : kRowsCg16TableU)
+          [kernel_id == PT_KERNEL_DX_CG16 ? 1 : 0];
     default: return nullptr;
   }
 }

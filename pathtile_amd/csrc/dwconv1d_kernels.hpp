@@ -1064,8 +1064,15 @@ __host__ __device__ constexpr size_t rows_cg_lds_bytes(int L, int hc = kRowsCgWa
 // finite first outputs skips the chain.
 //
 // LOAD_CPOL: cache policy of the input loads (stores are non-temporal).
+//
+// A4: rows are whole float4s (L % 4 == 0). Without it (any L; H % 8 == 0
+// and 16-byte aligned tensors, so a segment of HC rows is still a whole
+// number of 16-byte chunks and every sample's segments start 16-byte
+// aligned), a channel's row starts at an arbitrary float in the stage: the
+// lane reads its A operands and writes its outputs one float at a time, and
+// an output chunk that straddles L is written element by element.
 template <int LMAX, bool DX, int kDepth, int HC = kRowsCgWaves, int NIN = 2,
-          int LOAD_CPOL = kCpolNT>
+          int LOAD_CPOL = kCpolNT, bool A4 = true>
 __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
     const float* __restrict__ in, const float* __restrict__ w,
     float* __restrict__ out, int B, int H, int L, int K, int nranges,
@@ -1156,17 +1163,27 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
     const float* src = row + NU * kk;
     float* orow = outl + (s & 1) * sz + jj * sk + cb;
     float a[NU];
+    if constexpr (A4) {
 #pragma unroll
-    for (int q = 0; q < NU / 4; ++q) {
-      const float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
-      a[4 * q + 0] = v.x;
-      a[4 * q + 1] = v.y;
-      a[4 * q + 2] = v.z;
-      a[4 * q + 3] = v.w;
-    }
-    if (L != LMAX) {  // columns >= L belong to the next channel: zero them
+      for (int q = 0; q < NU / 4; ++q) {
+        const float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
+        a[4 * q + 0] = v.x;
+        a[4 * q + 1] = v.y;
+        a[4 * q + 2] = v.z;
+        a[4 * q + 3] = v.w;
+      }
+      if (L != LMAX) {  // columns >= L belong to the next channel: zero them
 #pragma unroll
-      for (int u = 0; u < NU; ++u) a[u] = u + NU * kk < L ? a[u] : 0.0f;
+        for (int u = 0; u < NU; ++u) a[u] = u + NU * kk < L ? a[u] : 0.0f;
+      }
+    } else {
+      // Columns >= L read the row's first element and are zeroed.
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const bool in = u + NU * kk < L;
+        const float v = row[in ? u + NU * kk : 0];
+        a[u] = in ? v : 0.0f;
+      }
     }
     // The MFMA computes the transposed tile (taps as A, rows as B; each lane
     // supplies the same values either way), so lane (jj, kk) holds output
@@ -1179,8 +1196,14 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
       for (int u = 0; u < NU; ++u)
         d = __builtin_amdgcn_mfma_f32_16x16x4f32(bt[u][tt], a[u], d, 0, 0, 0);
       if (tt == 0) bad = !__builtin_isfinite(d[0]);
-      const int t = 16 * tt + rq;  // L % 4 == 0: all four columns or none
-      if (t < L) *reinterpret_cast<f32x4*>(orow + t) = d;
+      const int t = 16 * tt + rq;
+      if constexpr (A4) {  // L % 4 == 0: all four columns or none
+        if (t < L) *reinterpret_cast<f32x4*>(orow + t) = d;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (t + e < L) orow[t + e] = d[e];
+      }
     }
     if (__builtin_amdgcn_ballot_w64(bad)) {
       if (bad) {

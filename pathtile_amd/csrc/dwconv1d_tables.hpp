@@ -51,6 +51,11 @@ extern const RowsCgFn kRowsCg16Table[2];
 // the same with plain (not non-temporal) input loads
 extern const RowsCgFn kRowsCgTablePL[2][3];
 extern const RowsCgFn kRowsCg16TablePL[2];
+// the four tables above for rows that are not whole float4s (L % 4 != 0)
+extern const RowsCgFn kRowsCgTableU[2][3];
+extern const RowsCgFn kRowsCg16TableU[2];
+extern const RowsCgFn kRowsCgTableUPL[2][3];
+extern const RowsCgFn kRowsCg16TableUPL[2];
 // BF16 I/O (uint16_t bit patterns; FP32 taps, FP32 accumulation)
 using RowsCgBf16Fn = void (*)(const uint16_t*, const float*, uint16_t*, int,
                               int, int, int, int, uint32_t);

@@ -763,8 +763,8 @@ class HipWarpRuntime:
         list every kernel that can serve them: the VALU tile kernel and, for
         K <= 9 on rows of L % 4 == 0, the VALU streaming kernel, both at this
         runtime's waves per block; the channel-group matrix-core kernel (8
-        waves; long FMA chains on 16-byte aligned rows with L % 4 == 0 and
-        H % 8 == 0) and, for 33 <= L <= 48, its 16-channel variant (16 waves,
+        waves; long FMA chains on 16-byte aligned tensors with H % 8 == 0)
+        and, for 33 <= L <= 48, its 16-channel variant (16 waves,
         H % 16 == 0)."""
         import pandas as pd
 
@@ -772,7 +772,7 @@ class HipWarpRuntime:
         cg_block = 8 * WAVE_SIZE
         cg16_block = 16 * WAVE_SIZE
         stream = K <= 9 and L % 4 == 0
-        cg16 = 33 <= L <= 48 and L % 4 == 0
+        cg16 = 33 <= L <= 48
         fwd_wpb, dx_wpb = self.waves_per_block, self.dx_waves_per_block
         kernels = [("fwd", _lib.PT_KERNEL_FWD, self.fwd_block, fwd_wpb)]
         if stream:

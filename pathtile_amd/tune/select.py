@@ -210,7 +210,7 @@ def fwd_dx_knob_inert(H: int, L: int, K: int) -> bool:
     matrix-core rule for 16-byte aligned rows, as the tuner allocates)."""
     H, L, K = int(H), int(L), int(K)
     lmax = 16 * ((L + 15) // 16)
-    return L % 4 == 0 and H % 8 == 0 and 2 * _useful_fma_per_row(L, K) * L >= 21 * lmax * lmax
+    return H % 8 == 0 and 2 * _useful_fma_per_row(L, K) * L >= 21 * lmax * lmax
 
 
 def path_regret(rows: list[dict], policy: dict[str, int]) -> dict[str, dict]:

@@ -49,11 +49,11 @@ def rt():
 
 
 def _valu_serves(H, L, K):
-    """The library's FWD/DX rule for 16-byte aligned rows: the matrix cores
-    when L % 4 == 0, H % 8 == 0 and a row needs >= 10.5 (LMAX / L)^2 useful
-    FMAs per output (LMAX = 16 ceil(L / 16)); the VALU kernel otherwise."""
+    """The library's FWD/DX rule for 16-byte aligned tensors: the matrix
+    cores when H % 8 == 0 and a row needs >= 10.5 (LMAX / L)^2 useful FMAs
+    per output (LMAX = 16 ceil(L / 16)); the VALU kernel otherwise."""
     lmax = 16 * ((L + 15) // 16)
-    mfma = L % 4 == 0 and H % 8 == 0 and \
+    mfma = H % 8 == 0 and \
         2 * oracle.useful_fma_per_row(L, K) * L >= 21 * lmax * lmax
     return not mfma
 

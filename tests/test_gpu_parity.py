@@ -6,7 +6,7 @@ Bars (stated per test):
   restatement of the reference's FP32 fmaf chain (oracle.fwd_f32_refchain /
   dx_f32_refchain) and within 1e-5 max-abs-scaled of FP64;
 * FWD / dX, channel-group matrix-core kernel (the default for long FMA
-  chains with L % 4 == 0, H % 8 == 0 and 16-byte aligned rows): within 1e-5
+  chains with H % 8 == 0 and 16-byte aligned tensors, any L): within 1e-5
   max-abs-scaled of FP64 (the matrix cores sum in their own order);
 * dK (atomic and deterministic): within 1e-4 max-abs-scaled of FP64
   (atomic order is not fixed); the deterministic variant is also bitwise
@@ -96,10 +96,10 @@ SHAPES = [
 
 def _mfma_serves(H, L, K, algo):
     """Whether the channel-group matrix-core FWD/DX kernel serves a 16-byte
-    aligned call: the layout must allow it (L % 4 == 0, H % 8 == 0) and,
-    unless forced, the row must need >= 10.5 (LMAX / L)^2 useful FMAs per
-    output (LMAX = 16 ceil(L / 16))."""
-    if algo in ("valu", "tile", "stream") or L % 4 or H % 8:
+    aligned call: the layout must allow it (H % 8 == 0, any L) and, unless
+    forced, the row must need >= 10.5 (LMAX / L)^2 useful FMAs per output
+    (LMAX = 16 ceil(L / 16))."""
+    if algo in ("valu", "tile", "stream") or H % 8:
         return False
     lmax = 16 * ((L + 15) // 16)
     return algo == "mfma" or 2 * oracle.useful_fma_per_row(L, K) * L >= 21 * lmax * lmax
@@ -137,18 +137,33 @@ def test_fwd_dx_bit_exact_and_fp64(rt, shape, algo, monkeypatch):
     (513, 8, 8, 3),       # short filter, forced onto the matrix cores
     (4096, 8, 48, 48),    # one channel group, many interleaved ranges
     (40, 4800, 16, 16),   # 600 channel groups, more than two per CU: one range each
-    # 16-channel workgroups (rows of 33-48 columns, H % 16 == 0), one input stage
+    # rows of 33-48 columns, H % 16 == 0: the 16-channel workgroups (one input
+    # stage) where forced or the call is large
     (1, 16, 48, 48),      # a single ragged step
     (33, 32, 36, 32),     # L below the bucket, ragged last step
     (4096, 16, 48, 48),   # one channel group, many interleaved ranges
     (100, 48, 40, 24),    # three channel groups, odd-ish K
     (257, 16, 44, 47),    # odd K, ragged
+    # rows that are not whole float4s (L % 4 != 0): element-wise LDS operands
+    (1, 8, 37, 48),       # a single ragged step
+    (1000, 96, 37, 48),   # E1, ragged last step
+    (33, 16, 45, 40),     # L three short of the bucket
+    (100, 8, 31, 16),     # 32 bucket
+    (50, 8, 13, 9),       # 16 bucket
+    (77, 24, 5, 7),       # L = 5: a row ends inside the first float4 of the next
+    (20, 8, 1, 1),        # L = 1
 ])
-def test_fwd_dx_matrix_core_kernel(rt, shape, monkeypatch):
+@pytest.mark.parametrize("channels", ["auto", "8", "16"])
+def test_fwd_dx_matrix_core_kernel(rt, shape, channels, monkeypatch):
     """The channel-group matrix-core kernel (forced) against FP64 on the
     layouts it serves, with infinities in the next channel's rows: its
-    masked columns must not leak into this channel's outputs."""
+    masked columns must not leak into this channel's outputs. channels:
+    the library's choice, or 8 / 16 channels per workgroup forced
+    (PATHTILE_ROWS_CHANNELS; 16 needs rows of 33-48 columns and H % 16 == 0,
+    else the library keeps 8)."""
     monkeypatch.setenv("PATHTILE_ROWS_ALGO", "mfma")
+    if channels != "auto":
+        monkeypatch.setenv("PATHTILE_ROWS_CHANNELS", channels)
     B, H, L, K = shape
     x, w, dy = _inputs(B, H, L, K, seed=4000 + B + H + L + K)
     x[:, 1::2, :] = float("inf")
@@ -172,8 +187,11 @@ def _same_bits_or_both_nan(a, b):
     (40, 8, 44, 48),      # L < row bucket
     (33, 8, 32, 17),      # 32 bucket, ragged last step
     (50, 16, 48, 4),      # short filter (VALU by default, matrix cores forced)
+    (40, 8, 37, 48),      # L % 4 != 0 (the matrix-core kernel's element-wise form)
+    (33, 16, 45, 32),     # same, H % 16 == 0
 ])
-def test_nonfinite_values_reach_only_the_reference_window(rt, shape, algo, monkeypatch):
+@pytest.mark.parametrize("channels", ["auto", "16"])
+def test_nonfinite_values_reach_only_the_reference_window(rt, shape, algo, channels, monkeypatch):
     """Inf, -Inf and NaN in x / dY (same channel as finite rows) and in one
     channel's taps. The reference's fmaf chain touches an element only
     through the taps whose window holds it (kernels/warp_tiled_ampere.py:
@@ -185,6 +203,8 @@ def test_nonfinite_values_reach_only_the_reference_window(rt, shape, algo, monke
     1e-5 of it; every other row stays within 1e-5 of FP64."""
     if algo != "auto":
         monkeypatch.setenv("PATHTILE_ROWS_ALGO", algo)
+    if channels != "auto":
+        monkeypatch.setenv("PATHTILE_ROWS_CHANNELS", channels)
     B, H, L, K = shape
     x, w, dy = _inputs(B, H, L, K, seed=6000 + B + H + L + K)
     rng = np.random.default_rng(B + L + K)
@@ -405,7 +425,7 @@ def test_golden_edge_fixtures(rt):
 def test_every_waves_per_block_gives_the_same_bits(wpb, L, H, algo, monkeypatch):
     """VALU: every waves_per_block reproduces the reference's fmaf chain
     (16 waves do not fit rows above 32: refused). Default: the matrix-core
-    kernel (L % 4 == 0, H % 8 == 0, K = 48) runs 8-channel workgroups
+    kernel (H % 8 == 0, K = 48) runs 8-channel workgroups
     whatever waves_per_block says (16 included, at every L), so every value
     gives the bits of waves_per_block = 1."""
     from pathtile_amd import runtime

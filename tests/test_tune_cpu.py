@@ -207,11 +207,12 @@ def _shape_rows(cid, H, L, K, times):
 
 
 def test_fwd_dx_knob_inert_follows_the_library_rule():
-    # matrix cores: L % 4 == 0, H % 8 == 0 and >= 10.5 (LMAX / L)^2 useful FMAs per output
+    # matrix cores: H % 8 == 0 and >= 10.5 (LMAX / L)^2 useful FMAs per output
     assert select.fwd_dx_knob_inert(128, 48, 48)      # P
     assert select.fwd_dx_knob_inert(128, 48, 47)      # E2
     assert not select.fwd_dx_knob_inert(256, 48, 4)   # S: short chain, VALU kernel
-    assert not select.fwd_dx_knob_inert(96, 37, 48)   # E1: L % 4 != 0
+    assert select.fwd_dx_knob_inert(96, 37, 48)       # E1: L % 4 != 0 is served too
+    assert not select.fwd_dx_knob_inert(96, 37, 8)    # short chain at L = 37: VALU
     assert not select.fwd_dx_knob_inert(12, 48, 48)   # H % 8 != 0
     # the useful-FMA threshold against a brute-force count: L = 40 (LMAX 48)
     L, K = 40, 32
