@@ -213,7 +213,7 @@ def time_paths(fns: dict, stream, trials: int, warmup: int, runs: int) -> dict:
     return {k: {"ms": mean(v), "std_ms": stdev(v), "trials_ms": v} for k, v in per.items()}
 
 
-def rows_kernel_name(H: int, L: int, K: int, dx: bool) -> str:
+def rows_kernel_name(B: int, H: int, L: int, K: int, dx: bool) -> str:
     """The FWD/DX kernel the library picks for 16-byte aligned rows: the
     channel-group matrix-core kernel where the layout allows it (H % 8 == 0)
     and a row needs >= 10.5 (LMAX / L)^2 useful FMAs per output
@@ -224,7 +224,11 @@ def rows_kernel_name(H: int, L: int, K: int, dx: bool) -> str:
     p = K // 2
     useful = sum(max(0, min(L, L - (j - p)) - max(0, p - j)) for j in range(K))
     lmax = 16 * ((L + 15) // 16)
-    mfma = algo == "mfma" or (algo != "valu" and 2 * useful * L >= 21 * lmax * lmax)
+    if L % 4 == 0:
+        fast = 2 * useful * L >= 21 * lmax * lmax
+    else:  # rows of L % 4 != 0: every call of >= 2^18 rows, else >= 5 (LMAX / L)^2
+        fast = B * H >= (1 << 18) or 2 * useful * L >= 10 * lmax * lmax
+    mfma = algo == "mfma" or (algo != "valu" and fast)
     if mfma and H % 8 == 0:
         return f"dwconv_rows_cg_kernel<{tag}>"
     return f"dwconv_rows_kernel<{tag}>"
@@ -322,7 +326,7 @@ def workload_leg(rt, name: str, args, dev, stream, keep: bool = False) -> dict:
         raise SystemExit(f"{name}: check of the timed outputs failed: {gate}, "
                          f"deterministic dK bitwise={det_bitwise}")
     nbytes = runtime.minimum_algorithmic_bytes(B, H, L, K)
-    kernels = {"fwd": rows_kernel_name(H, L, K, False), "bwd_input": rows_kernel_name(H, L, K, True),
+    kernels = {"fwd": rows_kernel_name(B, H, L, K, False), "bwd_input": rows_kernel_name(B, H, L, K, True),
                "bwd_weight": dk_kernel_name(H, L, rt.bwdk_block)}
     paths = {}
     for ph, t in timing.items():
@@ -581,7 +585,7 @@ def extras(rt, args, dev, stream, x, w, dy, y, gk) -> dict:
         idx = torch.arange(0, B, max(1, B // 256), device=dev)
         valu_gate = {"fwd": nerr(y[idx], fp64_fwd(x[idx], w)),
                      "bwd_input": nerr(dxv[idx], fp64_dx(dy[idx], w))}
-        kern = {"fwd": rows_kernel_name(H, L, K, False), "bwd_input": rows_kernel_name(H, L, K, True)}
+        kern = {"fwd": rows_kernel_name(B, H, L, K, False), "bwd_input": rows_kernel_name(B, H, L, K, True)}
         del dxv
     finally:
         if prev is None:

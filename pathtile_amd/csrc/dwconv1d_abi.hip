@@ -428,11 +428,12 @@ static int rows_waves_per_cu(int L, int K, long long ntiles) {
 // The channel-group matrix-core kernel costs the same whatever K is (it
 // multiplies by the whole LMAX x LMAX band matrix of the row bucket); the VALU
 // rows kernel's cost grows with the FMA chain. Measured on MI355X over
-// L = 16..48, K = 3..48 and B = 2048..65536, the matrix cores win once a row
-// needs at least 10.5 (LMAX / L)^2 useful FMAs per output on average (LMAX =
-// the row bucket 16, 32 or 48: rows that fill their bucket partly pay for
-// the matrix work they waste); below that the VALU kernel (bit-exact with the
-// reference's fmaf chain) is as fast or faster.
+// L = 16..48 (L % 4 == 0), K = 3..48 and B = 2048..65536, the matrix cores
+// win once a row needs at least 10.5 (LMAX / L)^2 useful FMAs per output on
+// average (LMAX = the row bucket 16, 32 or 48: rows that fill their bucket
+// partly pay for the matrix work they waste); below that the VALU kernel
+// (bit-exact with the reference's fmaf chain) is as fast or faster. Rows of
+// other lengths: kRowsOddMfmaRows below.
 // Where the VALU serves, the tile kernel (a lane per row through an LDS
 // transpose) runs, or the streaming kernel (float4 lanes, no LDS; rows of
 // L % 4 == 0 floats, at most 9 taps) where the channel period would idle
@@ -467,16 +468,26 @@ static bool rows_cg_ok(int H, int L, const void* in, const void* out) {
          rows_cg_lds_bytes(L) <= (size_t)max_lds_per_block();
 }
 
-static RowsAlgo rows_algo(int L, int K) {
+// Rows of L % 4 != 0 reach the VALU kernels a dword at a time; there the
+// matrix cores measured 1.4-2.7x faster at every K from 2^18 rows (B * H)
+// up (B16384 H128 L37 K4: 132 against 232 us; B4096 H64 L29 K4: 11.5
+// against 23.9), and below that from 5 (LMAX / L)^2 useful FMAs per output
+// (B1000 H96 L37: VALU 9.9 against 11.2 us at K = 4, a tie at K = 8, the
+// matrix cores 0.89x at K = 12; B2048 H64 L45 likewise).
+constexpr long long kRowsOddMfmaRows = 1LL << 18;
+
+static RowsAlgo rows_algo(int B, int H, int L, int K) {
   const char* env = getenv("PATHTILE_ROWS_ALGO");
   if (env && strcmp(env, "valu") == 0) return kRowsValu;
   if (env && strcmp(env, "tile") == 0) return kRowsTile;
   if (env && strcmp(env, "stream") == 0) return kRowsStream;
   if (env && strcmp(env, "mfma") == 0) return kRowsMfma;
   const long long lmax = 16LL * (mfma_index(L) + 1);
+  const long long u2l = 2 * useful_fma_per_row(L, K) * L;
   // useful / L >= 10.5 (lmax / L)^2, in integers
-  return 2 * useful_fma_per_row(L, K) * L >= 21 * lmax * lmax ? kRowsMfma
-                                                               : kRowsValu;
+  if (L % 4 == 0) return u2l >= 21 * lmax * lmax ? kRowsMfma : kRowsValu;
+  if ((long long)B * H >= kRowsOddMfmaRows) return kRowsMfma;
+  return u2l >= 10 * lmax * lmax ? kRowsMfma : kRowsValu;
 }
 
 // Launch of the channel-group kernel: one workgroup per (channel group,
@@ -614,7 +625,7 @@ static int rows_path(bool dx, const float* in, const float* w, float* out,
   if (!in || !w || !out) return PT_ERR_NULL;
   if (!aligned(in, 4) || !aligned(w, 4) || !aligned(out, 4))
     return PT_ERR_ALIGN;
-  const RowsAlgo algo = rows_algo(L, K);
+  const RowsAlgo algo = rows_algo(B, H, L, K);
   if (algo == kRowsMfma && rows_cg_ok(H, L, in, out))
     return rows_cg_path(dx, in, w, out, B, H, L, K, stream);
   // The VALU tile kernel: one 64-row LDS tile per wave. Its limits on the

@@ -105,7 +105,7 @@ def build_report(out: Path, policy: dict) -> dict:
     for name, rows, ctrl in (("train", train, train_ctrl), ("holdout", hold, hold_ctrl)):
         per, summary = select.holdout_regret(rows, recomputed)
         for r in per:
-            r["fwd_dx_knob_inert"] = select.fwd_dx_knob_inert(r["H"], r["L"], r["K"])
+            r["fwd_dx_knob_inert"] = select.fwd_dx_knob_inert(r["H"], r["L"], r["K"], r["B"])
         _write_csv(out / f"{name}_per_shape.csv", per)
         summary["per_path"] = select.path_regret(rows, recomputed)
         summary["knob_active_paths"] = select.active_knob_regret(rows, recomputed)

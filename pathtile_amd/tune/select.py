@@ -195,9 +195,10 @@ def verify_frozen_before_holdout(policy: dict, holdout_created_at: Iterable[str]
 # --------------------------------------------------------------------------
 KNOB_INERT_RULE = (
     "FWD/dX waves per workgroup cannot change the kernel where the matrix-core "
-    "FWD/dX kernel serves (L % 4 == 0, H % 8 == 0 and >= 10.5 (LMAX / L)^2 useful "
-    "FMAs per output, LMAX = 16 ceil(L / 16)): it always runs 8-wave workgroups. "
-    "There the FWD/dX candidates differ only by measurement noise.")
+    "FWD/dX kernel serves (H % 8 == 0 and >= 10.5 (LMAX / L)^2 useful FMAs per "
+    "output, LMAX = 16 ceil(L / 16); for L % 4 != 0 every call of >= 2^18 rows "
+    "and smaller ones from 5 (LMAX / L)^2): it always runs 8- or 16-wave "
+    "workgroups. There the FWD/dX candidates differ only by measurement noise.")
 
 
 def _useful_fma_per_row(L: int, K: int) -> int:
@@ -205,12 +206,20 @@ def _useful_fma_per_row(L: int, K: int) -> int:
     return sum(max(0, min(L, L - (j - p)) - max(0, p - j)) for j in range(K))
 
 
-def fwd_dx_knob_inert(H: int, L: int, K: int) -> bool:
+def fwd_dx_knob_inert(H: int, L: int, K: int, B: int) -> bool:
     """True where the FWD/dX knob cannot change the kernel (the library's
-    matrix-core rule for 16-byte aligned rows, as the tuner allocates)."""
-    H, L, K = int(H), int(L), int(K)
+    matrix-core rule for 16-byte aligned tensors, as the tuner allocates):
+    H % 8 == 0 and >= 10.5 (LMAX / L)^2 useful FMAs per output; for
+    L % 4 != 0, every call of at least 2^18 rows (B * H) and smaller ones
+    from 5 (LMAX / L)^2."""
+    H, L, K, B = int(H), int(L), int(K), int(B)
     lmax = 16 * ((L + 15) // 16)
-    return H % 8 == 0 and 2 * _useful_fma_per_row(L, K) * L >= 21 * lmax * lmax
+    u2l = 2 * _useful_fma_per_row(L, K) * L
+    if L % 4 == 0:
+        fast = u2l >= 21 * lmax * lmax
+    else:
+        fast = B * H >= (1 << 18) or u2l >= 10 * lmax * lmax
+    return H % 8 == 0 and fast
 
 
 def path_regret(rows: list[dict], policy: dict[str, int]) -> dict[str, dict]:
@@ -230,14 +239,14 @@ def path_regret(rows: list[dict], policy: dict[str, int]) -> dict[str, dict]:
             "max_regret_pct": normalize_roundoff(max(regs)),
         }
         if phase != "bwd_weight":
-            inert = [c for c in shapes if fwd_dx_knob_inert(*_hlk(rows, c))]
+            inert = [c for c in shapes if fwd_dx_knob_inert(*_hlkb(rows, c))]
             out[phase]["shapes_knob_inert"] = len(inert)
     return out
 
 
-def _hlk(rows: list[dict], config_id: str) -> tuple[int, int, int]:
+def _hlkb(rows: list[dict], config_id: str) -> tuple[int, int, int, int]:
     r = next(r for r in rows if r["config_id"] == config_id)
-    return int(r["H"]), int(r["L"]), int(r["K"])
+    return int(r["H"]), int(r["L"]), int(r["K"]), int(r["B"])
 
 
 def active_knob_regret(rows: list[dict], policy: dict[str, int]) -> dict:
@@ -247,7 +256,7 @@ def active_knob_regret(rows: list[dict], policy: dict[str, int]) -> dict:
     orc = oracle(rows)
     regs = []
     for cid in sorted({r["config_id"] for r in rows}):
-        inert = fwd_dx_knob_inert(*_hlk(rows, cid))
+        inert = fwd_dx_knob_inert(*_hlkb(rows, cid))
         frozen = best = 0.0
         for phase, key in POLICY_KEYS.items():
             f = selected_time(rows, cid, phase, policy[key])

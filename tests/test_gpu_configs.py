@@ -48,14 +48,19 @@ def rt():
     r.close()
 
 
-def _valu_serves(H, L, K):
+def _valu_serves(B, H, L, K):
     """The library's FWD/DX rule for 16-byte aligned tensors: the matrix
     cores when H % 8 == 0 and a row needs >= 10.5 (LMAX / L)^2 useful FMAs
-    per output (LMAX = 16 ceil(L / 16)); the VALU kernel otherwise."""
+    per output (LMAX = 16 ceil(L / 16)); for L % 4 != 0 every call of at
+    least 2^18 rows (B * H) and smaller ones from 5 (LMAX / L)^2; the VALU
+    kernel otherwise."""
     lmax = 16 * ((L + 15) // 16)
-    mfma = H % 8 == 0 and \
-        2 * oracle.useful_fma_per_row(L, K) * L >= 21 * lmax * lmax
-    return not mfma
+    u2l = 2 * oracle.useful_fma_per_row(L, K) * L
+    if L % 4 == 0:
+        fast = u2l >= 21 * lmax * lmax
+    else:
+        fast = B * H >= (1 << 18) or u2l >= 10 * lmax * lmax
+    return not (H % 8 == 0 and fast)
 
 
 def _full_size_case(rt, B, H, L, K, seed, monkeypatch):
@@ -73,7 +78,7 @@ def _full_size_case(rt, B, H, L, K, seed, monkeypatch):
     assert oracle.normalized_max_abs(ys, oracle.fwd_f64(x[it], w)) < FWD_TOL
     assert oracle.normalized_max_abs(dxs, oracle.dx_f64(dy[it], w)) < FWD_TOL
     y_chain, dx_chain = oracle.fwd_f32_refchain(x[it], w), oracle.dx_f32_refchain(dy[it], w)
-    if _valu_serves(H, L, K):
+    if _valu_serves(B, H, L, K):
         assert np.array_equal(ys, y_chain) and np.array_equal(dxs, dx_chain)
     else:
         monkeypatch.setenv("PATHTILE_ROWS_ALGO", "valu")

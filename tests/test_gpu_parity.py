@@ -94,15 +94,21 @@ SHAPES = [
 ]
 
 
-def _mfma_serves(H, L, K, algo):
+def _mfma_serves(B, H, L, K, algo):
     """Whether the channel-group matrix-core FWD/DX kernel serves a 16-byte
     aligned call: the layout must allow it (H % 8 == 0, any L) and, unless
     forced, the row must need >= 10.5 (LMAX / L)^2 useful FMAs per output
-    (LMAX = 16 ceil(L / 16))."""
+    (LMAX = 16 ceil(L / 16)); for L % 4 != 0, every call of at least 2^18
+    rows (B * H) and smaller ones from 5 (LMAX / L)^2."""
     if algo in ("valu", "tile", "stream") or H % 8:
         return False
+    if algo == "mfma":
+        return True
     lmax = 16 * ((L + 15) // 16)
-    return algo == "mfma" or 2 * oracle.useful_fma_per_row(L, K) * L >= 21 * lmax * lmax
+    u2l = 2 * oracle.useful_fma_per_row(L, K) * L
+    if L % 4 == 0:
+        return u2l >= 21 * lmax * lmax
+    return B * H >= (1 << 18) or u2l >= 10 * lmax * lmax
 
 
 @pytest.mark.parametrize("algo", ["auto", "valu", "tile", "stream", "mfma"])
@@ -118,7 +124,7 @@ def test_fwd_dx_bit_exact_and_fp64(rt, shape, algo, monkeypatch):
     y = _fwd(rt, xd, wd).cpu().numpy()
     dx = _dx(rt, dyd, wd).cpu().numpy()
     assert np.isfinite(y).all() and np.isfinite(dx).all()
-    if not _mfma_serves(H, L, K, algo):
+    if not _mfma_serves(B, H, L, K, algo):
         y_ref = oracle.fwd_f32_refchain(x, w)
         dx_ref = oracle.dx_f32_refchain(dy, w)
         assert np.array_equal(y, y_ref), oracle.normalized_max_abs(y, y_ref)
@@ -436,13 +442,13 @@ def test_every_waves_per_block_gives_the_same_bits(wpb, L, H, algo, monkeypatch)
     x, w, dy = _inputs(B, H, L, K, seed=7)
     xd, wd, dyd = _dev(x, w, dy)
     r = runtime.HipWarpRuntime(waves_per_block=wpb)
-    if wpb == 16 and L > 32 and not _mfma_serves(H, L, K, algo):
+    if wpb == 16 and L > 32 and not _mfma_serves(B, H, L, K, algo):
         with pytest.raises(ValueError, match="unsupported launch configuration"):
             _fwd(r, xd, wd)
         return
     y = _fwd(r, xd, wd).cpu().numpy()
     dx = _dx(r, dyd, wd).cpu().numpy()
-    if _mfma_serves(H, L, K, algo):
+    if _mfma_serves(B, H, L, K, algo):
         r1 = runtime.HipWarpRuntime(waves_per_block=1)
         assert np.array_equal(y, _fwd(r1, xd, wd).cpu().numpy())
         assert np.array_equal(dx, _dx(r1, dyd, wd).cpu().numpy())
@@ -654,5 +660,7 @@ def test_resource_report_lists_every_kernel(rt):
                                   "bwd_input", "bwd_input_stream", "bwd_input_matrix_cores",
                                   "bwd_input_matrix_cores_16", "bwd_weight"]
     assert (df["scratch_bytes"] == 0).all()
-    for L, K, n in ((16, 3, 7), (37, 48, 5), (8, 8, 7), (36, 9, 9)):
-        assert len(rt.resource_report(L, K)) == n
+    for L, K, n in ((16, 3, 7), (37, 48, 7), (8, 8, 7), (36, 9, 9)):
+        df = rt.resource_report(L, K)
+        assert len(df) == n
+        assert (df["scratch_bytes"] == 0).all()

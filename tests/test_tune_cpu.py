@@ -208,18 +208,19 @@ def _shape_rows(cid, H, L, K, times):
 
 def test_fwd_dx_knob_inert_follows_the_library_rule():
     # matrix cores: H % 8 == 0 and >= 10.5 (LMAX / L)^2 useful FMAs per output
-    assert select.fwd_dx_knob_inert(128, 48, 48)      # P
-    assert select.fwd_dx_knob_inert(128, 48, 47)      # E2
-    assert not select.fwd_dx_knob_inert(256, 48, 4)   # S: short chain, VALU kernel
-    assert select.fwd_dx_knob_inert(96, 37, 48)       # E1: L % 4 != 0 is served too
-    assert not select.fwd_dx_knob_inert(96, 37, 8)    # short chain at L = 37: VALU
-    assert not select.fwd_dx_knob_inert(12, 48, 48)   # H % 8 != 0
+    assert select.fwd_dx_knob_inert(128, 48, 48, 16384)       # P
+    assert select.fwd_dx_knob_inert(128, 48, 47, 16384)       # E2
+    assert not select.fwd_dx_knob_inert(256, 48, 4, 32768)    # S: short chain, VALU kernel
+    assert select.fwd_dx_knob_inert(96, 37, 48, 1000)         # E1: L % 4 != 0 is served too
+    assert not select.fwd_dx_knob_inert(96, 37, 8, 1000)      # short chain, small call: VALU
+    assert select.fwd_dx_knob_inert(96, 37, 8, 4096)          # L % 4 != 0 from 2^18 rows: matrix cores
+    assert not select.fwd_dx_knob_inert(12, 48, 48, 16384)    # H % 8 != 0
     # the useful-FMA threshold against a brute-force count: L = 40 (LMAX 48)
     L, K = 40, 32
     p = K // 2
     useful = sum(1 for t in range(L) for j in range(K) if 0 <= t + j - p < L)
     assert select._useful_fma_per_row(L, K) == useful
-    assert select.fwd_dx_knob_inert(64, L, K) == (2 * useful * L >= 21 * 48 * 48)
+    assert select.fwd_dx_knob_inert(64, L, K, 2048) == (2 * useful * L >= 21 * 48 * 48)
 
 
 def test_per_path_and_active_knob_regret():
