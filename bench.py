@@ -235,16 +235,16 @@ def rows_kernel_name(B: int, H: int, L: int, K: int, dx: bool) -> str:
 
 
 def dk_kernel_name(H: int, L: int, threads: int) -> str:
-    """The DK kernel the library picks for 16-byte aligned inputs: the
-    channel-group matrix-core kernel when rows are whole float4 (L % 4 == 0)
-    and H is a multiple of the channel group (at most 8 waves per workgroup,
-    one channel per wave for rows of 33-48 columns, two below), else the
-    per-channel matrix-core kernel (or the VALU kernel on request)."""
+    """The DK kernel the library picks: the channel-group matrix-core kernel
+    when H is a multiple of the channel group (at most 8 waves per
+    workgroup, one channel per wave for rows of 33-48 columns, two below;
+    any L), else the per-channel matrix-core kernel (or the VALU kernel on
+    request)."""
     if os.environ.get("PATHTILE_DK_ALGO") == "valu":
         return "dwconv_dk_kernel"
     wpb = threads // 64
     cpw = 1 if L > 32 else 2
-    if L % 4 == 0 and wpb <= 8 and H % (cpw * wpb) == 0:
+    if wpb <= 8 and H % (cpw * wpb) == 0:
         return "dwconv_dk_cg_kernel"
     return "dwconv_dk_mfma_kernel"
 

@@ -32,6 +32,7 @@ SOURCES = [
     "inst_dk_v.hip",
     "inst_dk_s.hip",
     "inst_dk_mfma.hip",
+    "inst_dk_cg1.hip",
     "inst_rows_mfma.hip",
     "inst_rows_mfma_u.hip",
     "inst_bf16.hip",

@@ -155,6 +155,8 @@ struct DkGeom {
   DkAlgo algo;
   bool cg;            // channel-group kernel
   bool nt;            // channel-group kernel with non-temporal loads
+  int epc;            // channel-group kernel: floats per staging load (4 or 1)
+  int cpw;            // channel-group kernel: channels per wave
   int wpb;
   int rows_per_wave;  // VALU: 64-sample chunks per wave; MFMA: samples;
                       // channel-group: samples per workgroup
@@ -162,14 +164,54 @@ struct DkGeom {
   long long nblocks;  // workgroups
 };
 
-// Channel-group DK: whole 16-byte aligned rows (L % 4 == 0) in groups of
-// dk_cpw(L) channels per wave (one in the 48-column row bucket, two below;
-// BF16 DK: two), at most 8 waves per workgroup.
+// Channel-group DK: groups of dk_cpw(L) channels per wave (one in the
+// 48-column row bucket, two below; BF16 DK: two), at most 8 waves per
+// workgroup. The FP32 kernel serves any row length (dk_cg_layout_ok); the
+// BF16 one needs whole 16-byte aligned rows (dk_cg_ok, L % 4 == 0).
 static int dk_cpw(int L) { return dk_cg_cpw(16 * (mfma_index(L) + 1)); }
 
-static bool dk_cg_ok(int H, int L, int threads, int cpw) {
+static bool dk_cg_layout_ok(int H, int threads, int cpw) {
   const int wpb = threads / kWave;
-  return L % 4 == 0 && wpb <= 8 && H % (cpw * wpb) == 0;
+  return wpb <= 8 && H % (cpw * wpb) == 0;
+}
+
+static bool dk_cg_ok(int H, int L, int threads, int cpw) {
+  return L % 4 == 0 && dk_cg_layout_ok(H, threads, cpw);
+}
+
+// Staging width of the FP32 channel-group DK: 16-byte chunks when both
+// tensors are 16-byte aligned and a group's segment (hc L floats) and a
+// sample (H L floats) are whole chunks, dwords otherwise.
+static int dk_cg_epc(int H, int L, int hc, bool vec16) {
+  return vec16 && ((long long)hc * L) % 4 == 0 && ((long long)H * L) % 4 == 0 ? 4 : 1;
+}
+
+// Rows of 33-48 columns on tensors of at least 256 MiB (non-temporal
+// loads): one channel per wave where a workgroup's segment (4 wpb L bytes)
+// is a whole number of 64-byte units, else two channels per wave where H
+// allows and the segments are then whole 16-byte chunks. Measured on MI355X over L = 33..48 at B16384
+// H128 K48 with 128 threads (three interleaved rounds): one channel won at
+// L = 40 and 48 (114.3 against 118.8 us, 122.7 against 125.7) and tied at
+// 36; two won everywhere else, by up to 9% at even L (L38 111.8 against
+// 119.6, L44 124.2 against 138.9, L46 125.3 against 137.1) and by 10-24%
+// at odd L, where one channel per wave leaves dword staging (L37 115.7
+// against 139.0, L41 122.8 against 155.7). Below 256 MiB one channel per
+// wave stayed 5-7% faster at every L tried (B4096 H128 L33..47 K48).
+static void dk_cg_staging(DkGeom& g, int H, int L, bool vec16) {
+  g.cpw = dk_cpw(L);
+  g.epc = dk_cg_epc(H, L, g.cpw * g.wpb, vec16);
+  if (g.cpw == 1 && g.nt && ((long long)4 * g.wpb * L) % 64 != 0 &&
+      H % (2 * g.wpb) == 0 && dk_cg_epc(H, L, 2 * g.wpb, vec16) == 4) {
+    g.cpw = 2;
+    g.epc = 4;
+  }
+}
+
+static DkCgFn dk_cg_fn(bool nt, int epc, int cpw, int L) {
+  if (cpw != dk_cpw(L)) return kDkCgPairNT;  // two channels per wave, 48 bucket
+  const DkCgFn* t = epc == 4 ? (nt ? kDkCgTableNT : kDkCgTable)
+                             : (nt ? kDkCgTable1NT : kDkCgTable1);
+  return t[mfma_index(L)];
 }
 
 // Tensors of at least the 256 MiB MALL stream differently from smaller ones
@@ -259,10 +301,13 @@ static DkGeom dk_geometry(int B, int H, int L, int K, int threads, bool vec16,
   g.wpb = threads / kWave;
   const long long wpb = g.wpb;
   const long long rows = (long long)B * H;
-  g.cg = g.algo == kDkMfma && vec16 && dk_cg_ok(H, L, threads, dk_cpw(L));
+  g.cg = g.algo == kDkMfma && dk_cg_layout_ok(H, threads, dk_cpw(L));
   g.nt = g.cg && cg_large(B, H, L);
+  g.epc = 4;
+  g.cpw = dk_cpw(L);
   if (g.cg) {
-    const long long ngroups = (long long)H / (dk_cpw(L) * wpb);
+    dk_cg_staging(g, H, L, vec16);
+    const long long ngroups = (long long)H / (g.cpw * wpb);
     long long nr = cg_ranges(B, H, L);
     // The stride rule was measured where its workgroups fill the resident
     // slots exactly (H a power of two). Where they overflow them, the few
@@ -271,10 +316,10 @@ static DkGeom dk_geometry(int B, int H, int L, int K, int threads, bool vec16,
     // (2016); B32768 H96 L48 K4 249 against 186 us. Cap at one round.
     if (device_cap) {
       const int mi = mfma_index(L);
-      const DkCgFn fn = (g.nt ? kDkCgTableNT : kDkCgTable)[mi];
+      const DkCgFn fn = dk_cg_fn(g.nt, g.epc, g.cpw, L);
       const long long resident =
           (long long)blocks_per_cu((const void*)fn, threads,
-                                   cg_lds_bytes(16 * (mi + 1), (int)wpb, L, dk_cpw(L))) *
+                                   cg_lds_bytes(16 * (mi + 1), (int)wpb, L, g.cpw)) *
           num_cus();
       if (ngroups * nr > resident) nr = resident / ngroups;
       if (nr < 1) nr = 1;
@@ -682,8 +727,8 @@ static int dk_path(bool det, const float* gy, const float* x, float* dst,
   uint32_t nblocks = (uint32_t)g.nblocks;
   int rpw = g.rows_per_wave, nbt = g.nbt, d = det ? 1 : 0;
   if (g.cg) {
-    DkCgFn fn = (g.nt ? kDkCgTableNT : kDkCgTable)[mfma_index(L)];
-    const size_t lds = cg_lds_bytes(16 * (mfma_index(L) + 1), g.wpb, L, dk_cpw(L));
+    DkCgFn fn = dk_cg_fn(g.nt, g.epc, g.cpw, L);
+    const size_t lds = cg_lds_bytes(16 * (mfma_index(L) + 1), g.wpb, L, g.cpw);
     void* args[] = {&gy, &x, &dst, &B, &H, &L, &K, &nbt, &nblocks, &d};
     return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream,
                   args);
@@ -1039,12 +1084,10 @@ int pt_dwconv1d_dk_det_workspace_bytes(int B, int H, int L, int K,
     *bytes = 0;
     return PT_OK;
   }
-  // Either kernel may serve the call (the channel-group one needs 16-byte
-  // aligned inputs): size for the larger partial count.
-  const pt::DkGeom g0 = pt::dk_geometry(B, H, L, K, threads_per_block, false);
-  const pt::DkGeom g1 = pt::dk_geometry(B, H, L, K, threads_per_block, true);
-  const int nbt = g0.nbt > g1.nbt ? g0.nbt : g1.nbt;
-  *bytes = (size_t)H * (size_t)K * (size_t)nbt * sizeof(float);
+  // The kernel and its partial count follow from the shape and block size
+  // (pointer alignment only sets the channel-group kernel's staging width).
+  const pt::DkGeom g = pt::dk_geometry(B, H, L, K, threads_per_block, true);
+  *bytes = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
   return PT_OK;
 }
 

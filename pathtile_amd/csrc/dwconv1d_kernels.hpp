@@ -1471,8 +1471,9 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_bf16mma_kernel(
 // a fixed multi-MiB stride apart, and the time then swung by 30 % with that
 // stride on MI355X).
 //
-// Per step the workgroup loads both tensors' segments (dwordx4; rows are
-// 16-byte aligned, L % 4 == 0) into registers two steps ahead and into one
+// Per step the workgroup loads both tensors' segments (dwordx4 chunks where
+// the tensors are 16-byte aligned and segments and samples are whole chunks,
+// dwords otherwise: any L) into registers two steps ahead and into one
 // of two LDS stages while the matrix cores consume the other; wave w
 // accumulates D_c[t][s] = sum_b dy[b,c,t] * x[b,c,s] for its channels, then
 // reduces the diagonals of each D_c (dk[c, j] = sum_t D_c[t][t + j - p])
@@ -1581,7 +1582,31 @@ __device__ __forceinline__ void dk_cg_epilogue(
   }
 }
 
-template <int LMAX, int LOAD_CPOL = kCpolNone, int CPW = dk_cg_cpw(LMAX)>
+// Staging units of the channel-group DK: EPC floats per lane and load (4:
+// dwordx4 chunks, for 16-byte aligned tensors whose segments and samples are
+// whole chunks; 1: dwords, for any row length and 4-byte aligned tensors).
+template <int EPC> struct CgUnit;
+template <> struct CgUnit<4> { using T = u32x4; };
+template <> struct CgUnit<1> { using T = uint32_t; };
+
+template <int EPC, int CPOL>
+__device__ __forceinline__ typename CgUnit<EPC>::T buf_load_unit(__amdgpu_buffer_rsrc_t r,
+                                                                 uint32_t voff) {
+  if constexpr (EPC == 4)
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, CPOL);
+  else
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, CPOL);
+}
+
+template <int EPC>
+__device__ __forceinline__ void unit_to_lds(float* dst, const typename CgUnit<EPC>::T v) {
+  if constexpr (EPC == 4)
+    chunk_to_lds(dst, v);
+  else
+    *dst = __uint_as_float(v);
+}
+
+template <int LMAX, int LOAD_CPOL = kCpolNone, int CPW = dk_cg_cpw(LMAX), int EPC = 4>
 __global__ __launch_bounds__(512) void dwconv_dk_cg_kernel(
     const float* __restrict__ gy, const float* __restrict__ x,
     float* __restrict__ dst, int B, int H, int L, int K, int nranges,
@@ -1603,7 +1628,7 @@ __global__ __launch_bounds__(512) void dwconv_dk_cg_kernel(
   const int tsteps = (B + kCgStep - 1) / kCgStep;
   const int nsteps = r < tsteps ? (tsteps - 1 - r) / nranges + 1 : 0;
 
-  constexpr int EPC = 4;                       // floats per 16-byte chunk
+  using U = typename CgUnit<EPC>::T;
   const int seg = hc * L;                     // elements per sample segment
   const int segc = seg / EPC;                 // chunks per segment
   const int sk = seg + kCgPad;                // LDS stride between samples
@@ -1623,15 +1648,15 @@ __global__ __launch_bounds__(512) void dwconv_dk_cg_kernel(
     const int k = e < per ? e / segc : kCgStep;  // kCgStep: no element
     const int q = e - (e / segc) * segc;
     ek[i] = k;
-    eoff[i] = (uint32_t)k * row_bytes + grp_bytes + 16u * (uint32_t)q;
+    eoff[i] = (uint32_t)k * row_bytes + grp_bytes + 4u * EPC * (uint32_t)q;
     elds[i] = (uint32_t)(k * sk + EPC * q);
   }
 
   // Global -> registers for local step s (global step r + s * nranges):
   // buffer resources rebased on the step's first sample; elements past the
   // stage or past B read 0 (no branch).
-  u32x4 stg[DEPTH][2][kNpt];
-  auto load_step = [&](int s, u32x4 (&st)[2][kNpt]) {
+  U stg[DEPTH][2][kNpt];
+  auto load_step = [&](int s, U (&st)[2][kNpt]) {
     const int bs = (r + s * nranges) * kCgStep;
     const size_t r0 = (size_t)bs * (size_t)H * (size_t)L;
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(gy + r0);
@@ -1640,17 +1665,17 @@ __global__ __launch_bounds__(512) void dwconv_dk_cg_kernel(
 #pragma unroll
     for (int i = 0; i < kNpt; ++i) {
       const uint32_t o = ek[i] < klim ? eoff[i] : kOob;
-      st[0][i] = buf_load_chunk<LOAD_CPOL>(rg, o);
-      st[1][i] = buf_load_chunk<LOAD_CPOL>(rx, o);
+      st[0][i] = buf_load_unit<EPC, LOAD_CPOL>(rg, o);
+      st[1][i] = buf_load_unit<EPC, LOAD_CPOL>(rx, o);
     }
   };
-  auto store_stage = [&](int buf, const u32x4 (&st)[2][kNpt]) {
+  auto store_stage = [&](int buf, const U (&st)[2][kNpt]) {
     float* base = lds + buf * 2 * sz;
 #pragma unroll
     for (int i = 0; i < kNpt; ++i) {
       if (ek[i] < kCgStep) {
-        chunk_to_lds(base + elds[i], st[0][i]);
-        chunk_to_lds(base + sz + elds[i], st[1][i]);
+        unit_to_lds<EPC>(base + elds[i], st[0][i]);
+        unit_to_lds<EPC>(base + sz + elds[i], st[1][i]);
       }
     }
   };

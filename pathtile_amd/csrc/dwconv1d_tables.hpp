@@ -42,6 +42,11 @@ using DkCgFn = void (*)(const float*, const float*, float*, int, int, int, int,
 // loads (tensors of at least 256 MiB)
 extern const DkCgFn kDkCgTable[3];
 extern const DkCgFn kDkCgTableNT[3];
+// the same staging dwords (any row length, 4-byte aligned tensors)
+extern const DkCgFn kDkCgTable1[3];
+extern const DkCgFn kDkCgTable1NT[3];
+// row bucket 48 with two channels per wave, 16-byte chunks, non-temporal
+extern const DkCgFn kDkCgPairNT;
 using RowsCgFn = void (*)(const float*, const float*, float*, int, int, int,
                           int, int, uint32_t);
 // channel-group matrix-core FWD / DX: [0 = FWD, 1 = DX][row bucket 16, 32, 48]

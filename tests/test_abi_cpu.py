@@ -268,16 +268,18 @@ def test_workspace_bytes(lib):
         assert out.value % (H * K * 4) == 0  # [H, K, num_btiles] floats
         return out.value // (H * K * 4)
 
-    # Two kernels can serve a call (the channel-group one needs 16-byte
-    # aligned rows), so the workspace holds the larger partial count:
-    #  * per-channel batch tiles of (threads / 64) waves x rows-per-wave
-    #    samples; rows per wave are whole load groups (48 / 24 / 16 samples
-    #    for rows of <= 16 / <= 32 / <= 48 floats), up to 128 samples;
-    #  * channel-group interleaved sample ranges (L % 4 == 0, <= 8 waves, H a
-    #    multiple of 2 * waves), at most one per 4-sample step: for tensors of
-    #    at least 256 MiB, of 2^k and 3 * 2^(k-1) in [8, 256] the one nearest
-    #    by ratio to 3 MiB / (16 H L bytes) (ties to the smaller); below that,
-    #    the power of two in [8, 256] nearest to 2.5 MiB / (16 H L bytes).
+    # The kernel, and so the partial count, follows from the shape and block
+    # size (alignment only sets the channel-group kernel's staging width):
+    #  * channel-group interleaved sample ranges where the layout allows (at
+    #    most 8 waves, H a multiple of the group: one channel per wave for
+    #    rows of 33-48 columns, two below; any L), at most one per 4-sample
+    #    step: for tensors of at least 256 MiB, of 2^k and 3 * 2^(k-1) in
+    #    [8, 256] the one nearest by ratio to 3 MiB / (16 H L bytes) (ties to
+    #    the smaller); below that, the power of two in [8, 256] nearest to
+    #    2.5 MiB / (16 H L bytes);
+    #  * otherwise per-channel batch tiles of (threads / 64) waves x
+    #    rows-per-wave samples; rows per wave are whole load groups (48 / 24
+    #    / 16 samples for rows of <= 16 / <= 32 / <= 48 floats), up to 128.
     # Both depend on the shape and block size only, never on the device.
     def per_channel(B, H, L, wpb):
         grp = 48 // (-(-L // 16))
@@ -287,7 +289,8 @@ def test_workspace_bytes(lib):
         return -(-B // (wpb * rpw))
 
     def channel_group(B, H, L, wpb):
-        if L % 4 or wpb > 8 or H % (2 * wpb):
+        cpw = 1 if L > 32 else 2
+        if wpb > 8 or H % (cpw * wpb):
             return 0
         if 4 * B * H * L >= 256 * 2**20:
             want = 3 * 2**20 / (16 * H * L)
@@ -301,18 +304,20 @@ def test_workspace_bytes(lib):
         return max(1, min(n, -(-B // 4)))
 
     for (B, H, L, K) in [(16384, 128, 48, 48), (16384, 64, 16, 3), (1000, 96, 37, 48),
-                         (32768, 256, 48, 4), (20, 4, 8, 3), (4096, 128, 24, 8), (3, 16, 48, 5)]:
+                         (32768, 256, 48, 4), (20, 4, 8, 3), (4096, 128, 24, 8), (3, 16, 48, 5),
+                         (1000, 7, 37, 48), (500, 12, 30, 9)]:
         for threads in (64, 128, 192, 256, 512, 768):
             wpb = threads // 64
             n = nbt(B, H, L, K, threads)
-            assert n == max(per_channel(B, H, L, wpb), channel_group(B, H, L, wpb)), (B, H, L, threads)
+            assert n == (channel_group(B, H, L, wpb) or per_channel(B, H, L, wpb)), (B, H, L, threads)
     assert nbt(16384, 128, 48, 48, 256) == 32   # 32 ranges (96 KiB steps), 32 tiles
     assert nbt(16384, 64, 16, 3, 256) == 128    # 64 MiB tensors, 16 KiB steps: 128
     assert nbt(16384, 128, 40, 48, 256) == 32   # 80 KiB steps: 38.4 -> 32 (not 48)
     assert nbt(16384, 128, 32, 8, 256) == 48    # 256 MiB tensors, 64 KiB steps: 48 = 3 * 2^4
     assert nbt(8192, 128, 32, 8, 256) == 32     # 128 MiB tensors: 2.5 MiB rule, 32
     assert nbt(16384, 128, 48, 48, 192) == 43   # per-channel: 3 waves x 128 samples
-    assert nbt(1000, 96, 37, 48, 64) == 63      # L % 4 != 0: per-channel only
+    assert nbt(1000, 96, 37, 48, 64) == 64      # L % 4 != 0: channel-group, 2.5 MiB rule
+    assert nbt(1000, 7, 37, 48, 128) == 32      # H % 2 != 0: per-channel, 2 waves x 16 samples
     st = lib.pt_dwconv1d_dk_det_workspace_bytes(0, 4, 8, 3, 256, ctypes.byref(out))
     assert st == _lib.PT_OK and out.value == 0
     lds = ctypes.c_int(0)

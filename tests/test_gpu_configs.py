@@ -118,6 +118,65 @@ def test_odd_k_config_full_size(rt, monkeypatch):
     _full_size_case(rt, 16384, 128, 48, 47, 78, monkeypatch)
 
 
+def test_odd_row_length_above_the_mall_full_size(rt, monkeypatch):
+    """L % 4 != 0 on tensors above 256 MiB (B16384 H128 L37 K48, 310 MB
+    each): FWD/dX on the matrix-core kernel's element-wise form with
+    non-temporal loads; dK on the channel-group kernel with two channels per
+    wave and 16-byte chunk staging. The same values in 4-byte aligned
+    storage take one channel per wave with dword staging (another range
+    count, so other bits): within 1e-4 of FP64 and bitwise reproducible."""
+    _full_size_case(rt, 16384, 128, 37, 48, 79, monkeypatch)
+    B, H, L, K = 16384, 128, 37, 48
+    x, w, dy = oracle.make_inputs(B, H, L, K, 79)
+    xd, dyd = x.cuda(), dy.cuda()
+    g_aligned = torch.full((H, K), float("nan"), device="cuda")
+    rt.launch_bwd_weight_deterministic(dyd, xd, g_aligned, K)
+    flat = torch.empty(2 * (xd.numel() + 1), device="cuda")
+    xm = flat[1:xd.numel() + 1].view(B, H, L)
+    dym = flat[xd.numel() + 2:].view(B, H, L)
+    assert xm.data_ptr() % 16 != 0 and dym.data_ptr() % 16 != 0
+    xm.copy_(xd)
+    dym.copy_(dyd)
+    del xd, dyd
+    g_mis = [torch.full((H, K), float("nan"), device="cuda") for _ in range(2)]
+    for g in g_mis:
+        rt.launch_bwd_weight_deterministic(dym, xm, g, K)
+    ga = torch.full((H, K), float("nan"), device="cuda")
+    rt.launch_bwd_weight(dym, xm, ga, K, zero_first=True)
+    ref = oracle.dk_f64(dy, x, K)
+    assert oracle.normalized_max_abs(g_aligned.cpu().numpy(), ref) < DK_TOL
+    assert oracle.normalized_max_abs(g_mis[0].cpu().numpy(), ref) < DK_TOL
+    assert oracle.normalized_max_abs(ga.cpu().numpy(), ref) < DK_TOL
+    assert torch.equal(g_mis[0], g_mis[1])
+
+
+@pytest.mark.parametrize("shape", [(12000, 128, 44, 48), (13800, 128, 38, 13)])
+def test_dk_two_channels_per_wave_above_the_mall(shape):
+    """Tensors just above 256 MiB with rows whose one-channel segments are
+    not whole 64-byte units (L = 44, 38 at 128 threads): the channel-group dK
+    runs two channels per wave. Atomic and deterministic within 1e-4 of
+    FP64, deterministic bitwise reproducible, taps without overlap exact 0."""
+    from pathtile_amd import runtime
+
+    B, H, L, K = shape
+    assert 4 * B * H * L >= 256 * 2**20
+    print(f"[case] dK above the MALL B={B} H={H} L={L} K={K}", flush=True)
+    x, w, dy = oracle.make_inputs(B, H, L, K, seed=B + L)
+    xd, dyd = x.cuda(), dy.cuda()
+    r = runtime.HipWarpRuntime(bwdk_block=128)
+    ga = torch.full((H, K), float("nan"), device="cuda")
+    r.launch_bwd_weight(dyd, xd, ga, K, zero_first=True)
+    g1 = torch.full((H, K), float("nan"), device="cuda")
+    g2 = torch.full((H, K), float("nan"), device="cuda")
+    r.launch_bwd_weight_deterministic(dyd, xd, g1, K)
+    r.launch_bwd_weight_deterministic(dyd, xd, g2, K)
+    ref = oracle.dk_f64(dy, x, K)
+    assert oracle.normalized_max_abs(ga.cpu().numpy(), ref) < DK_TOL
+    assert oracle.normalized_max_abs(g1.cpu().numpy(), ref) < DK_TOL
+    assert torch.equal(g1, g2)
+    r.close()
+
+
 REF_AMPERE_CASES = [(2, 4, 16, 8), (4, 8, 31, 16), (8, 16, 48, 24), (32, 64, 48, 48),
                     (128, 128, 48, 48)]        # kernels/warp_tiled_ampere.py:920-926
 REF_SHARED_CASES = [(2, 4, 48, 47), (2, 4, 48, 48), (2, 4, 48, 49),

@@ -365,23 +365,34 @@ def _misaligned(t):
     (5, 32, 40, 24),      # fewer steps than interleaved ranges, L < bucket
     (2048, 128, 20, 9),   # L in the 32 bucket, odd K
     (4099, 16, 16, 48),   # K > L: zero-overlap taps
+    (1001, 64, 37, 3),    # L % 4 != 0: dword staging whatever the alignment
+    (777, 32, 45, 48),    # same, L three short of the bucket
+    (300, 16, 29, 16),    # same, 32 bucket
+    (500, 12, 30, 9),     # L % 4 == 2: whole chunks where the group is even
+    (64, 96, 13, 5),      # 16 bucket, odd L
 ])
 @pytest.mark.parametrize("threads", [64, 128, 256, 512])
-def test_dk_channel_group_matches_per_channel(shape, threads):
-    """16-byte aligned rows with L % 4 == 0 and H a multiple of 2 x waves take
-    the channel-group kernel; the same values in misaligned storage take the
-    per-channel kernel. Both agree with FP64, and the deterministic variant is
-    bitwise reproducible on each path with the workspace the API sizes."""
+def test_dk_channel_group_staging_widths(shape, threads):
+    """Where H is a multiple of the channel group (one channel per wave for
+    rows of 33-48 columns, two below; at most 8 waves) the channel-group
+    kernel serves any L: 16-byte chunk staging for 16-byte aligned tensors
+    whose group segments and samples are whole chunks, dword staging
+    otherwise (odd L, or the same values in misaligned storage). The
+    geometry is the same either way, so the deterministic results of the
+    two stagings are bitwise equal; both agree with FP64 and repeat bit for
+    bit with the workspace the API sizes."""
     from pathtile_amd import runtime
 
     B, H, L, K = shape
-    if H % (2 * (threads // 64)):
+    cpw = 1 if L > 32 else 2
+    if H % (cpw * (threads // 64)):
         pytest.skip("H not a multiple of the channel group")
     x, w, dy = _inputs(B, H, L, K, seed=3000 + B + L + K)
     xd, dyd = _dev(x, dy)
     xm, dym = _misaligned(x), _misaligned(dy)
     ref = oracle.dk_f64(dy, x, K)
     r = runtime.HipWarpRuntime(bwdk_block=threads)
+    dets = []
     for a, b in ((dyd, xd), (dym, xm)):
         ga = _dk_atomic(r, a, b, K).cpu().numpy()
         g1 = _dk_det(r, a, b, K).cpu().numpy()
@@ -389,10 +400,12 @@ def test_dk_channel_group_matches_per_channel(shape, threads):
         assert oracle.normalized_max_abs(ga, ref) < DK_TOL
         assert oracle.normalized_max_abs(g1, ref) < DK_TOL
         assert np.array_equal(g1, g2)
+        dets.append(g1)
         for j in range(K):
             lo, hi = oracle.valid_tap_range(L, K, j)
             if hi <= lo:
                 assert np.all(ga[:, j] == 0.0) and np.all(g1[:, j] == 0.0)
+    assert np.array_equal(dets[0], dets[1])
     r.close()
 
 

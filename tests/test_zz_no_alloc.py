@@ -59,7 +59,8 @@ def _det_noalloc(lib, dy, x, K, threads):
 @pytest.mark.parametrize("threads", [128, 256])
 @pytest.mark.parametrize("first,second", [
     ((16384, 128, 48, 48), (300, 16, 48, 47)),   # channel-group kernel, then a smaller one
-    ((4096, 96, 37, 48), (1000, 8, 37, 5)),      # per-channel kernel (L % 4 != 0)
+    ((4096, 96, 37, 48), (1000, 8, 37, 5)),      # channel-group kernel, dword staging (L % 4 != 0)
+    ((4096, 7, 37, 48), (1000, 5, 20, 5)),       # per-channel kernel (H not a multiple of the group)
 ])
 def test_noalloc_matches_workspace_entry_point(first, second, threads):
     from pathtile_amd import _lib
