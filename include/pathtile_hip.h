@@ -54,7 +54,7 @@ extern "C" {
 #define PT_KERNEL_DX 1
 #define PT_KERNEL_DK 2
 #define PT_KERNEL_DK_REDUCE 3
-#define PT_KERNEL_DK_CG 4      /* channel-group DK (L % 4 == 0, H % (2 * waves) == 0) */
+#define PT_KERNEL_DK_CG 4      /* channel-group DK (H a multiple of channels per wave x waves) */
 #define PT_KERNEL_FWD_CG 5     /* channel-group matrix-core FWD (H % 8 == 0) */
 #define PT_KERNEL_DX_CG 6      /* channel-group matrix-core DX  (H % 8 == 0) */
 #define PT_KERNEL_FWD_STREAM 7 /* short-tap streaming FWD (K <= 9, L % 4 == 0) */
@@ -132,8 +132,9 @@ int pt_dwconv1d_dk_det_workspace_bytes(int B, int H, int L, int K,
 /*
  * Weight gradient, deterministic two-pass variant: per-batch-tile partials
  * into `workspace`, then a fixed-order reduction that overwrites dk (no
- * zero-init needed). Bitwise reproducible for a fixed shape and
- * threads_per_block. Replaces dwconv1d_warptile_bwd_weight_partials +
+ * zero-init needed). Bitwise reproducible for a fixed shape,
+ * threads_per_block and input alignment (16-byte aligned or not) on a
+ * given device. Replaces dwconv1d_warptile_bwd_weight_partials +
  * dwconv1d_warptile_reduce_partials
  * (kernels/warp_tiled_noatomic_optimized.py:881,1116; launch :1473-1554).
  */
