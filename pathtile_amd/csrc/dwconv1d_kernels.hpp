@@ -1301,7 +1301,7 @@ __host__ __device__ constexpr size_t rows_bf16mma_lds_bytes(int L, int hc) {
   return (size_t)4 * kRowsCgStep * (hc * L + 8) * sizeof(uint16_t);
 }
 
-template <int LMAX, bool DX, int HC>
+template <int LMAX, bool DX, int HC, int LOAD_CPOL = kCpolNT>
 __global__ __launch_bounds__(HC * kWave) void dwconv_rows_bf16mma_kernel(
     const uint16_t* __restrict__ in, const float* __restrict__ w,
     uint16_t* __restrict__ out, int B, int H, int L, int K, int nranges,
@@ -1352,7 +1352,7 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_bf16mma_kernel(
     const int klim = min(kRowsCgStep, B - bs);
 #pragma unroll
     for (int i = 0; i < kNpt; ++i)
-      st[i] = buf_load_chunk<kCpolNT>(rs, ek[i] < klim ? eoff[i] : kOob);
+      st[i] = buf_load_chunk<LOAD_CPOL>(rs, ek[i] < klim ? eoff[i] : kOob);
   };
   auto store_stage = [&](int buf, const u32x4 (&st)[kNpt]) {
 #pragma unroll

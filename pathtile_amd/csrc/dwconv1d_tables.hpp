@@ -67,6 +67,8 @@ using RowsCgBf16Fn = void (*)(const uint16_t*, const float*, uint16_t*, int,
 using DkBf16Fn = void (*)(const uint16_t*, const uint16_t*, float*, int, int,
                             int, int, int, uint32_t, int);
 extern const RowsCgBf16Fn kRowsCgTableBf16[2][2][3];
+// 8-channel groups with plain input loads: [dx][row bucket]
+extern const RowsCgBf16Fn kRowsCgTableBf16PL[2][3];
 using DkClFn = void (*)(const float*, const float*, float*, int, int, int, int,
                        int, uint32_t);
 extern const DkClFn kDkClTable[3];

@@ -18,6 +18,14 @@ const RowsCgBf16Fn kRowsCgTableBf16[2][2][3] = {
      {&dwconv_rows_bf16mma_kernel<16, true, 16>,
       &dwconv_rows_bf16mma_kernel<32, true, 16>,
       &dwconv_rows_bf16mma_kernel<48, true, 16>}}};
+// The same, 8-channel groups with plain (cached) input loads: [dx][row bucket]
+const RowsCgBf16Fn kRowsCgTableBf16PL[2][3] = {
+    {&dwconv_rows_bf16mma_kernel<16, false, 8, kCpolNone>,
+     &dwconv_rows_bf16mma_kernel<32, false, 8, kCpolNone>,
+     &dwconv_rows_bf16mma_kernel<48, false, 8, kCpolNone>},
+    {&dwconv_rows_bf16mma_kernel<16, true, 8, kCpolNone>,
+     &dwconv_rows_bf16mma_kernel<32, true, 8, kCpolNone>,
+     &dwconv_rows_bf16mma_kernel<48, true, 8, kCpolNone>}};
 // DK on the BF16 matrix cores: plain and non-temporal loads
 const DkBf16Fn kDkBf16mmaTable[3] = {&dwconv_dk_bf16mma_kernel<16, kCpolNone>,
                                        &dwconv_dk_bf16mma_kernel<32, kCpolNone>,

@@ -110,17 +110,25 @@ def test_bf16_dk_every_block_size(threads):
     assert oracle.normalized_max_abs(g.cpu().numpy(), ref) < DK_TOL
 
 
-def test_bf16_large_shape_sampled_rows(rt):
-    """B16384 H128 L48 K48 in BF16 (192 MiB per tensor): sampled rows of
-    FWD/dX against FP64 and dK over the full batch."""
-    B, H, L, K = 16384, 128, 48, 48
+@pytest.mark.parametrize("shape", [
+    (16384, 128, 48, 48),   # 192 MiB per tensor: 8-channel groups, plain loads
+    (22016, 128, 48, 40),   # 258 MiB per tensor: 16-channel groups, non-temporal loads
+    (16384, 136, 48, 48),   # 204 MiB, H % 16 != 0
+])
+def test_bf16_large_shape_sampled_rows(rt, shape):
+    """Large BF16 calls on both sides of the 256 MiB load-policy boundary:
+    sampled rows of FWD/dX against FP64 (the first and the last sample among
+    them) and dK over the full batch."""
+    B, H, L, K = shape
     x, w, dy = _inputs(B, H, L, K, seed=12)
     xd, wd, dyd = x.cuda(), w.cuda(), dy.cuda()
     y = torch.empty_like(xd)
     dx = torch.empty_like(dyd)
     rt.launch_fwd_bf16(xd, wd, y)
     rt.launch_bwd_input_bf16(dyd, wd, dx)
-    idx = torch.from_numpy(np.random.default_rng(3).choice(B, 128, replace=False))
+    idx = np.sort(np.random.default_rng(3).choice(B, 128, replace=False))
+    idx[0], idx[-1] = 0, B - 1
+    idx = torch.from_numpy(idx)
     _check_rounded(y[idx.cuda()], oracle.fwd_f64(x[idx].float(), w))
     _check_rounded(dx[idx.cuda()], oracle.dx_f64(dy[idx].float(), w))
     g = torch.empty(H, K, device="cuda")
