@@ -20,10 +20,10 @@
 //   * DK contracts the batch on the matrix cores (v_mfma_f32_16x16x4_f32):
 //     D_h[t][s] = sum_b dy[b,h,t] * x[b,h,s], and the taps are the diagonal
 //     sums dk[h,j] = sum_t D_h[t][t + j - p]. dwconv_dk_cg_kernel (default
-//     for 16-byte aligned rows, L % 4 == 0) streams contiguous channel-group
-//     segments [b, g*HC .. g*HC+HC, :] with each wave owning two channels;
-//     dwconv_dk_mfma_kernel (any shape) gives a wave a run of samples of one
-//     channel;
+//     wherever H is a multiple of the channel group, any L) streams
+//     contiguous channel-group segments [b, g*HC .. g*HC+HC, :] with each
+//     wave owning one or two channels; dwconv_dk_mfma_kernel (every other
+//     shape) gives a wave a run of samples of one channel;
 //   * DK (dwconv_dk_kernel, PATHTILE_DK_ALGO=valu): a WAVE owns 64 samples of
 //     one channel; a 16-column strided LDS transpose (TileIO) feeds each lane
 //     its row pair and the lane accumulates every tap on the VALU;
@@ -969,10 +969,10 @@ __global__ __launch_bounds__(1024) void dwconv_dk_mfma_kernel(
 //   DX : dx[b,h,t] = sum_s dy[b,h,s] * w[h, t - s + p]
 // i.e. per channel a product of the [samples x L] rows with the banded
 // Toeplitz matrix of the taps. Workgroup (g, r) owns channel group g (one
-// channel per wave, kRowsCgWaves waves) and the interleaved 16-sample steps
+// channel per wave, HC = 8 or 16 waves) and the interleaved 16-sample steps
 // r, r + nranges, ...; per step it stages the group's contiguous segments
-// [b, g*HC .. g*HC+HC, :] through LDS (two input and two output stages, one
-// barrier per step) and each wave runs v_mfma_f32_16x16x4_f32 with M = 16
+// [b, g*HC .. g*HC+HC, :] through LDS (input and output stages, one or two
+// barriers per step) and each wave runs v_mfma_f32_16x16x4_f32 with M = 16
 // samples, N = 16 output columns, K = 4 input columns. K slot kk of MFMA step
 // u is input column u + (LMAX/4) * kk, so a lane reads its A operands as
 // LMAX/4 consecutive floats and its B operands (the taps) are loaded once.
