@@ -150,12 +150,22 @@ def test_odd_row_length_above_the_mall_full_size(rt, monkeypatch):
     assert torch.equal(g_mis[0], g_mis[1])
 
 
-@pytest.mark.parametrize("shape", [(12000, 128, 44, 48), (13800, 128, 38, 13)])
+def test_eight_channel_groups_above_the_mall(rt, monkeypatch):
+    """H % 16 != 0 on tensors above 256 MiB: the matrix-core FWD/dX in
+    8-channel workgroups with non-temporal loads, in both forms (L = 48 and
+    L = 37, where rows are not whole float4s)."""
+    _full_size_case(rt, 12288, 136, 48, 48, 81, monkeypatch)
+    _full_size_case(rt, 14000, 136, 37, 40, 82, monkeypatch)
+
+
+@pytest.mark.parametrize("shape", [(12000, 128, 44, 48), (13800, 128, 38, 13),
+                                   (14000, 130, 37, 48)])
 def test_dk_two_channels_per_wave_above_the_mall(shape):
     """Tensors just above 256 MiB with rows whose one-channel segments are
     not whole 64-byte units (L = 44, 38 at 128 threads): the channel-group dK
-    runs two channels per wave. Atomic and deterministic within 1e-4 of
-    FP64, deterministic bitwise reproducible, taps without overlap exact 0."""
+    runs two channels per wave; with H % 4 != 0 (H = 130, L = 37) it keeps
+    one channel per wave and stages dwords. Atomic and deterministic within
+    1e-4 of FP64, deterministic bitwise reproducible."""
     from pathtile_amd import runtime
 
     B, H, L, K = shape
