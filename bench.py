@@ -67,22 +67,29 @@ def parse_args(argv=None):
     p.add_argument("--path-warmup", type=int, default=50, help="warm-up launches per path and trial")
     p.add_argument("--path-runs", type=int, default=100, help="timed launches per path and trial")
     p.add_argument("--no-legs", action="store_true",
-                   help="skip the other BASELINE configurations (S, E2, E1)")
+                   help="skip the other BASELINE configurations (S, E2, E1) and, unless "
+                        "their counts are given, the MIOpen and S4ConvD comparisons")
     p.add_argument("--no-extras", action="store_true",
                    help="skip the BF16, channels-last, long-row and VALU-kernel legs")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-runs", type=int, default=10)
-    p.add_argument("--gpu-library-steps", type=int, default=0, metavar="N",
-                   help="also time N calls per path of PyTorch's GPU convolution (MIOpen) "
-                        "on the same tensors")
-    p.add_argument("--s4convd-steps", type=int, default=0, metavar="N",
-                   help="also time N S4ConvD training steps (the reference's Model() at "
-                        "B16384 L48, SGD lr 1e-3 momentum 0.9) on each backend")
+    p.add_argument("--gpu-library-steps", type=int, default=None, metavar="N",
+                   help="time N calls per path of PyTorch's GPU convolution (MIOpen) on "
+                        "the same tensors (default 3; 0 skips; off with --no-legs)")
+    p.add_argument("--s4convd-steps", type=int, default=None, metavar="N",
+                   help="time N S4ConvD training steps (the reference's Model() at "
+                        "B16384 L48, SGD lr 1e-3 momentum 0.9) on each backend "
+                        "(default 3; 0 skips; off with --no-legs)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="N",
                    help="after timing, run N plain device copies of x into y "
                         "(known bytes: 2 * B*H*L*4 per copy) to calibrate "
                         "rocprofv3 FETCH_SIZE / WRITE_SIZE")
-    return p.parse_args(argv)
+    a = p.parse_args(argv)
+    if a.gpu_library_steps is None:
+        a.gpu_library_steps = 0 if a.no_legs else 3
+    if a.s4convd_steps is None:
+        a.s4convd_steps = 0 if a.no_legs else 3
+    return a
 
 
 def log(msg: str) -> None:
@@ -350,6 +357,8 @@ def workload_leg(rt, name: str, args, dev, stream, keep: bool = False) -> dict:
            "sampled_rows": int(idx.numel()),
            "bars": "FWD/dX <= 1e-5, dK <= 1e-4 max-abs-scaled vs PyTorch FP64 on the GPU"},
     }
+    if not keep and args.gpu_library_steps:
+        leg["gpu_library_baseline"] = gpu_library_baseline(x, w, dy, args.gpu_library_steps)
     if keep:
         leg["_tensors"] = (x_cpu, w_cpu, dy_cpu, x, w, dy, y, dx, gk)
     else:
