@@ -158,6 +158,9 @@ def test_fwd_dx_bit_exact_and_fp64(rt, shape, algo, monkeypatch):
     (50, 8, 13, 9),       # 16 bucket
     (77, 24, 5, 7),       # L = 5: a row ends inside the first float4 of the next
     (20, 8, 1, 1),        # L = 1
+    (100, 8, 2, 5),       # L = 2, K > L
+    (33, 16, 3, 48),      # L = 3, K far above L
+    (64, 24, 7, 7),
 ])
 @pytest.mark.parametrize("channels", ["auto", "8", "16"])
 def test_fwd_dx_matrix_core_kernel(rt, shape, channels, monkeypatch):
@@ -370,6 +373,10 @@ def _misaligned(t):
     (300, 16, 29, 16),    # same, 32 bucket
     (500, 12, 30, 9),     # L % 4 == 2: whole chunks where the group is even
     (64, 96, 13, 5),      # 16 bucket, odd L
+    (100, 16, 1, 3),      # L = 1: one column per row
+    (70, 32, 2, 5),       # L = 2, K > L: taps without overlap
+    (33, 16, 3, 48),      # L = 3
+    (129, 64, 7, 7),
 ])
 @pytest.mark.parametrize("threads", [64, 128, 256, 512])
 def test_dk_channel_group_staging_widths(shape, threads):
