@@ -1,6 +1,6 @@
 """Summaries of rocprofv3 results (rocpd SQLite ``*_results.db``) as Markdown.
 
-Three reports, each written for one workload:
+Five reports, each written for one workload:
 
 ``trace``   kernel-trace statistics: calls and average/min/max duration per
             kernel, plus the launch geometry and resources of the largest
@@ -21,6 +21,11 @@ Three reports, each written for one workload:
             ``SQ_INSTS_VALU_MFMA_MOPS_F32`` / ``..._BF16`` (units of 512
             flops), beside its useful flops; ``--emit SUBSTR=KEY`` writes a
             ``KEY: flops`` line per kernel for bench.py.
+``lds``     LDS instructions per wave, LDS-busy fraction per CU, bank-conflict
+            share of the LDS cycles and the share of wave cycles waiting for
+            LDS, from ``SQ_INSTS_LDS`` / ``SQ_LDS_IDX_ACTIVE`` /
+            ``SQ_LDS_BANK_CONFLICT`` / ``SQ_WAIT_INST_LDS`` /
+            ``SQ_WAVE_CYCLES`` / ``GRBM_GUI_ACTIVE``.
 
 Only the dispatches with the largest grid of each kernel, and none below a
 quarter of its median duration or counter value, are kept, so the small
@@ -35,6 +40,7 @@ Usage::
         --useful-fma SUBSTR=N --clock-mhz F
     python -m pathtile_amd.profiling mfma    DB --command CMD --out FILE \
         --useful-fma SUBSTR=N --emit SUBSTR=KEY
+    python -m pathtile_amd.profiling lds     DB --command CMD --out FILE
 """
 
 from __future__ import annotations
@@ -49,6 +55,7 @@ PEAK_FP32_VECTOR = 78.6e12   # MI355X, non-packed FP32 FMA on the SIMDs
 PEAK_FP32_MATRIX = 157.3e12  # MI355X dense FP32 matrix cores
 # MI355X: 256 CUs x 4 SIMDs; a wave64 VALU op occupies its SIMD16 for 4 cycles.
 NUM_SIMDS = 1024
+NUM_CUS = 256
 CYCLES_PER_WAVE_VALU = 4
 NUM_XCD = 8
 
@@ -257,6 +264,43 @@ def mfma_report(db: str, command: str, useful_fma: dict[str, int], emit: dict[st
     return "\n".join(out + [""] + sorted(lines)) + "\n"
 
 
+def lds_report(db: str, command: str, match: str = "pt::") -> str:
+    """LDS load per kernel: instructions per wave, how busy the LDS of a CU
+    is, the share of its busy cycles lost to bank conflicts and the share of
+    wave cycles spent waiting for LDS results."""
+    counters = ("SQ_WAVES", "SQ_INSTS_LDS", "SQ_LDS_IDX_ACTIVE", "SQ_LDS_BANK_CONFLICT",
+                "SQ_WAIT_INST_LDS", "SQ_WAVE_CYCLES", "GRBM_GUI_ACTIVE")
+    per = {}
+    for c in counters:
+        rows = _largest_dispatches(
+            [r for r in counter_rows(db, c) if match in r["name"]], "grid", "value")
+        for r in rows:
+            per.setdefault(r["name"], {}).setdefault(c, []).append(r["value"])
+    out = ["Command:", "", "```", command, "```", "",
+           f"LDS-busy = SQ_LDS_IDX_ACTIVE / ({NUM_CUS} CUs x GRBM_GUI_ACTIVE / {NUM_XCD} XCDs): "
+           "the fraction of cycles a CU's LDS serves indexed reads and writes. "
+           "Conflict share = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE: the part of those "
+           "cycles spent replaying bank conflicts. LDS wait = SQ_WAIT_INST_LDS / "
+           "SQ_WAVE_CYCLES: the fraction of a wave's life spent waiting for LDS results.", "",
+           "| kernel | dispatches | waves | LDS insts / wave | LDS-busy | conflict share | LDS wait |",
+           "|---|---|---|---|---|---|---|"]
+    for name, cs in per.items():
+        if not all(c in cs for c in counters):
+            continue
+        m = {c: statistics.mean(v) for c, v in cs.items()}
+        if m["SQ_INSTS_LDS"] == 0:
+            continue
+        gui = m["GRBM_GUI_ACTIVE"] / NUM_XCD
+        busy = m["SQ_LDS_IDX_ACTIVE"] / (NUM_CUS * gui)
+        conflict = m["SQ_LDS_BANK_CONFLICT"] / max(m["SQ_LDS_IDX_ACTIVE"], 1)
+        wait = m["SQ_WAIT_INST_LDS"] / max(m["SQ_WAVE_CYCLES"], 1)
+        n = len(cs["SQ_INSTS_LDS"])
+        out.append(f"| `{short_name(name)}` | {n} | {m['SQ_WAVES']:.0f} | "
+                   f"{m['SQ_INSTS_LDS'] / max(m['SQ_WAVES'], 1):.0f} | {busy:.3f} | "
+                   f"{conflict:.3f} | {wait:.3f} |")
+    return "\n".join(out) + "\n"
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(prog="python -m pathtile_amd.profiling")
     sub = p.add_subparsers(dest="cmd", required=True)
@@ -291,6 +335,11 @@ def main(argv=None) -> int:
                    help="KERNEL_SUBSTR=KEY: write 'KEY: flops' for that kernel (repeatable)")
     m.add_argument("--title", default="Issued matrix flops")
     m.add_argument("--out", required=True)
+    d = sub.add_parser("lds")
+    d.add_argument("db")
+    d.add_argument("--command", required=True)
+    d.add_argument("--title", default="LDS load")
+    d.add_argument("--out", required=True)
     a = p.parse_args(argv)
 
     def pairs(items, conv):
@@ -308,6 +357,8 @@ def main(argv=None) -> int:
     elif a.cmd == "valu":
         text = f"# {a.title}\n\n" + valu_report(a.db, a.command, pairs(a.useful_fma, int),
                                                 a.clock_mhz)
+    elif a.cmd == "lds":
+        text = f"# {a.title}\n\n" + lds_report(a.db, a.command)
     else:
         text = f"# {a.title}\n\n" + mfma_report(a.db, a.command, pairs(a.useful_fma, int),
                                                 pairs(a.emit, str))
