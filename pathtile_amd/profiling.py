@@ -1,6 +1,6 @@
 """Summaries of rocprofv3 results (rocpd SQLite ``*_results.db``) as Markdown.
 
-Five reports, each written for one workload:
+Six reports, each written for one workload:
 
 ``trace``   kernel-trace statistics: calls and average/min/max duration per
             kernel, plus the launch geometry and resources of the largest
@@ -21,6 +21,9 @@ Five reports, each written for one workload:
             ``SQ_INSTS_VALU_MFMA_MOPS_F32`` / ``..._BF16`` (units of 512
             flops), beside its useful flops; ``--emit SUBSTR=KEY`` writes a
             ``KEY: flops`` line per kernel for bench.py.
+``mix``     VALU instruction mix from the ``SQ_INSTS_VALU_*`` class counters:
+            each class's share of ``SQ_INSTS_VALU`` and the FP32 fraction
+            (FMA + add + multiply in FP32).
 ``lds``     LDS instructions per wave, LDS-busy fraction per CU, bank-conflict
             share of the LDS cycles and the share of wave cycles waiting for
             LDS, from ``SQ_INSTS_LDS`` / ``SQ_LDS_IDX_ACTIVE`` /
@@ -40,6 +43,7 @@ Usage::
         --useful-fma SUBSTR=N --clock-mhz F
     python -m pathtile_amd.profiling mfma    DB --command CMD --out FILE \
         --useful-fma SUBSTR=N --emit SUBSTR=KEY
+    python -m pathtile_amd.profiling mix     DB --command CMD --out FILE
     python -m pathtile_amd.profiling lds     DB --command CMD --out FILE
 """
 
@@ -264,6 +268,44 @@ def mfma_report(db: str, command: str, useful_fma: dict[str, int], emit: dict[st
     return "\n".join(out + [""] + sorted(lines)) + "\n"
 
 
+MIX_COUNTERS = ("SQ_INSTS_VALU", "SQ_INSTS_VALU_FMA_F32", "SQ_INSTS_VALU_ADD_F32",
+                "SQ_INSTS_VALU_MUL_F32", "SQ_INSTS_VALU_INT32", "SQ_INSTS_VALU_CVT",
+                "SQ_INSTS_VALU_MFMA_F32", "SQ_INSTS_VALU_MFMA_BF16")
+
+
+def mix_report(db: str, command: str, match: str = "pt::") -> str:
+    """VALU instruction mix per kernel: each class as a share of all VALU
+    instructions, and the FP32 fraction (FMA + add + multiply in FP32)."""
+    per = {}
+    for c in MIX_COUNTERS:
+        rows = _largest_dispatches(
+            [r for r in counter_rows(db, c) if match in r["name"]], "grid", "value")
+        for r in rows:
+            per.setdefault(r["name"], {}).setdefault(c, []).append(r["value"])
+    out = ["Command:", "", "```", command, "```", "",
+           "Wave-level instruction counts per dispatch (mean over the dispatches with each "
+           "kernel's largest grid), each as a share of SQ_INSTS_VALU. FP32 fraction = "
+           "(FMA_F32 + ADD_F32 + MUL_F32) / VALU; MFMA = MFMA_F32 + MFMA_BF16 instructions.", "",
+           "| kernel | dispatches | VALU insts | FP32 fraction | FMA_F32 | ADD_F32 | MUL_F32 | INT32 | CVT | MFMA |",
+           "|---|---|---|---|---|---|---|---|---|---|"]
+    for name, cs in per.items():
+        if not all(c in cs for c in MIX_COUNTERS):
+            continue
+        m = {c: statistics.mean(v) for c, v in cs.items()}
+        tot = m["SQ_INSTS_VALU"]
+        if tot == 0:
+            continue
+        sh = {c: m[c] / tot for c in MIX_COUNTERS[1:]}
+        fp32 = sh["SQ_INSTS_VALU_FMA_F32"] + sh["SQ_INSTS_VALU_ADD_F32"] + sh["SQ_INSTS_VALU_MUL_F32"]
+        mfma = sh["SQ_INSTS_VALU_MFMA_F32"] + sh["SQ_INSTS_VALU_MFMA_BF16"]
+        n = len(cs["SQ_INSTS_VALU"])
+        out.append(f"| `{short_name(name)}` | {n} | {tot:.0f} | {fp32:.3f} | "
+                   f"{sh['SQ_INSTS_VALU_FMA_F32']:.3f} | {sh['SQ_INSTS_VALU_ADD_F32']:.3f} | "
+                   f"{sh['SQ_INSTS_VALU_MUL_F32']:.3f} | {sh['SQ_INSTS_VALU_INT32']:.3f} | "
+                   f"{sh['SQ_INSTS_VALU_CVT']:.3f} | {mfma:.3f} |")
+    return "\n".join(out) + "\n"
+
+
 def lds_report(db: str, command: str, match: str = "pt::") -> str:
     """LDS load per kernel: instructions per wave, how busy the LDS of a CU
     is, the share of its busy cycles lost to bank conflicts and the share of
@@ -335,6 +377,11 @@ def main(argv=None) -> int:
                    help="KERNEL_SUBSTR=KEY: write 'KEY: flops' for that kernel (repeatable)")
     m.add_argument("--title", default="Issued matrix flops")
     m.add_argument("--out", required=True)
+    x = sub.add_parser("mix")
+    x.add_argument("db")
+    x.add_argument("--command", required=True)
+    x.add_argument("--title", default="VALU instruction mix")
+    x.add_argument("--out", required=True)
     d = sub.add_parser("lds")
     d.add_argument("db")
     d.add_argument("--command", required=True)
@@ -357,6 +404,8 @@ def main(argv=None) -> int:
     elif a.cmd == "valu":
         text = f"# {a.title}\n\n" + valu_report(a.db, a.command, pairs(a.useful_fma, int),
                                                 a.clock_mhz)
+    elif a.cmd == "mix":
+        text = f"# {a.title}\n\n" + mix_report(a.db, a.command)
     elif a.cmd == "lds":
         text = f"# {a.title}\n\n" + lds_report(a.db, a.command)
     else:

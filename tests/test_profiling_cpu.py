@@ -89,3 +89,14 @@ def test_trace_report_drops_gate_dispatches(tmp_path):
     text = profiling.trace_report(_db(tmp_path / "t.db", kernels=k), "cmd")
     r = _row(text, "pt::dwconv_rows_cg_kernel<48, false, 2, 16>")
     assert r[1:3] == ["2", "132.00"]
+
+
+def test_mix_report(tmp_path):
+    vals = {"SQ_INSTS_VALU": 1000, "SQ_INSTS_VALU_FMA_F32": 400, "SQ_INSTS_VALU_ADD_F32": 100,
+            "SQ_INSTS_VALU_MUL_F32": 50, "SQ_INSTS_VALU_INT32": 200, "SQ_INSTS_VALU_CVT": 10,
+            "SQ_INSTS_VALU_MFMA_F32": 90, "SQ_INSTS_VALU_MFMA_BF16": 30}
+    rows = [(K_MAIN, d, 4096, c, v) for d in range(2) for c, v in vals.items()]
+    rows += [(K_MAIN, 5, 64, c, 1.0) for c in vals]
+    text = profiling.mix_report(_db(tmp_path / "m.db", rows), "cmd")
+    r = _row(text, "pt::dwconv_rows_cg_kernel<48, false, 2, 16>")
+    assert r[1:] == ["2", "1000", "0.550", "0.400", "0.100", "0.050", "0.200", "0.010", "0.120"]
