@@ -538,23 +538,32 @@ static RowsAlgo rows_algo(int B, int H, int L, int K) {
 // Launch of the channel-group kernel: one workgroup per (channel group,
 // sample range), the ranges interleaved in 16-sample steps. As many ranges as
 // fill the CUs with min(max_per_cu, resident) workgroups each (two 8-channel
-// workgroups measured best where the LDS allows them, L <= 32; one above),
+// workgroups measured best where the LDS allows them, L <= 39; one above),
 // rounded down: a grid a few workgroups past one round runs those few in a
 // second round and nearly doubles the time (B16384 H160 L48 K48, 10
 // channel groups: 26 ranges, 260 workgroups on 256 CUs, 276 us; 25 ranges
 // fit one round).
+// min_steps: fewer workgroups per CU while a workgroup would get fewer than
+// this many steps (0: off). Two 8-channel FP32 workgroups per CU won from
+// 4 steps each (B2048 H128 L24 K24 10.6 against 11.0 us, B4096 H96 L33 K40
+// 26.5 against 28.9, B16384 H64 L35 K16 53.2 against 64.5), tied at 2 and
+// lost below (E1 B1000 H96 L37 K48, 1.5 steps: 12.1 against 10.8; B1000
+// H96 L36 K48 11.4 against 9.3; B2048 H64 L36 K48, 2 steps: 11.7 against
+// 11.1), where one per CU runs each workgroup's steps back to back with no
+// second workgroup competing for the CU.
 // hc: channels (= waves) per workgroup; lds: dynamic LDS per workgroup;
 // max_per_cu: workgroups per CU the range count is sized for (at most what
 // fits).
 template <typename T, typename Fn>
 static int rows_cg_launch(Fn fn, const T* in, const float* w, T* out, int B,
                           int H, int L, int K, void* stream, int hc,
-                          size_t lds, int max_per_cu) {
+                          size_t lds, int max_per_cu, int min_steps = 0) {
   const int threads = hc * kWave;
   int per_cu = blocks_per_cu((const void*)fn, threads, lds);
   if (per_cu > max_per_cu) per_cu = max_per_cu;
   const long long ngroups = (long long)H / hc;
   const long long tsteps = ((long long)B + kRowsCgStep - 1) / kRowsCgStep;
+  while (per_cu > 1 && tsteps < (long long)min_steps * (num_cus() * per_cu / ngroups)) --per_cu;
   long long nr = (long long)num_cus() * per_cu / ngroups;
   if (nr > tsteps) nr = tsteps;
   if (nr < 1) nr = 1;
@@ -588,6 +597,10 @@ static int rows_cg_launch(Fn fn, const T* in, const float* w, T* out, int B,
 // PATHTILE_ROWS_CHANNELS=8 or =16 forces the channel count where the layout
 // allows it (16: rows of 33-48 columns, H % 16 == 0); the library reads the
 // variable on every call.
+// Steps per workgroup below which the 8-channel FP32 kernel runs one
+// workgroup per CU (rows_cg_launch).
+constexpr int kRowsCgMinSteps = 3;
+
 static int rows_cg_channels_env() {
   const char* env = getenv("PATHTILE_ROWS_CHANNELS");
   if (env && strcmp(env, "8") == 0) return 8;
@@ -613,7 +626,7 @@ static int rows_cg_path(bool dx, const float* in, const float* w, float* out,
   const RowsCgFn(*t8)[3] = a4 ? (plain ? kRowsCgTablePL : kRowsCgTable)
                               : (plain ? kRowsCgTableUPL : kRowsCgTableU);
   return rows_cg_launch(t8[dx ? 1 : 0][mfma_index(L)], in, w, out, B, H, L, K,
-                        stream, kRowsCgWaves, rows_cg_lds_bytes(L), 2);
+                        stream, kRowsCgWaves, rows_cg_lds_bytes(L), 2, kRowsCgMinSteps);
 }
 
 static long long gcd_ll(long long a, long long b) {

@@ -1177,12 +1177,16 @@ __global__ __launch_bounds__(HC * kWave) void dwconv_rows_cg_kernel(
         for (int u = 0; u < NU; ++u) a[u] = u + NU * kk < L ? a[u] : 0.0f;
       }
     } else {
-      // Columns >= L read the row's first element and are zeroed.
+      // Columns >= L are read where they lie (the next channel's row, or
+      // past the input stage into the next stage of the allocation, which
+      // always follows: at most LMAX - L - 5 floats past a stage) and
+      // zeroed. Reading in place keeps one base address for the whole row:
+      // a per-column clamped address cost 21 VGPRs (129 against 108), which
+      // held the 8-channel kernel to one workgroup per CU.
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
-        const bool in = u + NU * kk < L;
-        const float v = row[in ? u + NU * kk : 0];
-        a[u] = in ? v : 0.0f;
+        const float v = src[u];
+        a[u] = u + NU * kk < L ? v : 0.0f;
       }
     }
     // The MFMA computes the transposed tile (taps as A, rows as B; each lane
