@@ -222,21 +222,20 @@ def time_paths(fns: dict, stream, trials: int, warmup: int, runs: int) -> dict:
 
 def rows_kernel_name(B: int, H: int, L: int, K: int, dx: bool) -> str:
     """The FWD/DX kernel the library picks for 16-byte aligned rows: the
-    channel-group matrix-core kernel where the layout allows it (H % 8 == 0)
-    and a row needs >= 10.5 (LMAX / L)^2 useful FMAs per output
-    (LMAX = 16 ceil(L / 16)), else the VALU rows kernel (or either on
-    request through PATHTILE_ROWS_ALGO)."""
+    channel-group matrix-core kernel where pathtile_amd.rows_rule says the
+    matrix cores serve, else the VALU rows kernel (or either on request
+    through PATHTILE_ROWS_ALGO)."""
+    from pathtile_amd import rows_rule
+
     tag = "DX" if dx else "FWD"
     algo = os.environ.get("PATHTILE_ROWS_ALGO")
-    p = K // 2
-    useful = sum(max(0, min(L, L - (j - p)) - max(0, p - j)) for j in range(K))
-    lmax = 16 * ((L + 15) // 16)
-    if L % 4 == 0:
-        fast = 2 * useful * L >= 21 * lmax * lmax
-    else:  # rows of L % 4 != 0: every call of >= 2^18 rows, else >= 5 (LMAX / L)^2
-        fast = B * H >= (1 << 18) or 2 * useful * L >= 10 * lmax * lmax
-    mfma = algo == "mfma" or (algo != "valu" and fast)
-    if mfma and H % 8 == 0:
+    if algo == "mfma":
+        mfma = H % 8 == 0
+    elif algo in ("valu", "tile", "stream"):
+        mfma = False
+    else:
+        mfma = rows_rule.matrix_cores_serve(B, H, L, K)
+    if mfma:
         return f"dwconv_rows_cg_kernel<{tag}>"
     return f"dwconv_rows_kernel<{tag}>"
 

@@ -80,7 +80,10 @@ const char* pt_status_string(int status);
  * workgroup holds a 64-row LDS tile per wave, so 16 waves fit only rows up
  * to 32 (PT_ERR_CONFIG for longer rows on this kernel). Where a row needs at
  * least 10.5 (LMAX / L)^2 useful FMAs per output on average (LMAX =
- * 16 ceil(L / 16)) and the layout allows it (H % 8 == 0, x and y 16-byte
+ * 16 ceil(L / 16); on tensors of at most 256 MiB, rows of 16 columns from
+ * 9.5 x 16 useful FMAs per row and rows of 20-28 from 12.5 L) and the
+ * layout allows it
+ * (H % 8 == 0, x and y 16-byte
  * aligned; any L), the channel-group matrix-core kernel runs instead:
  * 8 waves (channels) per workgroup, or 16 for rows of 33-48 columns when
  * H % 16 == 0 and the call is large (tensors above 256 MiB or at least 24

@@ -478,7 +478,8 @@ static int rows_waves_per_cu(int L, int K, long long ntiles) {
 // average (LMAX = the row bucket 16, 32 or 48: rows that fill their bucket
 // partly pay for the matrix work they waste); below that the VALU kernel
 // (bit-exact with the reference's fmaf chain) is as fast or faster. Rows of
-// other lengths: kRowsOddMfmaRows below.
+// other lengths: kRowsOddMfmaRows below. Rows of 16-28 columns on tensors
+// of at most 256 MiB: rows_small_plain_mfma below.
 // Where the VALU serves, the tile kernel (a lane per row through an LDS
 // transpose) runs, or the streaming kernel (float4 lanes, no LDS; rows of
 // L % 4 == 0 floats, at most 9 taps) where the channel period would idle
@@ -521,6 +522,27 @@ static bool rows_cg_ok(int H, int L, const void* in, const void* out) {
 // matrix cores 0.89x at K = 12; B2048 H64 L45 likewise).
 constexpr long long kRowsOddMfmaRows = 1LL << 18;
 
+// Rows of L % 4 == 0 on tensors that take plain loads (at most 256 MiB),
+// in the 16-column bucket or filling the 32-column bucket partly (L = 20,
+// 24, 28): the matrix cores from 9.5 x 16 useful FMAs per row (L = 16) and
+// from 12.5 L (L = 20-28). Both admit every row the general rule admits;
+// its (LMAX / L)^2 = 1.78 at L = 24 (2.56 at L = 20) overcharges the
+// half-empty bucket, whose unused columns cost the matrix cores little at
+// these sizes. Measured on MI355X (FWD, three interleaved rounds,
+// matrix-core time / VALU time) at B1024 H96 to B16384 H128 and B4096 H256:
+// L24 K16 0.89-0.99 at all sizes, L24 K20 0.87-1.02, L24 K24 0.69-0.92,
+// L20 K16 0.84-0.91, L20 K24 0.67-0.94, L16 K12 0.92-1.05. The rows left
+// out were mixed: L24 K12 0.92-1.26 and L20 K12 0.85-1.17 (the small calls
+// lose), L16 K10 0.96-1.05. L = 32 keeps the general rule: there the
+// sizes disagreed (K12 0.78 at B2048 H128, 0.90 at B4096 H128, 0.99-1.12
+// elsewhere). Above 256 MiB the general rule stays too: there the VALU
+// kernel won L = 24 at every K tried (B32768 H256 L24 K6-24: the matrix
+// cores took 1.02-1.12x its time).
+static bool rows_small_plain_mfma(int L, long long useful) {
+  if (L == 16) return 2 * useful >= 19 * 16;        // useful >= 9.5 x 16
+  return 2 * useful >= 25LL * L;                    // L = 20, 24, 28
+}
+
 static RowsAlgo rows_algo(int B, int H, int L, int K) {
   const char* env = getenv("PATHTILE_ROWS_ALGO");
   if (env && strcmp(env, "valu") == 0) return kRowsValu;
@@ -529,8 +551,12 @@ static RowsAlgo rows_algo(int B, int H, int L, int K) {
   if (env && strcmp(env, "mfma") == 0) return kRowsMfma;
   const long long lmax = 16LL * (mfma_index(L) + 1);
   const long long u2l = 2 * useful_fma_per_row(L, K) * L;
-  // useful / L >= 10.5 (lmax / L)^2, in integers
-  if (L % 4 == 0) return u2l >= 21 * lmax * lmax ? kRowsMfma : kRowsValu;
+  if (L % 4 == 0) {
+    if (L >= 16 && L < 32 && rows_plain_loads(B, H, L))
+      return rows_small_plain_mfma(L, useful_fma_per_row(L, K)) ? kRowsMfma : kRowsValu;
+    // useful / L >= 10.5 (lmax / L)^2, in integers
+    return u2l >= 21 * lmax * lmax ? kRowsMfma : kRowsValu;
+  }
   if ((long long)B * H >= kRowsOddMfmaRows) return kRowsMfma;
   return u2l >= 10 * lmax * lmax ? kRowsMfma : kRowsValu;
 }

@@ -1,0 +1,47 @@
+"""Which FWD/dX kernel the library runs for a 16-byte aligned call, as a
+host-side predicate (the rule itself is rows_algo in csrc/dwconv1d_abi.hip;
+this restates it for the bench's kernel names, the tuner's knob-inert flag
+and the tests that pick their tolerance by kernel).
+
+The channel-group matrix-core kernel serves when H % 8 == 0 and:
+  * L % 4 == 0 on tensors of at most 256 MiB: for L = 16 at least
+    9.5 x 16 useful FMAs per row, for L = 20, 24, 28 at least 12.5 L;
+  * L % 4 == 0 otherwise: at least 10.5 (LMAX / L)^2 useful FMAs per output;
+  * L % 4 != 0: every call of at least 2^18 rows (B * H), smaller ones from
+    5 (LMAX / L)^2 useful FMAs per output;
+with LMAX = 16 ceil(L / 16). The VALU kernels serve every other call.
+"""
+
+from __future__ import annotations
+
+PLAIN_LOAD_BYTES = 256 * 2**20
+ODD_MFMA_ROWS = 1 << 18
+
+
+def useful_fma_per_row(L: int, K: int) -> int:
+    """Multiply-adds of one row that touch a real element (zero padding,
+    p = K // 2)."""
+    p = K // 2
+    return sum(max(0, min(L, L - (j - p)) - max(0, p - j)) for j in range(K))
+
+
+def plain_loads(B: int, H: int, L: int) -> bool:
+    """FP32 FWD/dX input loads are plain (cached) up to 256 MiB."""
+    return 4 * B * H * L <= PLAIN_LOAD_BYTES
+
+
+def matrix_cores_serve(B: int, H: int, L: int, K: int) -> bool:
+    """The library's default FWD/dX kernel choice for 16-byte aligned
+    tensors (PATHTILE_ROWS_ALGO unset)."""
+    B, H, L, K = int(B), int(H), int(L), int(K)
+    if H % 8:
+        return False
+    lmax = 16 * ((L + 15) // 16)
+    useful = useful_fma_per_row(L, K)
+    if L % 4 == 0:
+        if plain_loads(B, H, L) and L == 16:
+            return 2 * useful >= 19 * 16
+        if plain_loads(B, H, L) and 16 < L < 32:
+            return 2 * useful >= 25 * L
+        return 2 * useful * L >= 21 * lmax * lmax
+    return B * H >= ODD_MFMA_ROWS or 2 * useful * L >= 10 * lmax * lmax

@@ -20,6 +20,8 @@ import math
 from datetime import datetime
 from typing import Iterable
 
+from .. import rows_rule
+
 PHASES = ("fwd", "bwd_input", "bwd_weight")
 POLICY_KEYS = {
     "fwd": "fwd_waves_per_block",
@@ -195,31 +197,19 @@ def verify_frozen_before_holdout(policy: dict, holdout_created_at: Iterable[str]
 # --------------------------------------------------------------------------
 KNOB_INERT_RULE = (
     "FWD/dX waves per workgroup cannot change the kernel where the matrix-core "
-    "FWD/dX kernel serves (H % 8 == 0 and >= 10.5 (LMAX / L)^2 useful FMAs per "
-    "output, LMAX = 16 ceil(L / 16); for L % 4 != 0 every call of >= 2^18 rows "
-    "and smaller ones from 5 (LMAX / L)^2): it always runs 8- or 16-wave "
-    "workgroups. There the FWD/dX candidates differ only by measurement noise.")
-
-
-def _useful_fma_per_row(L: int, K: int) -> int:
-    p = K // 2
-    return sum(max(0, min(L, L - (j - p)) - max(0, p - j)) for j in range(K))
+    "FWD/dX kernel serves (H % 8 == 0 and, for L % 4 == 0 on tensors of at most "
+    "256 MiB, >= 9.5 x 16 useful FMAs per row at L = 16 and >= 12.5 L at L = 20-28, "
+    ">= 10.5 (LMAX / L)^2 useful FMAs per output otherwise, LMAX = 16 ceil(L / 16); "
+    "for L % 4 != 0 every call of >= 2^18 rows and smaller ones from 5 (LMAX / L)^2): "
+    "it always runs 8- or 16-wave workgroups. There the FWD/dX candidates differ "
+    "only by measurement noise.")
 
 
 def fwd_dx_knob_inert(H: int, L: int, K: int, B: int) -> bool:
-    """True where the FWD/dX knob cannot change the kernel (the library's
-    matrix-core rule for 16-byte aligned tensors, as the tuner allocates):
-    H % 8 == 0 and >= 10.5 (LMAX / L)^2 useful FMAs per output; for
-    L % 4 != 0, every call of at least 2^18 rows (B * H) and smaller ones
-    from 5 (LMAX / L)^2."""
-    H, L, K, B = int(H), int(L), int(K), int(B)
-    lmax = 16 * ((L + 15) // 16)
-    u2l = 2 * _useful_fma_per_row(L, K) * L
-    if L % 4 == 0:
-        fast = u2l >= 21 * lmax * lmax
-    else:
-        fast = B * H >= (1 << 18) or u2l >= 10 * lmax * lmax
-    return H % 8 == 0 and fast
+    """True where the FWD/dX knob cannot change the kernel: where the
+    library's matrix-core rule serves a 16-byte aligned call (the tuner's
+    tensors are torch allocations), pathtile_amd.rows_rule."""
+    return rows_rule.matrix_cores_serve(B, H, L, K)
 
 
 def path_regret(rows: list[dict], policy: dict[str, int]) -> dict[str, dict]:

@@ -32,6 +32,7 @@ import pytest
 import torch
 
 import oracle
+from pathtile_amd import rows_rule
 
 pytestmark = pytest.mark.gpu
 
@@ -49,18 +50,9 @@ def rt():
 
 
 def _valu_serves(B, H, L, K):
-    """The library's FWD/DX rule for 16-byte aligned tensors: the matrix
-    cores when H % 8 == 0 and a row needs >= 10.5 (LMAX / L)^2 useful FMAs
-    per output (LMAX = 16 ceil(L / 16)); for L % 4 != 0 every call of at
-    least 2^18 rows (B * H) and smaller ones from 5 (LMAX / L)^2; the VALU
-    kernel otherwise."""
-    lmax = 16 * ((L + 15) // 16)
-    u2l = 2 * oracle.useful_fma_per_row(L, K) * L
-    if L % 4 == 0:
-        fast = u2l >= 21 * lmax * lmax
-    else:
-        fast = B * H >= (1 << 18) or u2l >= 10 * lmax * lmax
-    return not (H % 8 == 0 and fast)
+    """The VALU kernel serves a 16-byte aligned call wherever the library's
+    rule does not pick the matrix cores (pathtile_amd.rows_rule)."""
+    return not rows_rule.matrix_cores_serve(B, H, L, K)
 
 
 def _full_size_case(rt, B, H, L, K, seed, monkeypatch):

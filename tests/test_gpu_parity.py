@@ -23,6 +23,7 @@ import pytest
 import torch
 
 import oracle
+from pathtile_amd import rows_rule
 
 pytestmark = pytest.mark.gpu
 
@@ -97,18 +98,12 @@ SHAPES = [
 def _mfma_serves(B, H, L, K, algo):
     """Whether the channel-group matrix-core FWD/DX kernel serves a 16-byte
     aligned call: the layout must allow it (H % 8 == 0, any L) and, unless
-    forced, the row must need >= 10.5 (LMAX / L)^2 useful FMAs per output
-    (LMAX = 16 ceil(L / 16)); for L % 4 != 0, every call of at least 2^18
-    rows (B * H) and smaller ones from 5 (LMAX / L)^2."""
+    forced, the library's rule must pick it (pathtile_amd.rows_rule)."""
     if algo in ("valu", "tile", "stream") or H % 8:
         return False
     if algo == "mfma":
         return True
-    lmax = 16 * ((L + 15) // 16)
-    u2l = 2 * oracle.useful_fma_per_row(L, K) * L
-    if L % 4 == 0:
-        return u2l >= 21 * lmax * lmax
-    return B * H >= (1 << 18) or u2l >= 10 * lmax * lmax
+    return rows_rule.matrix_cores_serve(B, H, L, K)
 
 
 @pytest.mark.parametrize("algo", ["auto", "valu", "tile", "stream", "mfma"])

@@ -5,6 +5,7 @@ from __future__ import annotations
 
 import pytest
 
+from pathtile_amd import rows_rule
 from pathtile_amd.tune import select, shapes
 
 
@@ -215,12 +216,30 @@ def test_fwd_dx_knob_inert_follows_the_library_rule():
     assert not select.fwd_dx_knob_inert(96, 37, 8, 1000)      # short chain, small call: VALU
     assert select.fwd_dx_knob_inert(96, 37, 8, 4096)          # L % 4 != 0 from 2^18 rows: matrix cores
     assert not select.fwd_dx_knob_inert(12, 48, 48, 16384)    # H % 8 != 0
+    # rows of 16 and 20-28 columns on tensors of at most 256 MiB: 9.5 x 16
+    # useful FMAs per row at L = 16, 12.5 L at L = 20-28 (L24 K16: 320 >= 300);
+    # above 256 MiB the general rule (320 * 24 * 2 < 21 * 32 * 32)
+    assert select.fwd_dx_knob_inert(128, 24, 16, 16384)       # 201 MB
+    assert not select.fwd_dx_knob_inert(256, 24, 16, 32768)   # 805 MB
+    assert not select.fwd_dx_knob_inert(128, 24, 14, 16384)   # 287 < 300
+    assert select.fwd_dx_knob_inert(128, 20, 16, 16384)       # 256 >= 250
+    assert not select.fwd_dx_knob_inert(128, 20, 12, 16384)   # 204 < 250
+    assert select.fwd_dx_knob_inert(128, 16, 12, 16384)       # 156 >= 152
+    assert not select.fwd_dx_knob_inert(128, 16, 10, 16384)   # 135 < 152
+    assert not select.fwd_dx_knob_inert(128, 32, 11, 8192)    # L = 32: general rule (10.06 < 10.5)
+    assert select.fwd_dx_knob_inert(128, 32, 12, 8192)        # 10.9 >= 10.5
+    assert not select.fwd_dx_knob_inert(128, 40, 16, 16384)   # 48-column bucket: general rule
     # the useful-FMA threshold against a brute-force count: L = 40 (LMAX 48)
     L, K = 40, 32
     p = K // 2
     useful = sum(1 for t in range(L) for j in range(K) if 0 <= t + j - p < L)
-    assert select._useful_fma_per_row(L, K) == useful
+    assert rows_rule.useful_fma_per_row(L, K) == useful
     assert select.fwd_dx_knob_inert(64, L, K, 2048) == (2 * useful * L >= 21 * 48 * 48)
+    # and in the 32-column bucket: L = 24 (plain loads at B2048 H64)
+    L, K = 24, 20
+    useful = sum(1 for t in range(L) for j in range(K) if 0 <= t + j - K // 2 < L)
+    assert rows_rule.useful_fma_per_row(L, K) == useful
+    assert select.fwd_dx_knob_inert(64, L, K, 2048) == (2 * useful >= 25 * L)
 
 
 def test_per_path_and_active_knob_regret():
