@@ -92,6 +92,13 @@ SHAPES = [
     (64, 128, 48, 48),
     (8000, 64, 48, 48),   # several tiles per wave, ragged last chunk group
     (8000, 64, 37, 8),    # same, dword row path
+    # rows of 16 and 20-28 columns below 256 MiB: the matrix cores from
+    # 9.5 x 16 (L = 16) and 12.5 L (L = 20-28) useful FMAs per row
+    (64, 32, 24, 16),     # 320 >= 300: matrix cores
+    (40, 8, 24, 14),      # 287 < 300: VALU, bit-exact
+    (50, 16, 20, 24),     # 336 >= 250: matrix cores
+    (33, 8, 16, 12),      # 156 >= 152: matrix cores
+    (33, 8, 16, 10),      # 135 < 152: VALU, bit-exact
 ]
 
 
