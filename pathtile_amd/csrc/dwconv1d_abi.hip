@@ -610,7 +610,8 @@ static int rows_cg_launch(Fn fn, const T* in, const float* w, T* out, int B,
 //    the kernel itself 3-6% faster there (P: 133.7 against 142.4 us FWD;
 //    B16384 H96 L37 K48 92.2 against 95.9 us);
 //  * otherwise 8, two per CU where the LDS allows (two input and two output
-//    stages). Measured on MI355X at 1, 2, 4 and 8 channels, 8 was fastest
+//    stages) and each workgroup gets at least kRowsCgMinSteps steps, else
+//    one (rows_cg_launch). Measured on MI355X at 1, 2, 4 and 8 channels, 8 was fastest
 //    (at P: 227, 171, 156, 140 us). On tensors of at most 256 MiB (plain
 //    loads) with fewer steps per CU the 16-channel grid gives the CUs
 //    uneven step counts and fewer steps to overlap, and 8 channels measured

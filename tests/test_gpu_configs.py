@@ -25,8 +25,6 @@ own validation shapes, and on every tuner candidate (marked ``gpu``).
 
 from __future__ import annotations
 
-import math
-
 import numpy as np
 import pytest
 import torch
