@@ -165,3 +165,41 @@ def test_bf16_autograd(rt):
     _check_rounded(y.detach(), oracle.fwd_f64(x.float(), w))
     _check_rounded(gx, oracle.dx_f64(dy.float(), w))
     assert oracle.normalized_max_abs(gk.cpu().numpy(), oracle.dk_f64(dy.float(), x.float(), K)) < DK_TOL
+
+
+def _random_bf16_shapes(n: int, seed: int):
+    """Seeded shapes inside the BF16 path's layout (H % 8 == 0, L % 4 == 0)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        B = int(rng.choice([1, 15, 16, 17, 64, 129, 300, 700]))
+        H = int(8 * rng.integers(1, 9))
+        L = int(4 * rng.integers(1, 13))
+        K = int(rng.integers(1, 49) if i % 2 else rng.integers(24, 49))
+        out.append((B, H, L, K))
+    return out
+
+
+@pytest.mark.parametrize("shape", _random_bf16_shapes(24, 20261203), ids=lambda s: "B{}H{}L{}K{}".format(*s))
+def test_bf16_random_shapes(rt, shape):
+    """FWD/dX within one BF16 rounding of FP64, atomic and deterministic dK
+    within 1e-4 of FP64 with a bitwise repeat, on seeded random shapes."""
+    B, H, L, K = shape
+    x, w, dy = _inputs(B, H, L, K, seed=9700 + B + 3 * H + 5 * L + 7 * K)
+    xd, wd, dyd = x.cuda(), w.cuda(), dy.cuda()
+    y = torch.empty_like(xd)
+    dx = torch.empty_like(dyd)
+    rt.launch_fwd_bf16(xd, wd, y)
+    rt.launch_bwd_input_bf16(dyd, wd, dx)
+    _check_rounded(y, oracle.fwd_f64(x.float(), w))
+    _check_rounded(dx, oracle.dx_f64(dy.float(), w))
+    ref = oracle.dk_f64(dy.float(), x.float(), K)
+    ga = torch.full((H, K), float("nan"), device="cuda")
+    rt.launch_bwd_weight_bf16(dyd, xd, ga, K, zero_first=True)
+    g1 = torch.full((H, K), float("nan"), device="cuda")
+    g2 = torch.full((H, K), float("nan"), device="cuda")
+    rt.launch_bwd_weight_deterministic_bf16(dyd, xd, g1, K)
+    rt.launch_bwd_weight_deterministic_bf16(dyd, xd, g2, K)
+    assert oracle.normalized_max_abs(ga.cpu().numpy(), ref) < DK_TOL
+    assert oracle.normalized_max_abs(g1.cpu().numpy(), ref) < DK_TOL
+    assert torch.equal(g1, g2)
