@@ -121,3 +121,24 @@ def test_channels_last_dk_runtime_errors(rt):
         rt.launch_bwd_weight_channels_last(x, x.clone(), torch.zeros(3, 32, device="cuda"))
     with pytest.raises(ValueError, match=r"\[B,1,L,H\]"):
         rt.launch_bwd_weight_channels_last(x[:, 0], x[:, 0].clone(), torch.zeros(1, 3, 32, device="cuda"))
+
+
+def _random_cl_cases(n: int, seed: int):
+    """Seeded cases inside the bridge's contract (H % 32 == 0, B / GZ a
+    multiple of 16): any L up to 48, K up to 48, several sample groups."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        gz = int(rng.choice([1, 2, 3, 5, 8]))
+        B = gz * 16 * int(rng.integers(1, 5))
+        H = 32 * int(rng.integers(1, 5))
+        L = int(rng.integers(1, 49))
+        K = int(rng.integers(1, 49) if i % 2 else rng.integers(24, 49))
+        out.append((B, H, L, K, gz))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_cl_cases(16, 20261204),
+                         ids=lambda c: "B{}H{}L{}K{}GZ{}".format(*c))
+def test_channels_last_dk_random_cases(rt, case):
+    test_channels_last_dk_against_fp64(rt, case)
