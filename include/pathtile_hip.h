@@ -102,6 +102,25 @@ int pt_dwconv1d_fwd_f32(const float* x, const float* w, float* y, int B, int H,
                         int L, int K, int waves_per_block, void* stream);
 
 /*
+ * pt_dwconv1d_fwd_f32 / pt_dwconv1d_dx_f32 with the kernel chosen by the
+ * caller: PT_ROWS_AUTO as those entry points (PATHTILE_ROWS_ALGO, then the
+ * library's rule), PT_ROWS_VALU the VALU kernels (the reference's fmaf
+ * chain bit for bit, any layout), PT_ROWS_MATRIX the matrix-core kernel
+ * wherever the layout allows it (else the VALU kernels). An explicit choice
+ * takes precedence over PATHTILE_ROWS_ALGO; any other value of algo is
+ * PT_ERR_CONFIG. No counterpart in the reference, whose one kernel per path
+ * leaves nothing to choose: for a caller that needs the reference's bits
+ * (or the matrix cores) in one runtime, not in the whole process.
+ */
+#define PT_ROWS_AUTO 0
+#define PT_ROWS_VALU 1
+#define PT_ROWS_MATRIX 2
+int pt_dwconv1d_fwd_f32_algo(const float* x, const float* w, float* y, int B, int H,
+                             int L, int K, int waves_per_block, int algo, void* stream);
+int pt_dwconv1d_dx_f32_algo(const float* dy, const float* w, float* dx, int B, int H,
+                            int L, int K, int waves_per_block, int algo, void* stream);
+
+/*
  * Input gradient dx = conv^T(dy, w).
  * Replaces dwconv1d_warptile_bwd_input in AmpereWarpRuntime.launch_bwd_input
  * (kernels/warp_tiled_ampere.py:749-770). Kernel choice as for the forward

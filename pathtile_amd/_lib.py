@@ -27,6 +27,11 @@ PT_ERR_ALIGN = -6
 PT_ERR_SCRATCH = -7
 PT_DK_SCRATCH_BYTES = 8 << 20
 
+# FWD / DX kernel choice of the *_algo entry points
+PT_ROWS_AUTO = 0
+PT_ROWS_VALU = 1
+PT_ROWS_MATRIX = 2
+
 PT_KERNEL_FWD = 0
 PT_KERNEL_DX = 1
 PT_KERNEL_DK = 2
@@ -49,6 +54,8 @@ SIGNATURES = {
     "pt_status_string": (ctypes.c_char_p, [_i]),
     "pt_dwconv1d_fwd_f32": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "pt_dwconv1d_dx_f32": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "pt_dwconv1d_fwd_f32_algo": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "pt_dwconv1d_dx_f32_algo": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "pt_dwconv1d_dk_atomic_f32": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "pt_dwconv1d_dk_det_workspace_bytes": (_i, [_i, _i, _i, _i, _i, _szp]),
     "pt_dwconv1d_dk_det_f32": (

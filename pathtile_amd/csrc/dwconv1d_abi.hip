@@ -543,7 +543,11 @@ static bool rows_small_plain_mfma(int L, long long useful) {
   return 2 * useful >= 25LL * L;                    // L = 20, 24, 28
 }
 
-static RowsAlgo rows_algo(int B, int H, int L, int K) {
+// forced: PT_ROWS_AUTO (the environment, then the rule), PT_ROWS_VALU or
+// PT_ROWS_MATRIX (the caller's choice, over the environment).
+static RowsAlgo rows_algo(int B, int H, int L, int K, int forced = PT_ROWS_AUTO) {
+  if (forced == PT_ROWS_VALU) return kRowsValu;
+  if (forced == PT_ROWS_MATRIX) return kRowsMfma;
   const char* env = getenv("PATHTILE_ROWS_ALGO");
   if (env && strcmp(env, "valu") == 0) return kRowsValu;
   if (env && strcmp(env, "tile") == 0) return kRowsTile;
@@ -702,15 +706,18 @@ static int stream_path(bool dx, const float* in, const float* w, float* out,
 }
 
 static int rows_path(bool dx, const float* in, const float* w, float* out,
-                     int B, int H, int L, int K, int wpb, void* stream) {
+                     int B, int H, int L, int K, int wpb, void* stream,
+                     int forced = PT_ROWS_AUTO) {
   int st = check_shape(B, H, L, K);
   if (st != PT_OK) return st;
   if (!valid_wpb(wpb)) return PT_ERR_CONFIG;
+  if (forced != PT_ROWS_AUTO && forced != PT_ROWS_VALU && forced != PT_ROWS_MATRIX)
+    return PT_ERR_CONFIG;
   if (B == 0 || H == 0) return PT_OK;  // empty tensors may have NULL data
   if (!in || !w || !out) return PT_ERR_NULL;
   if (!aligned(in, 4) || !aligned(w, 4) || !aligned(out, 4))
     return PT_ERR_ALIGN;
-  const RowsAlgo algo = rows_algo(B, H, L, K);
+  const RowsAlgo algo = rows_algo(B, H, L, K, forced);
   if (algo == kRowsMfma && rows_cg_ok(H, L, in, out))
     return rows_cg_path(dx, in, w, out, B, H, L, K, stream);
   // The VALU tile kernel: one 64-row LDS tile per wave. Its limits on the
@@ -1100,6 +1107,16 @@ int pt_dwconv1d_fwd_f32(const float* x, const float* w, float* y, int B, int H,
 int pt_dwconv1d_dx_f32(const float* dy, const float* w, float* dx, int B,
                        int H, int L, int K, int waves_per_block, void* stream) {
   return pt::rows_path(true, dy, w, dx, B, H, L, K, waves_per_block, stream);
+}
+
+int pt_dwconv1d_fwd_f32_algo(const float* x, const float* w, float* y, int B, int H,
+                             int L, int K, int waves_per_block, int algo, void* stream) {
+  return pt::rows_path(false, x, w, y, B, H, L, K, waves_per_block, stream, algo);
+}
+
+int pt_dwconv1d_dx_f32_algo(const float* dy, const float* w, float* dx, int B, int H,
+                            int L, int K, int waves_per_block, int algo, void* stream) {
+  return pt::rows_path(true, dy, w, dx, B, H, L, K, waves_per_block, stream, algo);
 }
 
 int pt_dwconv1d_dk_atomic_f32(const float* dy, const float* x, float* dk,

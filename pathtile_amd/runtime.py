@@ -296,6 +296,11 @@ def _stream_handle(device: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+# FWD/dX kernel choice of HipWarpRuntime(rows_algo=...): the C ABI's
+# PT_ROWS_AUTO, PT_ROWS_VALU and PT_ROWS_MATRIX.
+ROWS_ALGOS = {"auto": _lib.PT_ROWS_AUTO, "valu": _lib.PT_ROWS_VALU, "mfma": _lib.PT_ROWS_MATRIX}
+
+
 class HipWarpRuntime:
     """Owns the launch configuration of the three paths and launches them
     through the C ABI (the reference's AmpereWarpRuntime, :625-846).
@@ -306,6 +311,11 @@ class HipWarpRuntime:
     bwdk_btile          samples per dK wave chunk; fixed at 64 (one per lane)
     fast_math           accepted for signature compatibility; the kernels are
                         FMA-only, so it changes nothing
+    rows_algo           FWD/dX kernel: "auto" (PATHTILE_ROWS_ALGO, then the
+                        library's rule), "valu" (the VALU kernels: the
+                        reference's fmaf chain bit for bit) or "mfma" (the
+                        matrix cores wherever the layout allows); an explicit
+                        choice takes precedence over PATHTILE_ROWS_ALGO
     """
 
     def __init__(
@@ -316,7 +326,10 @@ class HipWarpRuntime:
         fast_math: bool = False,
         *,
         dx_waves_per_block: int | None = None,
+        rows_algo: str = "auto",
     ) -> None:
+        if rows_algo not in ROWS_ALGOS:
+            raise ValueError(f"rows_algo must be one of {', '.join(ROWS_ALGOS)}")
         if dx_waves_per_block is None:
             dx_waves_per_block = (DEFAULT_DX_WAVES_PER_BLOCK
                                   if waves_per_block == DEFAULT_WAVES_PER_BLOCK
@@ -338,6 +351,8 @@ class HipWarpRuntime:
         self.bwdk_btile = int(bwdk_btile)
         self.bwdk_block = int(bwdk_block)
         self.fast_math = bool(fast_math)
+        self.rows_algo = rows_algo
+        self._rows_algo_id = ROWS_ALGOS[rows_algo]
         self.technique = "WaveRow-mi355x"
         self.profile = MI355X
         self._lib = _lib.load()
@@ -390,10 +405,10 @@ class HipWarpRuntime:
 
         def launch() -> None:
             with torch.cuda.device(x.device):
-                st = self._lib.pt_dwconv1d_fwd_f32(
+                st = self._lib.pt_dwconv1d_fwd_f32_algo(
                     _ptr(x), _ptr(k), _ptr(y), B, H, L, K,
-                    self.waves_per_block, _stream_handle(x.device))
-            _lib.check(st, "pt_dwconv1d_fwd_f32")
+                    self.waves_per_block, self._rows_algo_id, _stream_handle(x.device))
+            _lib.check(st, "pt_dwconv1d_fwd_f32_algo")
 
         (collector or KERNEL_EVENTS).launch("fwd", launch, {"B": B, "H": H, "L": L, "K": K})
 
@@ -412,10 +427,10 @@ class HipWarpRuntime:
 
         def launch() -> None:
             with torch.cuda.device(gy.device):
-                st = self._lib.pt_dwconv1d_dx_f32(
+                st = self._lib.pt_dwconv1d_dx_f32_algo(
                     _ptr(gy), _ptr(k), _ptr(gx), B, H, L, K,
-                    self.dx_waves_per_block, _stream_handle(gy.device))
-            _lib.check(st, "pt_dwconv1d_dx_f32")
+                    self.dx_waves_per_block, self._rows_algo_id, _stream_handle(gy.device))
+            _lib.check(st, "pt_dwconv1d_dx_f32_algo")
 
         (collector or KERNEL_EVENTS).launch("bwd_input", launch, {"B": B, "H": H, "L": L, "K": K})
 

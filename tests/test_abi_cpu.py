@@ -39,6 +39,8 @@ def test_header_declares_the_expected_entry_points():
     for name in (
         "pt_dwconv1d_fwd_f32",
         "pt_dwconv1d_dx_f32",
+        "pt_dwconv1d_fwd_f32_algo",
+        "pt_dwconv1d_dx_f32_algo",
         "pt_dwconv1d_dk_atomic_f32",
         "pt_dwconv1d_dk_det_f32",
         "pt_dwconv1d_dk_det_workspace_bytes",
@@ -111,6 +113,14 @@ def test_argument_validation_before_launch(lib):
     # empty batch / channels: nothing to launch
     assert lib.pt_dwconv1d_fwd_f32(pa, pb, pc, 0, 4, 8, 3, 4, S) == _lib.PT_OK
     assert lib.pt_dwconv1d_dx_f32(pa, pb, pc, 5, 0, 8, 3, 4, S) == _lib.PT_OK
+    # the *_algo entry points: PT_ROWS_AUTO, PT_ROWS_VALU, PT_ROWS_MATRIX only
+    for algo in (-1, 3, 7):
+        assert lib.pt_dwconv1d_fwd_f32_algo(pa, pb, pc, 1, 1, 8, 3, 4, algo, S) == _lib.PT_ERR_CONFIG
+        assert lib.pt_dwconv1d_dx_f32_algo(pa, pb, pc, 1, 1, 8, 3, 4, algo, S) == _lib.PT_ERR_CONFIG
+    for algo in (_lib.PT_ROWS_AUTO, _lib.PT_ROWS_VALU, _lib.PT_ROWS_MATRIX):
+        assert lib.pt_dwconv1d_fwd_f32_algo(None, pb, pc, 1, 1, 8, 3, 4, algo, S) == _lib.PT_ERR_NULL
+        assert lib.pt_dwconv1d_dx_f32_algo(pa, pb, pc, 1, 1, 49, 3, 4, algo, S) == _lib.PT_ERR_SHAPE
+        assert lib.pt_dwconv1d_fwd_f32_algo(pa, pb, pc, 0, 4, 8, 3, 4, algo, S) == _lib.PT_OK
     # workspace too small for the deterministic dK
     assert lib.pt_dwconv1d_dk_det_f32(pa, pb, pc, None, 0, 64, 2, 8, 3, 256, S) == _lib.PT_ERR_WORKSPACE
     del P

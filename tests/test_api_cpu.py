@@ -59,8 +59,13 @@ def test_runtime_config_validation():
     for bad in (32, 96, 1024, 0):
         with pytest.raises(ValueError, match="bwdk_block must be a multiple of 64"):
             rt.HipWarpRuntime(bwdk_block=bad)
+    with pytest.raises(ValueError, match="rows_algo must be one of"):
+        rt.HipWarpRuntime(rows_algo="tile")
+    for name in ("auto", "valu", "mfma"):
+        assert rt.HipWarpRuntime(rows_algo=name).rows_algo == name
     r = rt.HipWarpRuntime(waves_per_block=8, bwdk_block=512, dx_waves_per_block=2)
     assert (r.fwd_block, r.dx_waves_per_block, r.bwdk_block) == (512, 2, 512)
+    assert r.rows_algo == "auto"
     r.close()
     r.close()  # idempotent
     with pytest.raises(RuntimeError):

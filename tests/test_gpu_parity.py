@@ -686,3 +686,35 @@ def test_resource_report_lists_every_kernel(rt):
         df = rt.resource_report(L, K)
         assert len(df) == n
         assert (df["scratch_bytes"] == 0).all()
+
+
+@pytest.mark.parametrize("env", [None, "mfma", "valu"])
+def test_runtime_rows_algo_overrides_the_environment(env, monkeypatch):
+    """HipWarpRuntime(rows_algo=...) picks the FWD/dX kernel per runtime,
+    over PATHTILE_ROWS_ALGO: "valu" gives the reference's fmaf chain bit for
+    bit where the default takes the matrix cores (C1), "mfma" stays within
+    1e-5 of FP64 on a short chain the default leaves to the VALU kernel."""
+    from pathtile_amd import runtime
+
+    if env is None:
+        monkeypatch.delenv("PATHTILE_ROWS_ALGO", raising=False)
+    else:
+        monkeypatch.setenv("PATHTILE_ROWS_ALGO", env)
+    r_valu = runtime.HipWarpRuntime(rows_algo="valu")
+    B, H, L, K = 64, 16, 48, 48
+    assert rows_rule.matrix_cores_serve(B, H, L, K)
+    x, w, dy = _inputs(B, H, L, K, seed=31)
+    xd, wd, dyd = _dev(x, w, dy)
+    assert np.array_equal(_fwd(r_valu, xd, wd).cpu().numpy(), oracle.fwd_f32_refchain(x, w))
+    assert np.array_equal(_dx(r_valu, dyd, wd).cpu().numpy(), oracle.dx_f32_refchain(dy, w))
+    r_mfma = runtime.HipWarpRuntime(rows_algo="mfma")
+    B, H, L, K = 257, 8, 48, 4
+    assert not rows_rule.matrix_cores_serve(B, H, L, K)
+    x, w, dy = _inputs(B, H, L, K, seed=32)
+    xd, wd, dyd = _dev(x, w, dy)
+    y = _fwd(r_mfma, xd, wd).cpu().numpy()
+    dx = _dx(r_mfma, dyd, wd).cpu().numpy()
+    assert oracle.normalized_max_abs(y, oracle.fwd_f64(x, w)) < FWD_TOL
+    assert oracle.normalized_max_abs(dx, oracle.dx_f64(dy, w)) < FWD_TOL
+    r_valu.close()
+    r_mfma.close()
