@@ -10,6 +10,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "dwconv1d_kernels.hpp"
@@ -77,24 +78,32 @@ static bool aligned(const void* p, uintptr_t a) {
 }
 
 // --- device queries (cached per device / per kernel) -----------------------
-static int num_cus() {
-  static int cache[64];
+// One device attribute of the current device, queried once per device.
+// Entries are atomics because calls may come from several host threads;
+// threads that race to fill an entry store the same value.
+template <hipDeviceAttribute_t A>
+static int device_attr(int fallback) {
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
     (void)hipGetLastError();
     dev = 0;
   }
-  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
-          hipSuccess ||
-      n <= 0) {
-    (void)hipGetLastError();
-    n = 256;
+  const bool cached = dev >= 0 && dev < 64;
+  if (cached) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
   }
-  if (dev >= 0 && dev < 64) cache[dev] = n;
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, A, dev) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    n = fallback;
+  }
+  if (cached) cache[dev].store(n, std::memory_order_relaxed);
   return n;
 }
+
+static int num_cus() { return device_attr<hipDeviceAttributeMultiprocessorCount>(256); }
 
 struct OccEntry {
   const void* fn;
@@ -391,42 +400,13 @@ static size_t rows_lds_per_wave(int L) {
   return (size_t)kWave * (size_t)(lmax + 4) * sizeof(float);
 }
 
+// 160 KiB: gfx950, the one target of this library.
 static int max_lds_per_block() {
-  static int cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) {
-    (void)hipGetLastError();
-    dev = 0;
-  }
-  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock,
-                            dev) != hipSuccess ||
-      n <= 0) {
-    (void)hipGetLastError();
-    n = 160 * 1024;  // gfx950, the one target of this library
-  }
-  if (dev >= 0 && dev < 64) cache[dev] = n;
-  return n;
+  return device_attr<hipDeviceAttributeMaxSharedMemoryPerBlock>(160 * 1024);
 }
 
 static int lds_per_cu() {
-  static int cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) {
-    (void)hipGetLastError();
-    dev = 0;
-  }
-  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
-                            dev) != hipSuccess ||
-      n <= 0) {
-    (void)hipGetLastError();
-    n = max_lds_per_block();
-  }
-  if (dev >= 0 && dev < 64) cache[dev] = n;
-  return n;
+  return device_attr<hipDeviceAttributeMaxSharedMemoryPerMultiprocessor>(max_lds_per_block());
 }
 
 // Dynamic LDS that makes exactly `bpc` workgroups fit on a CU (at least
