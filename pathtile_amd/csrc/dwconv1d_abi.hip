@@ -452,14 +452,12 @@ static int rows_waves_per_cu(int L, int K, long long ntiles) {
 // --- FWD / DX algorithm ----------------------------------------------------
 // The channel-group matrix-core kernel costs the same whatever K is (it
 // multiplies by the whole LMAX x LMAX band matrix of the row bucket); the VALU
-// rows kernel's cost grows with the FMA chain. Measured on MI355X over
-// L = 16..48 (L % 4 == 0), K = 3..48 and B = 2048..65536, the matrix cores
-// win once a row needs at least 10.5 (LMAX / L)^2 useful FMAs per output on
-// average (LMAX = the row bucket 16, 32 or 48: rows that fill their bucket
-// partly pay for the matrix work they waste); below that the VALU kernel
-// (bit-exact with the reference's fmaf chain) is as fast or faster. Rows of
-// other lengths: kRowsOddMfmaRows below. Rows of 16-28 columns on tensors
-// of at most 256 MiB: rows_small_plain_mfma below.
+// rows kernel's cost grows with the FMA chain. Rows of L % 4 == 0 from 16 to
+// 48 columns take the matrix cores from the K of rows_mfma_min_k below;
+// shorter ones once a row needs at least 10.5 (LMAX / L)^2 useful FMAs per
+// output on average (LMAX = the row bucket 16, 32 or 48); below that the
+// VALU kernel (bit-exact with the reference's fmaf chain) is as fast or
+// faster. Rows of other lengths: kRowsOddMfmaRows below.
 // Where the VALU serves, the tile kernel (a lane per row through an LDS
 // transpose) runs, or the streaming kernel (float4 lanes, no LDS; rows of
 // L % 4 == 0 floats, at most 9 taps) where the channel period would idle
@@ -502,25 +500,38 @@ static bool rows_cg_ok(int H, int L, const void* in, const void* out) {
 // matrix cores 0.89x at K = 12; B2048 H64 L45 likewise).
 constexpr long long kRowsOddMfmaRows = 1LL << 18;
 
-// Rows of L % 4 == 0 on tensors that take plain loads (at most 256 MiB),
-// in the 16-column bucket or filling the 32-column bucket partly (L = 20,
-// 24, 28): the matrix cores from 9.5 x 16 useful FMAs per row (L = 16) and
-// from 12.5 L (L = 20-28). Both admit every row the general rule admits;
-// its (LMAX / L)^2 = 1.78 at L = 24 (2.56 at L = 20) overcharges the
-// half-empty bucket, whose unused columns cost the matrix cores little at
-// these sizes. Measured on MI355X (FWD, three interleaved rounds,
-// matrix-core time / VALU time) at B1024 H96 to B16384 H128 and B4096 H256:
-// L24 K16 0.89-0.99 at all sizes, L24 K20 0.87-1.02, L24 K24 0.69-0.92,
-// L20 K16 0.84-0.91, L20 K24 0.67-0.94, L16 K12 0.92-1.05. The rows left
-// out were mixed: L24 K12 0.92-1.26 and L20 K12 0.85-1.17 (the small calls
-// lose), L16 K10 0.96-1.05. L = 32 keeps the general rule: there the
-// sizes disagreed (K12 0.78 at B2048 H128, 0.90 at B4096 H128, 0.99-1.12
-// elsewhere). Above 256 MiB the general rule stays too: there the VALU
-// kernel won L = 24 at every K tried (B32768 H256 L24 K6-24: the matrix
-// cores took 1.02-1.12x its time).
-static bool rows_small_plain_mfma(int L, long long useful) {
-  if (L == 16) return 2 * useful >= 19 * 16;        // useful >= 9.5 x 16
-  return 2 * useful >= 25LL * L;                    // L = 20, 24, 28
+// Rows of L % 4 == 0 from 16 to 48 columns: the smallest K from which the
+// matrix cores serve. Which kernel wins depends on how much of its row
+// bucket L fills for each kernel (16, 32 or 48 columns for the matrix
+// cores, steps of 8 for the VALU kernel), on the size of the call and, at
+// 48 columns, on H and the load regime. Measured on MI355X (FWD,
+// interleaved rounds, inputs rotated past the MALL below 256 MiB;
+// matrix-core time / VALU time):
+//  * calls of at least 2^17 rows (B x H): L16 K6 0.92-0.99; L20-32 and L44
+//    K10-16 0.78-1.00 (K6-8 0.89-1.06); L36 and L40 K20 0.84-0.95 (K9-16
+//    0.91-1.03 at L36, 1.00-1.13 at L40); L48 K10-16 0.91-0.98 on tensors
+//    of at most 256 MiB with H <= 128, where above 256 MiB or at H = 256 the
+//    two tie or the VALU kernel wins by up to 4%; K20 0.84-0.95 everywhere;
+//  * smaller calls (B512 H128 to B1536 H96, 4-25 us), where the matrix
+//    cores' fixed cost weighs more: L16 K12 0.90-0.98 (K9 up to 1.06), L20
+//    K16 0.83-0.94, L24 K24 0.75-0.83 (K16 0.94-1.03), L28 and L32 K16
+//    0.74-0.95 (K12 up to 1.10), L36 and L44 K24 0.71-0.94 (K16 up to
+//    1.14), L40 K32 0.80-0.93 (K24 up to 1.07), L48 K24 0.79-0.97.
+constexpr long long kRowsSmallCall = 1LL << 17;
+
+static int rows_mfma_min_k(int L, int H, long long rows, bool plain) {
+  const bool small = rows < kRowsSmallCall;
+  switch (L) {
+    case 16: return small ? 12 : 5;
+    case 20: return small ? 16 : 9;
+    case 24: return small ? 17 : 9;
+    case 28:
+    case 32: return small ? 13 : 9;
+    case 36: return 17;
+    case 40: return small ? 25 : 17;
+    case 44: return small ? 17 : 9;
+    default: return small || !plain || H > 128 ? 17 : 9;  // L = 48
+  }
 }
 
 // forced: PT_ROWS_AUTO (the environment, then the rule), PT_ROWS_VALU or
@@ -536,8 +547,9 @@ static RowsAlgo rows_algo(int B, int H, int L, int K, int forced = PT_ROWS_AUTO)
   const long long lmax = 16LL * (mfma_index(L) + 1);
   const long long u2l = 2 * useful_fma_per_row(L, K) * L;
   if (L % 4 == 0) {
-    if (L >= 16 && L < 32 && rows_plain_loads(B, H, L))
-      return rows_small_plain_mfma(L, useful_fma_per_row(L, K)) ? kRowsMfma : kRowsValu;
+    if (L >= 16)
+      return K >= rows_mfma_min_k(L, H, (long long)B * H, rows_plain_loads(B, H, L))
+                 ? kRowsMfma : kRowsValu;
     // useful / L >= 10.5 (lmax / L)^2, in integers
     return u2l >= 21 * lmax * lmax ? kRowsMfma : kRowsValu;
   }
@@ -587,12 +599,16 @@ static int rows_cg_launch(Fn fn, const T* in, const float* w, T* out, int B,
 
 // Channels (waves) per workgroup, whatever the caller's waves per block:
 //  * rows of 33-48 columns with H % 16 == 0, on tensors above 256 MiB or
-//    with at least 24 steps per CU: 16, one per CU, with one input and two
-//    output stages in LDS (148 KB at L = 48). Each step then moves 16
-//    segments of 3 KB instead of 1.5 KB; a copy kernel with the same access
-//    pattern ran in 129.8 us at P against 136.4 us for 1.5 KB segments, and
-//    the kernel itself 3-6% faster there (P: 133.7 against 142.4 us FWD;
-//    B16384 H96 L37 K48 92.2 against 95.9 us);
+//    with at least 24 steps per CU, when L % 4 != 0 or the rows are long
+//    and wide (L > 40 and H L above kRowsCg8MaxSampleFloats): 16, one per
+//    CU, with one input and two output stages in LDS (148 KB at L = 48).
+//    Each step then moves 16 segments of 3 KB instead of 1.5 KB: at
+//    B16384 H256 L48 7-9% faster than 8 channels, B16384 H128 L37 K48
+//    (the element-wise form) 11%. Since the 8-channel kernel issues its
+//    next loads before the matrix work, 8 channels win elsewhere (FWD, 8
+//    interleaved rounds, 8/16 time ratio: L40 0.91-0.94 at H64-256, L44
+//    0.94-0.97 at H64-128, L36 0.96-0.98 at H128, P 0.97-0.99; B16384
+//    H256 L44 1.01, L36 1.00);
 //  * otherwise 8, two per CU where the LDS allows (two input and two output
 //    stages) and each workgroup gets at least kRowsCgMinSteps steps, else
 //    one (rows_cg_launch). Measured on MI355X at 1, 2, 4 and 8 channels, 8 was fastest
@@ -611,6 +627,9 @@ static int rows_cg_launch(Fn fn, const T* in, const float* w, T* out, int B,
 // Steps per workgroup below which the 8-channel FP32 kernel runs one
 // workgroup per CU (rows_cg_launch).
 constexpr int kRowsCgMinSteps = 3;
+// Floats per sample (H L) up to which rows of whole float4s keep 8-channel
+// workgroups at any size (P: 128 x 48).
+constexpr long long kRowsCg8MaxSampleFloats = 128LL * 48;
 
 static int rows_cg_channels_env() {
   const char* env = getenv("PATHTILE_ROWS_CHANNELS");
@@ -625,8 +644,10 @@ static int rows_cg_path(bool dx, const float* in, const float* w, float* out,
   const bool a4 = L % 4 == 0;
   const long long tsteps = ((long long)B + kRowsCgStep - 1) / kRowsCgStep;
   const int forced = rows_cg_channels_env();
-  const bool want16 = forced ? forced == 16
-                             : !plain || tsteps * (H / 16) >= 24LL * num_cus();
+  const bool want16 =
+      forced ? forced == 16
+             : (!plain || tsteps * (H / 16) >= 24LL * num_cus()) &&
+                   (!a4 || (L > 40 && (long long)H * L > kRowsCg8MaxSampleFloats));
   if (mfma_index(L) == 2 && H % 16 == 0 && want16 &&
       rows_cg_lds_bytes(L, 16, 1) <= (size_t)max_lds_per_block()) {
     const RowsCgFn* t16 = a4 ? (plain ? kRowsCg16TablePL : kRowsCg16Table)

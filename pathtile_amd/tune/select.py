@@ -197,12 +197,13 @@ def verify_frozen_before_holdout(policy: dict, holdout_created_at: Iterable[str]
 # --------------------------------------------------------------------------
 KNOB_INERT_RULE = (
     "FWD/dX waves per workgroup cannot change the kernel where the matrix-core "
-    "FWD/dX kernel serves (H % 8 == 0 and, for L % 4 == 0 on tensors of at most "
-    "256 MiB, >= 9.5 x 16 useful FMAs per row at L = 16 and >= 12.5 L at L = 20-28, "
-    ">= 10.5 (LMAX / L)^2 useful FMAs per output otherwise, LMAX = 16 ceil(L / 16); "
-    "for L % 4 != 0 every call of >= 2^18 rows and smaller ones from 5 (LMAX / L)^2): "
-    "it always runs 8- or 16-wave workgroups. There the FWD/dX candidates differ "
-    "only by measurement noise.")
+    "FWD/dX kernel serves (H % 8 == 0 and, for L % 4 == 0 with 16 <= L <= 48, K at "
+    "least a threshold by L: 5 at L = 16, 9 at L = 20-32 and 44, 17 at L = 36 and 40, "
+    "9 at L = 48 on tensors of at most 256 MiB with H <= 128 and 17 otherwise, higher "
+    "on calls of fewer than 2^17 rows; for L < 16 >= 10.5 (16 / L)^2 useful FMAs per "
+    "output; for L % 4 != 0 every call of >= 2^18 rows and smaller ones from 5 "
+    "(LMAX / L)^2, LMAX = 16 ceil(L / 16)): it always runs 8- or 16-wave workgroups. "
+    "There the FWD/dX candidates differ only by measurement noise.")
 
 
 def fwd_dx_knob_inert(H: int, L: int, K: int, B: int) -> bool:

@@ -208,7 +208,7 @@ def _shape_rows(cid, H, L, K, times):
 
 
 def test_fwd_dx_knob_inert_follows_the_library_rule():
-    # matrix cores: H % 8 == 0 and >= 10.5 (LMAX / L)^2 useful FMAs per output
+    # matrix cores: H % 8 == 0 and the library's thresholds
     assert select.fwd_dx_knob_inert(128, 48, 48, 16384)       # P
     assert select.fwd_dx_knob_inert(128, 48, 47, 16384)       # E2
     assert not select.fwd_dx_knob_inert(256, 48, 4, 32768)    # S: short chain, VALU kernel
@@ -216,30 +216,33 @@ def test_fwd_dx_knob_inert_follows_the_library_rule():
     assert not select.fwd_dx_knob_inert(96, 37, 8, 1000)      # short chain, small call: VALU
     assert select.fwd_dx_knob_inert(96, 37, 8, 4096)          # L % 4 != 0 from 2^18 rows: matrix cores
     assert not select.fwd_dx_knob_inert(12, 48, 48, 16384)    # H % 8 != 0
-    # rows of 16 and 20-28 columns on tensors of at most 256 MiB: 9.5 x 16
-    # useful FMAs per row at L = 16, 12.5 L at L = 20-28 (L24 K16: 320 >= 300);
-    # above 256 MiB the general rule (320 * 24 * 2 < 21 * 32 * 32)
-    assert select.fwd_dx_knob_inert(128, 24, 16, 16384)       # 201 MB
-    assert not select.fwd_dx_knob_inert(256, 24, 16, 32768)   # 805 MB
-    assert not select.fwd_dx_knob_inert(128, 24, 14, 16384)   # 287 < 300
-    assert select.fwd_dx_knob_inert(128, 20, 16, 16384)       # 256 >= 250
-    assert not select.fwd_dx_knob_inert(128, 20, 12, 16384)   # 204 < 250
-    assert select.fwd_dx_knob_inert(128, 16, 12, 16384)       # 156 >= 152
-    assert not select.fwd_dx_knob_inert(128, 16, 10, 16384)   # 135 < 152
-    assert not select.fwd_dx_knob_inert(128, 32, 11, 8192)    # L = 32: general rule (10.06 < 10.5)
-    assert select.fwd_dx_knob_inert(128, 32, 12, 8192)        # 10.9 >= 10.5
-    assert not select.fwd_dx_knob_inert(128, 40, 16, 16384)   # 48-column bucket: general rule
-    # the useful-FMA threshold against a brute-force count: L = 40 (LMAX 48)
-    L, K = 40, 32
-    p = K // 2
-    useful = sum(1 for t in range(L) for j in range(K) if 0 <= t + j - p < L)
-    assert rows_rule.useful_fma_per_row(L, K) == useful
-    assert select.fwd_dx_knob_inert(64, L, K, 2048) == (2 * useful * L >= 21 * 48 * 48)
-    # and in the 32-column bucket: L = 24 (plain loads at B2048 H64)
-    L, K = 24, 20
+    # rows of L % 4 == 0 from 16 to 48 columns: the matrix cores from a K
+    # that depends on L, on calls of fewer than 2^17 rows (B * H) and, at
+    # L = 48, on the load regime and H
+    assert select.fwd_dx_knob_inert(128, 24, 9, 16384)        # L24 from K = 9
+    assert not select.fwd_dx_knob_inert(128, 24, 8, 16384)
+    assert select.fwd_dx_knob_inert(256, 24, 16, 32768)       # above 256 MiB too
+    assert not select.fwd_dx_knob_inert(96, 24, 16, 1024)     # 98304 rows: from K = 17
+    assert select.fwd_dx_knob_inert(96, 24, 17, 1024)
+    assert select.fwd_dx_knob_inert(128, 16, 5, 16384)        # L16 from K = 5
+    assert not select.fwd_dx_knob_inert(128, 16, 4, 16384)
+    assert not select.fwd_dx_knob_inert(128, 40, 16, 16384)   # L40 from K = 17
+    assert select.fwd_dx_knob_inert(128, 40, 17, 16384)
+    assert not select.fwd_dx_knob_inert(64, 40, 24, 2000)     # 128000 rows: from K = 25
+    assert select.fwd_dx_knob_inert(64, 40, 25, 2000)
+    assert select.fwd_dx_knob_inert(128, 48, 9, 8192)         # L48, 201 MB, H <= 128: K >= 9
+    assert not select.fwd_dx_knob_inert(128, 48, 16, 16384)   # above 256 MiB: K >= 17
+    assert not select.fwd_dx_knob_inert(256, 48, 16, 4096)    # H > 128: K >= 17
+    assert select.fwd_dx_knob_inert(256, 48, 17, 4096)
+    # rows of fewer than 16 columns: >= 10.5 (16 / L)^2 useful FMAs per
+    # output, with the useful count against brute force
+    L, K = 12, 24
     useful = sum(1 for t in range(L) for j in range(K) if 0 <= t + j - K // 2 < L)
     assert rows_rule.useful_fma_per_row(L, K) == useful
-    assert select.fwd_dx_knob_inert(64, L, K, 2048) == (2 * useful >= 25 * L)
+    assert select.fwd_dx_knob_inert(64, L, K, 2048) == (2 * useful * L >= 21 * 16 * 16)
+    L, K = 40, 32
+    useful = sum(1 for t in range(L) for j in range(K) if 0 <= t + j - K // 2 < L)
+    assert rows_rule.useful_fma_per_row(L, K) == useful
 
 
 def test_per_path_and_active_knob_regret():
