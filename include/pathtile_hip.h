@@ -78,17 +78,20 @@ const char* pt_status_string(int status);
  * Two kernels serve FWD and DX. The lane-per-row VALU kernel reproduces the
  * reference's fmaf chain bit for bit and honours waves_per_block; its
  * workgroup holds a 64-row LDS tile per wave, so 16 waves fit only rows up
- * to 32 (PT_ERR_CONFIG for longer rows on this kernel). Where a row needs at
- * least 10.5 (LMAX / L)^2 useful FMAs per output on average (LMAX =
- * 16 ceil(L / 16); on tensors of at most 256 MiB, rows of 16 columns from
- * 9.5 x 16 useful FMAs per row and rows of 20-28 from 12.5 L) and the
- * layout allows it
- * (H % 8 == 0, x and y 16-byte
- * aligned; any L), the channel-group matrix-core kernel runs instead:
- * 8 waves (channels) per workgroup, or 16 for rows of 33-48 columns when
- * H % 16 == 0 and the call is large (tensors above 256 MiB or at least 24
- * 16-sample steps per CU), whatever waves_per_block says, so every value is
- * accepted there and gives the same bits; it sums in the
+ * to 32 (PT_ERR_CONFIG for longer rows on this kernel). Where the FMA chain
+ * is long enough and the layout allows it (H % 8 == 0, x and y 16-byte
+ * aligned; any L), the channel-group matrix-core kernel runs instead. For
+ * rows of L % 4 == 0 from 16 to 48 columns "long enough" means K at least
+ * 5 (L = 16), 9 (L = 20-32, 44; L = 48 on tensors of at most 256 MiB with
+ * H <= 128) or 17 (L = 36, 40; L = 48 otherwise), higher on calls of fewer
+ * than 2^17 rows (B x H); shorter rows need 10.5 (16 / L)^2 useful FMAs per
+ * output; rows of other lengths take it from 2^18 rows at any K, and below
+ * that from 5 (LMAX / L)^2 useful FMAs per output (LMAX = 16 ceil(L / 16)).
+ * It runs 8 waves (channels) per workgroup, or 16 on large calls (tensors
+ * above 256 MiB or at least 24 16-sample steps per CU) with H % 16 == 0 for
+ * rows of 33-47 columns with L % 4 != 0 and for rows of more than 40
+ * columns with H L > 128 x 48, whatever waves_per_block says, so every
+ * value is accepted there and gives the same bits; it sums in the
  * matrix cores' order (within FP32 rounding of the reference: about 3e-7
  * max-abs-scaled against FP64). On both kernels an Inf or NaN input or tap
  * reaches exactly the outputs whose reference window holds it (those
