@@ -2105,11 +2105,15 @@ __global__ __launch_bounds__(kClWaves * kWave) void dwconv_dk_cl_kernel(
       for (int d = 0; d < 2; ++d) {
         const int s = s0 + d;
         if (s < nsteps) {
-          mfma_step(d);
+          // Stage d ^ 1 was last read by mfma_step of step s - 1, finished
+          // by every thread before the previous barrier: store step s + 1
+          // and issue the loads of s + 2 before this step's matrix work
+          // (1-2% faster than after it at every shape measured).
           if (s + 1 < nsteps) {
             store_stage(d ^ 1);
             if (s + 2 < nsteps) load_step(s + 2);
           }
+          mfma_step(d);
           __syncthreads();
         }
       }
