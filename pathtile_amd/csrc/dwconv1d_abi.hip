@@ -706,6 +706,30 @@ static int stream_path(bool dx, const float* in, const float* w, float* out,
   return launch((const void*)fn, nblocks, (uint32_t)threads, 0, stream, args);
 }
 
+// Fronts of the VALU tile kernel. With one front the whole grid walks one
+// contiguous window of the input (and of the output, at the same offset),
+// and the time then depends on where the two tensors lie relative to each
+// other: at B32768 H256 L48 K4, with the output moved 0-512 MiB from the
+// input inside one allocation, 552-633 us (FWD and DX alike), 32 MiB the
+// worst. Two fronts, each half of the waves walking half of the tiles, ran
+// 543-552 us at every one of those 17 offsets (mean 548 against 575), 4
+// fronts 551-558, 8 563-566, 16 576-583, 32 602-609 (smaller windows per
+// front). Across 18 shapes of this kernel, one placement each, two fronts
+// measured 0.98-1.014x the time of one (B65536 H128 L16 K4 the 1.014).
+// Returns the largest power of two up to the requested count
+// (PATHTILE_ROWS_FRONTS, else 2) that divides the waves into equal sets
+// whose step keeps each lane's channel (a multiple of `period` tiles), on
+// grids that take more than one round; else 1.
+static int rows_fronts(long long nwaves, long long ntiles, long long period) {
+  int req = 2;
+  const char* env = getenv("PATHTILE_ROWS_FRONTS");
+  if (env) req = atoi(env);
+  if (ntiles <= nwaves) return 1;
+  int f = 1;
+  while (2 * f <= req && nwaves % (2LL * f * period) == 0) f *= 2;
+  return f;
+}
+
 static int rows_path(bool dx, const float* in, const float* w, float* out,
                      int B, int H, int L, int K, int wpb, void* stream,
                      int forced = PT_ROWS_AUTO) {
@@ -740,9 +764,10 @@ static int rows_path(bool dx, const float* in, const float* w, float* out,
   RowsFn fn = dx ? (vec ? (plain ? kDxTableVP : kDxTableV) : kDxTableS)[li][ki]
                  : (vec ? (plain ? kFwdTableVP : kFwdTableV) : kFwdTableS)[li][ki];
   // Persistent grid: one round of resident workgroups, no more than there
-  // are tiles. Wave g takes tiles g, g + G, ...; lane i's channel stays
-  // fixed when G is a multiple of P = H / gcd(H, 64), i.e. the workgroup
-  // count a multiple of Q = P / gcd(P, wpb). Rounding down to that idles
+  // are tiles. Wave g takes tiles g, g + G, ... (per front: rows_fronts);
+  // lane i's channel stays fixed when G is a multiple of P = H / gcd(H, 64),
+  // i.e. the workgroup count a multiple of Q = P / gcd(P, wpb), and with
+  // fronts each front's share of G too. Rounding down to that idles
   // nb % Q workgroups; a lane whose channel changes reloads its taps every
   // tile, which measured 16% slower than idling 13% of the waves
   // (B30000 H37 L32 K8) and 25% faster than idling 49% (B2000 H131 L44 K9).
@@ -764,7 +789,9 @@ static int rows_path(bool dx, const float* in, const float* w, float* out,
   uint32_t nblocks = (uint32_t)nb;
   uint32_t uR = (uint32_t)R, uT = (uint32_t)ntiles;
   uint32_t lmagic = (uint32_t)(((1u << 20) + (uint32_t)L - 1) / (uint32_t)L);
-  void* args[] = {&in, &w, &out, &H, &L, &K, &uR, &uT, &lmagic};
+  uint32_t nfront = (uint32_t)rows_fronts(nb * wpb, ntiles, periodic ? P : 1);
+  uint32_t chunk = (uint32_t)((ntiles + nfront - 1) / nfront);
+  void* args[] = {&in, &w, &out, &H, &L, &K, &uR, &uT, &lmagic, &nfront, &chunk};
   return launch((const void*)fn, nblocks, (uint32_t)(wpb * kWave), lds, stream,
                 args);
 }

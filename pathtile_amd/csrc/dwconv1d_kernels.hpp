@@ -327,9 +327,12 @@ __device__ __forceinline__ void load_taps(const float* __restrict__ w, int h,
 // aligned), one per lane, so every HBM load/store instruction of a wave
 // covers 1 KiB of contiguous memory (dwordx4) and tiles never share a cache
 // line. Lane i's row r0 + i belongs to channel (r0 + i) % H; its taps sit in
-// VGPRs. The grid is persistent: wave g takes tiles g, g + G, g + 2G, ...
-// with G a multiple of H / gcd(H, 64) where possible, so a lane keeps its
-// channel (and its taps) for the whole kernel.
+// VGPRs. The grid is persistent and walks the tiles in `nfront` fronts:
+// the tiles split into nfront contiguous chunks, and wave g takes tiles
+// c + g', c + g' + G', c + g' + 2G', ... of chunk g % nfront (start c,
+// g' = g / nfront, G' = G / nfront), with G' a multiple of H / gcd(H, 64)
+// where possible, so a lane keeps its channel (and its taps) for the whole
+// kernel. With one front this is the order g, g + G, g + 2G, ...
 //
 // Per tile: flat loads -> LDS (padded row stride S = LMAX + 4 floats, so the
 // ds_read_b128 of a lane's own row is bank-conflict free) -> own row into
@@ -382,7 +385,7 @@ template <int LMAX, int KB, bool DX, bool VEC, int LOAD_CPOL = kCpolNT,
 __global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kernel(
     const float* __restrict__ in, const float* __restrict__ w,
     float* __restrict__ out, int H, int L, int K, uint32_t R, uint32_t ntiles,
-    uint32_t lmagic) {
+    uint32_t lmagic, uint32_t nfront, uint32_t chunk) {
   using W = Window<LMAX, KB, DX>;
   constexpr int S = LMAX + 4;     // padded LDS row stride (floats)
   constexpr int NV = LMAX / 4;    // dwordx4 steps per lane (vector path)
@@ -409,7 +412,14 @@ __global__ __launch_bounds__(rows_max_threads(LMAX, VEC)) void dwconv_rows_kerne
   // the reference skips the term. Without padding no such term exists.
   const bool padded = L != LMAX || K != KB;
 
-  for (uint32_t t0 = gwave; t0 < ntiles; t0 += nwaves) {
+  // Fronts: the tiles split into nfront chunks of `chunk` consecutive tiles
+  // and the waves into nfront equal sets (nwaves % nfront == 0, set by the
+  // host), wave g walking chunk g % nfront. nfront = 1, chunk = ntiles is
+  // the plain order g, g + G, g + 2G, ...
+  const uint32_t front = gwave % nfront;
+  const uint32_t fstep = nwaves / nfront;
+  const uint32_t tend = min(front * chunk + chunk, ntiles);
+  for (uint32_t t0 = front * chunk + gwave / nfront; t0 < tend; t0 += fstep) {
     // readfirstlane keeps per-tile bases opaque to loop strength reduction.
     const uint32_t t = __builtin_amdgcn_readfirstlane(t0);
     const uint32_t r0 = t * kWave;

@@ -13,7 +13,7 @@ constexpr int kNumKB = 7;  // tap buckets below
 constexpr int kKBuckets[kNumKB] = {4, 8, 16, 24, 32, 40, 48};
 
 using RowsFn = void (*)(const float*, const float*, float*, int, int, int,
-                        uint32_t, uint32_t, uint32_t);
+                        uint32_t, uint32_t, uint32_t, uint32_t, uint32_t);
 using DkFn = void (*)(const float*, const float*, float*, int, int, int, int,
                       int, int, uint32_t, int);
 using DkMfmaFn = void (*)(const float*, const float*, float*, int, int, int,
