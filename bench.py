@@ -14,9 +14,13 @@ reference's protocol (artifact/REPRODUCIBILITY.md:81-93): 3 trials, each of
 even trials (benchmark/benchmark_pathtile_candidate_sweep.py:488-501), mean
 of the trial means; the between-trial standard deviation is reported beside
 it. The timed launches run back to back between two HIP events on the launch
-stream. ``ms_per_step`` is the wall time of the contract's ``--steps``
-interleaved FWD/dX/zero+dK steps (after ``--warmup`` steps) between two
-device synchronisations. After timing, the outputs of the timed launches are
+stream; ``paths_rotated`` repeats FWD, dX and dK over rotated buffer sets, so
+that no launch finds its inputs in the MALL (the cold control), and the
+roofline takes the slower of the two. ``ms_per_step`` is the wall time of the
+contract's ``--steps`` interleaved FWD/dX/zero+dK steps (after 0.3 s of steps
+and ``--warmup`` steps) between two device synchronisations, with an event
+pair beside it (``ms_per_step_gpu``). Every configuration prints its
+per-path ms and % of peak on stderr. After timing, the outputs of the timed launches are
 checked against PyTorch FP64 on the GPU: FWD/dX on sampled batch rows (all
 channels), dK over the whole batch. The same protocol and checks run for the
 BASELINE's other configurations (S, E2, E1) as separate legs.
@@ -221,23 +225,12 @@ def time_paths(fns: dict, stream, trials: int, warmup: int, runs: int) -> dict:
 
 
 def rows_kernel_name(B: int, H: int, L: int, K: int, dx: bool) -> str:
-    """The FWD/DX kernel the library picks for 16-byte aligned rows: the
-    channel-group matrix-core kernel where pathtile_amd.rows_rule says the
-    matrix cores serve, else the VALU rows kernel (or either on request
-    through PATHTILE_ROWS_ALGO)."""
-    from pathtile_amd import rows_rule
+    """The FWD/DX kernel the library runs for this call on 16-byte aligned
+    tensors, as its own dispatch reports it (pt_rows_kernel_id; the
+    PATHTILE_ROWS_* environment included)."""
+    from pathtile_amd import runtime
 
-    tag = "DX" if dx else "FWD"
-    algo = os.environ.get("PATHTILE_ROWS_ALGO")
-    if algo == "mfma":
-        mfma = H % 8 == 0
-    elif algo in ("valu", "tile", "stream"):
-        mfma = False
-    else:
-        mfma = rows_rule.matrix_cores_serve(B, H, L, K)
-    if mfma:
-        return f"dwconv_rows_cg_kernel<{tag}>"
-    return f"dwconv_rows_kernel<{tag}>"
+    return runtime.rows_kernel_name(B, H, L, K, dx=dx)
 
 
 def dk_kernel_name(H: int, L: int, threads: int) -> str:
@@ -356,6 +349,8 @@ def workload_leg(rt, name: str, args, dev, stream, keep: bool = False) -> dict:
            "sampled_rows": int(idx.numel()),
            "bars": "FWD/dX <= 1e-5, dK <= 1e-4 max-abs-scaled vs PyTorch FP64 on the GPU"},
     }
+    log(f"{name}: {path_line(paths)}; FWD+dX+dK {agg:.4f} ms "
+        f"({leg['aggregate_pct_peak']:.1f}%)")
     if not keep and args.gpu_library_steps:
         leg["gpu_library_baseline"] = gpu_library_baseline(x, w, dy, args.gpu_library_steps)
     if keep:
@@ -364,6 +359,66 @@ def workload_leg(rt, name: str, args, dev, stream, keep: bool = False) -> dict:
         del x, w, dy, y, dx, gk, gd, gd2, ref
         torch.cuda.empty_cache()
     return leg
+
+
+PATH_TAGS = {"fwd": "FWD", "bwd_input": "dX", "bwd_weight": "dK",
+             "bwd_weight_zero": "dK+zero", "bwd_weight_det": "dK det"}
+
+
+def path_line(paths: dict) -> str:
+    """One stderr line of per-path ms and % of the 8 TB/s peak."""
+    return ", ".join(f"{PATH_TAGS.get(k, k)} {v['ms']:.4f} ms ({v['pct_peak']:.1f}%)"
+                     for k, v in paths.items())
+
+
+def compact_leg(leg: dict) -> dict:
+    """A configuration leg for the JSON line: per path [ms, between-trial std
+    ms, % of 8 TB/s], the kernels, the aggregate and the check errors."""
+    p = leg["paths"]
+    chk = leg["check_of_timed_outputs"]
+    out = {
+        "config": leg["config"],
+        "fwd_dx_dk_ms": leg["fwd_dx_dk_ms"],
+        "aggregate_pct_peak": leg["aggregate_pct_peak"],
+        "paths": {k: [v["ms"], v["std_ms"], v["pct_peak"]] for k, v in p.items()},
+        "kernels": sorted({v["kernel"] for v in p.values()}),
+        "check_max_err": {k: v for k, v in chk.items() if isinstance(v, float)},
+        "det_dk_bitwise_repeat": chk["deterministic_dk_bitwise_repeat"],
+    }
+    if "gpu_library_baseline" in leg:
+        out["miopen_ms"] = leg["gpu_library_baseline"]["paths_ms"]
+    return out
+
+
+def rotated_paths(rt, args, stream, x, w, dy, K, gk) -> dict:
+    """FWD, dX and dK timed over rotated buffer sets (the cold control): each
+    launch reads tensors that at least one other set's launch has streamed
+    past since their last use (2 x 403 MB at P, past the 256 MB MALL), so
+    no launch can find its inputs in the MALL."""
+    import torch
+
+    nsets = max(2, -(-(512 << 20) // (2 * x.numel() * 4)) + 1)
+    sets = [(x, dy, torch.empty_like(x), torch.empty_like(dy))]
+    sets += [(x.clone(), dy.clone(), torch.empty_like(x), torch.empty_like(dy))
+             for _ in range(nsets - 1)]
+    cur = {"fwd": 0, "bwd_input": 0, "bwd_weight": 0}
+
+    def rotated(ph, call):
+        def fn():
+            i = cur[ph] = (cur[ph] + 1) % nsets
+            call(*sets[i])
+        return fn
+
+    fns = {
+        "fwd": rotated("fwd", lambda xs, dys, ys, dxs: rt.launch_fwd(xs, w, ys)),
+        "bwd_input": rotated("bwd_input", lambda xs, dys, ys, dxs: rt.launch_bwd_input(dys, w, dxs)),
+        "bwd_weight": rotated("bwd_weight", lambda xs, dys, ys, dxs: rt.launch_bwd_weight(dys, xs, gk, K)),
+    }
+    device_warmup(fns)
+    t = time_paths(fns, stream, args.trials, args.path_warmup, args.path_runs)
+    del sets
+    torch.cuda.empty_cache()
+    return {"sets": nsets, "timing": t}
 
 
 def cpu_baseline(x, w, dy, runs: int) -> dict:
@@ -579,12 +634,9 @@ def extras(rt, args, dev, stream, x, w, dy, y, gk) -> dict:
                 "paths": {ph: {"ms": round(v["ms"], 5), "std_ms": round(v["std_ms"], 5),
                                "pct_peak": round(100 * nb / (v["ms"] / 1e3) / 1e9 / PEAK_HBM_GBPS, 2)}
                           for ph, v in t_cold.items()},
-                "note": "the same paths cycling over buffer sets so that no launch finds "
-                        "its inputs in the 256 MB MALL",
             },
             "gate_vs_fp32_path": float(f"{bf16_gate:.3e}"),
-            "note": "x, dY, y, dX bfloat16; taps and dK FP32; FP32 accumulation; "
-                    "algorithmic bytes (2 B H L * 2 + H K * 4) per path",
+            "note": "x, dY, y, dX bf16; taps, dK fp32; bytes 2BHL*2 + HK*4 per path",
         }
 
     # Channels-last dK through the Flash-DWC bridge ABI (flash_dk_fp32).
@@ -606,8 +658,7 @@ def extras(rt, args, dev, stream, x, w, dy, y, gk) -> dict:
             "gbps": round(gb, 1), "pct_peak": round(100 * gb / PEAK_HBM_GBPS, 2),
             "kernel": f"dwconv_dk_cl_kernel<{16 * ((L + 15) // 16)}>",
             "gate_vs_row_major": float(f"{cl_gate:.3e}"),
-            "note": "flash_dk_fp32 (x, dY [B,1,L,H]; dw [1,K,H] accumulated), GZ=1; "
-                    "algorithmic bytes as the row-major dK"}
+            "note": "flash_dk_fp32, x/dY [B,1,L,H], GZ=1"}
         del xc, dyc, dwc
 
     # The VALU rows kernel (the reference's lane-per-row structure, bit-exact
@@ -637,7 +688,7 @@ def extras(rt, args, dev, stream, x, w, dy, y, gk) -> dict:
                                / PEAK_HBM_GBPS, 2), "kernel": kern[ph]}
         for ph, v in t.items()
     } | {"check_vs_fp64": {k: float(f"{v:.3e}") for k, v in valu_gate.items()},
-         "note": "PATHTILE_ROWS_ALGO=valu: the bit-exact VALU FWD/DX kernel, same protocol"}
+         "note": "PATHTILE_ROWS_ALGO=valu (bit-exact VALU kernel)"}
     return out
 
 
@@ -711,15 +762,10 @@ def long_rows_leg(rt, args, dev, stream) -> dict:
         "kernels": {"fwd": "dwconv_rows_long_s3_kernel<192, 192, false, true>",
                     "bwd_input": "dwconv_rows_long_s3_kernel<192, 192, true, true>",
                     "bwd_weight": "dwconv_dk_long_s3_kernel<192, true>"},
-        "fp32_mfma_kernels": {"paths": paths(t_fp32, False),
-                              "fwd_dx_dk_ms": round(sum(v["ms"] for v in t_fp32.values()), 5)},
+        "fp32_mfma_kernels_ms": {k: round(v["ms"], 5) for k, v in t_fp32.items()},
         "check_fwd_first_256_samples": {k: float(f"{v:.3e}") for k, v in gate.items()},
-        "note": "pt_dwconv1d_{fwd,dx,dk}_long_f32; default = BF16 matrix cores on three-way split "
-                "FP32 operands (FP32-accurate), fp32_mfma_kernels = PATHTILE_LONG_ALGO=fp32; "
-                "tflops_useful = 2 * real multiply-adds / time; frac_bf16_mfma_peak = BF16 matrix "
-                "flops the split kernels issue (rocprofv3 SQ_INSTS_VALU_MFMA_MOPS_BF16, "
-                "profiles/pmc_mfma_long_l192_k192.md) / time / 2.5 PFLOP/s; HBM bytes "
-                "2 B H L 4 + H K 4 per path",
+        "note": "BF16 matrix cores on 3-way split FP32 operands; issued BF16 flops from "
+                "profiles/pmc_mfma_long_l192_k192.md; fp32_mfma_kernels_ms: PATHTILE_LONG_ALGO=fp32",
     }
 
 
@@ -749,7 +795,15 @@ def main(argv=None) -> int:
     log(f"workload {args.workload} config={cfg}")
     main_leg = workload_leg(rt, args.workload, args, dev, stream, keep=True)
     x_cpu, w_cpu, dy_cpu, x, w, dy, y, dx, gk = main_leg.pop("_tensors")
-    log(f"{args.workload}: {main_leg['fwd_dx_dk_ms']:.4f} ms, checks {main_leg['check_of_timed_outputs']}")
+    log(f"{args.workload}: checks {main_leg['check_of_timed_outputs']}")
+    nbytes = main_leg["algorithmic_bytes_per_path"]
+    cold = rotated_paths(rt, args, stream, x, w, dy, K, gk)
+    cold_paths = {}
+    for ph, t in cold["timing"].items():
+        gbps = runtime.algorithmic_bandwidth_gbps(nbytes, t["ms"])
+        cold_paths[ph] = {"ms": round(t["ms"], 5), "std_ms": round(t["std_ms"], 5),
+                          "gbps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_HBM_GBPS, 2)}
+    log(f"{args.workload} over {cold['sets']} rotated buffer sets: {path_line(cold_paths)}")
 
     def step():
         rt.launch_fwd(x, w, y)
@@ -758,15 +812,27 @@ def main(argv=None) -> int:
         rt.launch_bwd_weight(dy, x, gk, K)
 
     # The contract's steps: `warmup` untimed, then exactly `steps` interleaved
-    # FWD / dX / zero + dK steps, wall-clocked between two synchronisations.
+    # FWD / dX / zero + dK steps, wall-clocked between two synchronisations,
+    # with an event pair on the launch stream beside the wall clock. Before
+    # the warm-up steps the GPU runs 0.3 s of steps: on MI355X bursts of
+    # ~10 ms from a quiet GPU run these steps at 0.470-0.480 ms and after
+    # 0.3 s of sustained work at 0.388 ms (the per-path sum), which a 1 s
+    # pause followed by 0.1 s of work keeps (a clock ramp, not host time:
+    # the host enqueues a launch in ~10 us).
+    device_warmup({"step": step})
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    e0.record(stream)
     for _ in range(args.steps):
         step()
+    e1.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
+    gpu_step_ms = e0.elapsed_time(e1) / args.steps
 
     # The reference's per-launch protocol (kernels/warp_tiled_ampere.py:
     # 1059-1070): an event pair around every launch; dK re-zeroed outside.
@@ -788,10 +854,12 @@ def main(argv=None) -> int:
 
     paths = main_leg["paths"]
     agg = main_leg["fwd_dx_dk_ms"]
-    nbytes = main_leg["algorithmic_bytes_per_path"]
     dominant = max(("fwd", "bwd_input", "bwd_weight"), key=lambda k: paths[k]["ms"])
     tag = {"fwd": "fwd", "bwd_input": "dx", "bwd_weight": "dk"}[dominant]
-    ach = paths[dominant]["gbps"]
+    # The roofline takes the slower of the back-to-back and the rotated
+    # (cold) timing of the dominant path.
+    cold_slower = cold_paths[dominant]["ms"] > paths[dominant]["ms"]
+    ach = (cold_paths if cold_slower else paths)[dominant]["gbps"]
     traffic = read_traffic(f"{tag}_{args.workload}")
     line = {
         "metric": METRIC,
@@ -801,10 +869,11 @@ def main(argv=None) -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(wall_ms / args.steps, 5),
+        "ms_per_step_gpu": round(gpu_step_ms, 5),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": round(agg / REFERENCE_AGGREGATE_MS, 5),
-        "vs_baseline_ref": "reference aggregate 11.283 ms on A100 PCIe (README.md:96); value/ref, lower is better",
+        "vs_baseline_ref": "A100 PCIe aggregate 11.283 ms (README.md:96); value/ref",
         "dtype": "f32",
         "data": "synthetic (CPU torch.Generator: x, w, dY; x,dY~N(0,1), w~N(0,1/K))",
         "config": {
@@ -816,20 +885,23 @@ def main(argv=None) -> int:
             "dk_threads_per_block": cfg["dk_threads_per_block"],
             "launch_config_source": cfg["source"],
         },
-        "protocol": (f"value = FWD + dX + dK (atomic, excl. zero-init); each path: {args.trials} "
-                     f"trials x ({args.path_warmup} warm-up + {args.path_runs} timed launches back "
-                     "to back between two HIP events on the launch stream), path order reversed "
-                     "on even trials, mean of trial means (std_ms = between-trial std); "
-                     "per_launch_event_ms = an event pair per launch; ms_per_step = wall time of "
-                     "`steps` interleaved FWD/dX/zero+dK steps"),
+        "protocol": (f"value = FWD + dX + dK (atomic, excl. zero-init); per path {args.trials} trials "
+                     f"x ({args.path_warmup} warm-up + {args.path_runs} launches back to back between "
+                     "two events on the launch stream), order reversed on even trials, mean of trial "
+                     "means; paths_rotated: the same over rotated buffer sets (no MALL reuse); "
+                     "ms_per_step: wall time of `steps` FWD/dX/zero+dK steps after 0.3 s and "
+                     "`warmup` warm-up steps (ms_per_step_gpu: event pair); legs: [ms, std_ms, "
+                     "% of 8 TB/s]"),
         "value_std_ms": main_leg["fwd_dx_dk_std_ms"],
         "aggregate_gbps": round(3 * nbytes / (agg / 1e3) / 1e9, 1),
         "aggregate_pct_peak": main_leg["aggregate_pct_peak"],
         "algorithmic_bytes_per_path": nbytes,
         "paths": paths,
+        "paths_rotated": cold_paths | {"sets": cold["sets"]},
         "check_of_timed_outputs": main_leg["check_of_timed_outputs"],
         "roofline": {
             "kernel": paths[dominant]["kernel"],
+            "timing": "rotated buffers" if cold_slower else "back to back",
             "bound": "hbm",
             "achieved": ach,
             "peak": PEAK_HBM_GBPS,
@@ -839,6 +911,8 @@ def main(argv=None) -> int:
             "algorithmic_bytes": nbytes,
         },
     }
+    log(f"{args.workload} contract steps: {line['ms_per_step']:.4f} ms per step (wall), "
+        f"{line['ms_per_step_gpu']:.4f} ms (events)")
     if not args.no_extras:
         log("extras: BF16, channels-last, VALU FWD/dX ...")
         line.update(extras(rt, args, dev, stream, x, w, dy, y, gk))
@@ -857,8 +931,7 @@ def main(argv=None) -> int:
         legs = {}
         for name in WORKLOADS:
             if name != args.workload:
-                legs[name] = workload_leg(rt, name, args, dev, stream)
-                log(f"{name}: {legs[name]['fwd_dx_dk_ms']:.4f} ms")
+                legs[name] = compact_leg(workload_leg(rt, name, args, dev, stream))
         line["baseline_configs"] = legs
     if not args.no_extras:
         log("long rows ...")

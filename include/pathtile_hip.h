@@ -124,6 +124,20 @@ int pt_dwconv1d_dx_f32_algo(const float* dy, const float* w, float* dx, int B, i
                             int L, int K, int waves_per_block, int algo, void* stream);
 
 /*
+ * Which kernel pt_dwconv1d_fwd_f32_algo (dx = 0) or pt_dwconv1d_dx_f32_algo
+ * (dx != 0) would launch for this call on the current device, with tensors
+ * 16-byte aligned (aligned16 != 0) or only 4-byte aligned: *kernel_id
+ * receives PT_KERNEL_FWD / _DX (VALU tile kernel), _FWD_STREAM / _DX_STREAM,
+ * _FWD_CG / _DX_CG (8-channel matrix cores) or _FWD_CG16 / _DX_CG16, or -1
+ * when B or H is 0. The same dispatch code runs as in a launch (environment
+ * variables included) and stops before launching; the return value is the
+ * status that call would return. No counterpart in the reference, which has
+ * one kernel per path: for harnesses that name or report the kernel.
+ */
+int pt_rows_kernel_id(int B, int H, int L, int K, int waves_per_block,
+                      int algo, int aligned16, int dx, int* kernel_id);
+
+/*
  * Input gradient dx = conv^T(dy, w).
  * Replaces dwconv1d_warptile_bwd_input in AmpereWarpRuntime.launch_bwd_input
  * (kernels/warp_tiled_ampere.py:749-770). Kernel choice as for the forward

@@ -56,6 +56,7 @@ SIGNATURES = {
     "pt_dwconv1d_dx_f32": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "pt_dwconv1d_fwd_f32_algo": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "pt_dwconv1d_dx_f32_algo": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "pt_rows_kernel_id": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, _ip]),
     "pt_dwconv1d_dk_atomic_f32": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "pt_dwconv1d_dk_det_workspace_bytes": (_i, [_i, _i, _i, _i, _i, _szp]),
     "pt_dwconv1d_dk_det_f32": (

@@ -639,7 +639,8 @@ static int rows_cg_channels_env() {
 }
 
 static int rows_cg_path(bool dx, const float* in, const float* w, float* out,
-                        int B, int H, int L, int K, void* stream) {
+                        int B, int H, int L, int K, void* stream,
+                        int* probe = nullptr) {
   const bool plain = rows_plain_loads(B, H, L);
   const bool a4 = L % 4 == 0;
   const long long tsteps = ((long long)B + kRowsCgStep - 1) / kRowsCgStep;
@@ -652,11 +653,19 @@ static int rows_cg_path(bool dx, const float* in, const float* w, float* out,
       rows_cg_lds_bytes(L, 16, 1) <= (size_t)max_lds_per_block()) {
     const RowsCgFn* t16 = a4 ? (plain ? kRowsCg16TablePL : kRowsCg16Table)
                              : (plain ? kRowsCg16TableUPL : kRowsCg16TableU);
+    if (probe) {
+      *probe = dx ? PT_KERNEL_DX_CG16 : PT_KERNEL_FWD_CG16;
+      return PT_OK;
+    }
     return rows_cg_launch(t16[dx ? 1 : 0], in, w, out, B, H, L, K, stream, 16,
                           rows_cg_lds_bytes(L, 16, 1), 1);
   }
   const RowsCgFn(*t8)[3] = a4 ? (plain ? kRowsCgTablePL : kRowsCgTable)
                               : (plain ? kRowsCgTableUPL : kRowsCgTableU);
+  if (probe) {
+    *probe = dx ? PT_KERNEL_DX_CG : PT_KERNEL_FWD_CG;
+    return PT_OK;
+  }
   return rows_cg_launch(t8[dx ? 1 : 0][mfma_index(L)], in, w, out, B, H, L, K,
                         stream, kRowsCgWaves, rows_cg_lds_bytes(L), 2, kRowsCgMinSteps);
 }
@@ -684,7 +693,12 @@ static bool stream_ok(int H, int L, int K, const void* in, const void* out) {
 // workgroups than fit at once; if that is more waves than there are spans,
 // every span gets its own wave instead.
 static int stream_path(bool dx, const float* in, const float* w, float* out,
-                       int B, int H, int L, int K, int wpb, void* stream) {
+                       int B, int H, int L, int K, int wpb, void* stream,
+                       int* probe = nullptr) {
+  if (probe) {
+    *probe = dx ? PT_KERNEL_DX_STREAM : PT_KERNEL_FWD_STREAM;
+    return PT_OK;
+  }
   const StreamFn fn =
       (rows_plain_loads(B, H, L) ? kStreamTablePL : kStreamTable)[dx ? 1 : 0][K - 1];
   const int threads = wpb * kWave;
@@ -730,21 +744,26 @@ static int rows_fronts(long long nwaves, long long ntiles, long long period) {
   return f;
 }
 
+// probe: when not NULL, nothing is launched; *probe receives the
+// PT_KERNEL_* id of the kernel the call would launch (-1: none, B or H = 0).
 static int rows_path(bool dx, const float* in, const float* w, float* out,
                      int B, int H, int L, int K, int wpb, void* stream,
-                     int forced = PT_ROWS_AUTO) {
+                     int forced = PT_ROWS_AUTO, int* probe = nullptr) {
   int st = check_shape(B, H, L, K);
   if (st != PT_OK) return st;
   if (!valid_wpb(wpb)) return PT_ERR_CONFIG;
   if (forced != PT_ROWS_AUTO && forced != PT_ROWS_VALU && forced != PT_ROWS_MATRIX)
     return PT_ERR_CONFIG;
-  if (B == 0 || H == 0) return PT_OK;  // empty tensors may have NULL data
+  if (B == 0 || H == 0) {  // empty tensors may have NULL data
+    if (probe) *probe = -1;
+    return PT_OK;
+  }
   if (!in || !w || !out) return PT_ERR_NULL;
   if (!aligned(in, 4) || !aligned(w, 4) || !aligned(out, 4))
     return PT_ERR_ALIGN;
   const RowsAlgo algo = rows_algo(B, H, L, K, forced);
   if (algo == kRowsMfma && rows_cg_ok(H, L, in, out))
-    return rows_cg_path(dx, in, w, out, B, H, L, K, stream);
+    return rows_cg_path(dx, in, w, out, B, H, L, K, stream, probe);
   // The VALU tile kernel: one 64-row LDS tile per wave. Its limits on the
   // waves per workgroup hold for the streaming kernel too, so both VALU
   // kernels accept the same launch configurations.
@@ -754,7 +773,7 @@ static int rows_path(bool dx, const float* in, const float* w, float* out,
   if (wpb * kWave > rows_max_threads(8 * (lbucket_index(L) + 1), vec))
     return PT_ERR_CONFIG;
   if (algo == kRowsStream && stream_ok(H, L, K, in, out))
-    return stream_path(dx, in, w, out, B, H, L, K, wpb, stream);
+    return stream_path(dx, in, w, out, B, H, L, K, wpb, stream, probe);
   const long long R = (long long)B * H;
   const long long ntiles = (R + kWave - 1) / kWave;
   const int wpc = rows_waves_per_cu(L, K, ntiles);
@@ -782,7 +801,11 @@ static int rows_path(bool dx, const float* in, const float* w, float* out,
   const long long Q = P / gcd_ll(P, wpb);  // blocks per channel period
   const bool periodic = nb == need || Q <= 1 || (nb >= Q && 4 * (nb % Q) <= nb);
   if (!periodic && algo != kRowsTile && stream_ok(H, L, K, in, out))
-    return stream_path(dx, in, w, out, B, H, L, K, wpb, stream);
+    return stream_path(dx, in, w, out, B, H, L, K, wpb, stream, probe);
+  if (probe) {
+    *probe = dx ? PT_KERNEL_DX : PT_KERNEL_FWD;
+    return PT_OK;
+  }
   if (periodic && nb < need && Q > 1) nb = nb / Q * Q;
   if (nb < 1) nb = 1;
   if (nb >= (1LL << 31)) return PT_ERR_SHAPE;
@@ -1140,6 +1163,17 @@ int pt_dwconv1d_dx_f32(const float* dy, const float* w, float* dx, int B,
 int pt_dwconv1d_fwd_f32_algo(const float* x, const float* w, float* y, int B, int H,
                              int L, int K, int waves_per_block, int algo, void* stream) {
   return pt::rows_path(false, x, w, y, B, H, L, K, waves_per_block, stream, algo);
+}
+
+int pt_rows_kernel_id(int B, int H, int L, int K, int waves_per_block,
+                      int algo, int aligned16, int dx, int* kernel_id) {
+  if (!kernel_id) return PT_ERR_NULL;
+  *kernel_id = -1;
+  // Stand-in addresses with the requested alignment; the probe returns
+  // before anything is launched, so they are never dereferenced.
+  const float* p = reinterpret_cast<const float*>((uintptr_t)(aligned16 ? 256 : 260));
+  return pt::rows_path(dx != 0, p, p, const_cast<float*>(p), B, H, L, K,
+                       waves_per_block, nullptr, algo, kernel_id);
 }
 
 int pt_dwconv1d_dx_f32_algo(const float* dy, const float* w, float* dx, int B, int H,

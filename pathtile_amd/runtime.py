@@ -300,6 +300,48 @@ def _stream_handle(device: torch.device) -> ctypes.c_void_p:
 # PT_ROWS_AUTO, PT_ROWS_VALU and PT_ROWS_MATRIX.
 ROWS_ALGOS = {"auto": _lib.PT_ROWS_AUTO, "valu": _lib.PT_ROWS_VALU, "mfma": _lib.PT_ROWS_MATRIX}
 
+# PT_KERNEL_* ids of the FWD / dX kernels -> (kernel template, matrix cores?)
+ROWS_KERNELS = {
+    _lib.PT_KERNEL_FWD: ("dwconv_rows_kernel<FWD>", False),
+    _lib.PT_KERNEL_DX: ("dwconv_rows_kernel<DX>", False),
+    _lib.PT_KERNEL_FWD_STREAM: ("dwconv_stream_kernel<FWD>", False),
+    _lib.PT_KERNEL_DX_STREAM: ("dwconv_stream_kernel<DX>", False),
+    _lib.PT_KERNEL_FWD_CG: ("dwconv_rows_cg_kernel<FWD>", True),
+    _lib.PT_KERNEL_DX_CG: ("dwconv_rows_cg_kernel<DX>", True),
+    _lib.PT_KERNEL_FWD_CG16: ("dwconv_rows_cg_kernel<FWD, 16 channels>", True),
+    _lib.PT_KERNEL_DX_CG16: ("dwconv_rows_cg_kernel<DX, 16 channels>", True),
+}
+
+
+def rows_kernel_id(B: int, H: int, L: int, K: int, dx: bool = False,
+                   waves_per_block: int = 4, algo: str = "auto",
+                   aligned16: bool = True) -> int:
+    """PT_KERNEL_* id of the kernel a FWD (dx=False) or dX launch of this
+    shape would run on the current device (-1: nothing, B or H = 0); the
+    library's dispatch itself answers (pt_rows_kernel_id), so no restated
+    rule can drift from it. Raises ValueError where the launch would."""
+    out = ctypes.c_int(-1)
+    st = _lib.load().pt_rows_kernel_id(int(B), int(H), int(L), int(K), int(waves_per_block),
+                                       ROWS_ALGOS[algo], int(bool(aligned16)), int(bool(dx)),
+                                       ctypes.byref(out))
+    _lib.check(st, "pt_rows_kernel_id")
+    return int(out.value)
+
+
+def rows_kernel_name(B: int, H: int, L: int, K: int, dx: bool = False,
+                     waves_per_block: int = 4, algo: str = "auto",
+                     aligned16: bool = True) -> str:
+    """Name of the kernel rows_kernel_id reports ("none" for empty calls)."""
+    kid = rows_kernel_id(B, H, L, K, dx, waves_per_block, algo, aligned16)
+    return ROWS_KERNELS[kid][0] if kid >= 0 else "none"
+
+
+def rows_on_matrix_cores(B: int, H: int, L: int, K: int, dx: bool = False,
+                         waves_per_block: int = 4, aligned16: bool = True) -> bool:
+    """True where the library serves this FWD/dX call on the matrix cores."""
+    kid = rows_kernel_id(B, H, L, K, dx, waves_per_block, "auto", aligned16)
+    return kid >= 0 and ROWS_KERNELS[kid][1]
+
 
 class HipWarpRuntime:
     """Owns the launch configuration of the three paths and launches them
@@ -757,6 +799,15 @@ class HipWarpRuntime:
         (collector or KERNEL_EVENTS).launch("bwd_weight_long", launch, {"B": B, "H": H, "L": L, "K": K})
 
     # ------------------------------------------------------------- reporting
+    def rows_kernel(self, B: int, H: int, L: int, K: int, dx: bool = False,
+                    aligned16: bool = True) -> str:
+        """Name of the kernel this runtime's FWD (or dX) launch would run
+        for the shape (the library's own dispatch, queried through
+        pt_rows_kernel_id on the current device)."""
+        wpb = self.dx_waves_per_block if dx else self.waves_per_block
+        return rows_kernel_name(B, H, L, K, dx=dx, waves_per_block=wpb,
+                                algo=self.rows_algo, aligned16=aligned16)
+
     def kernel_attributes(self, kernel_id: int, L: int, K: int) -> dict[str, int]:
         regs, lds, scratch, maxt = (ctypes.c_int(0) for _ in range(4))
         st = self._lib.pt_kernel_attributes(kernel_id, L, K, ctypes.byref(regs),

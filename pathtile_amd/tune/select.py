@@ -20,7 +20,6 @@ import math
 from datetime import datetime
 from typing import Iterable
 
-from .. import rows_rule
 
 PHASES = ("fwd", "bwd_input", "bwd_weight")
 POLICY_KEYS = {
@@ -209,8 +208,11 @@ KNOB_INERT_RULE = (
 def fwd_dx_knob_inert(H: int, L: int, K: int, B: int) -> bool:
     """True where the FWD/dX knob cannot change the kernel: where the
     library's matrix-core rule serves a 16-byte aligned call (the tuner's
-    tensors are torch allocations), pathtile_amd.rows_rule."""
-    return rows_rule.matrix_cores_serve(B, H, L, K)
+    tensors are torch allocations), as the library's dispatch reports it
+    (pt_rows_kernel_id)."""
+    from .. import runtime
+
+    return runtime.rows_on_matrix_cores(B, H, L, K)
 
 
 def path_regret(rows: list[dict], policy: dict[str, int]) -> dict[str, dict]:

@@ -415,3 +415,56 @@ def test_noalloc_dk_validation_and_scratch_limit_before_launch(lib):
     assert "static scratch" in _lib.status_string(_lib.PT_ERR_SCRATCH)
     with pytest.raises(ValueError, match="static scratch"):
         _lib.check(_lib.PT_ERR_SCRATCH, "pt_dwconv1d_dk_det_f32_noalloc")
+
+
+def test_rows_kernel_query_matches_the_restated_rule(lib, monkeypatch):
+    """pt_rows_kernel_id runs the library's own FWD/dX dispatch up to the
+    launch. Its matrix-core / VALU answer must equal the Python restatement
+    (pathtile_amd.rows_rule, used where no device is present) at every row
+    length and tap count, in each size class the rule separates: calls of
+    fewer than 2^17 rows, of at least 2^18 rows, tensors of at most and above
+    256 MiB, H above 128, H not a multiple of 8. The matrix-core choice does
+    not depend on device queries, so this holds without a GPU."""
+    from pathtile_amd import rows_rule, runtime
+
+    monkeypatch.delenv("PATHTILE_ROWS_ALGO", raising=False)
+    monkeypatch.delenv("PATHTILE_ROWS_CHANNELS", raising=False)
+    mismatches = []
+    for B, H in ((1000, 96), (2048, 64), (16384, 128), (4096, 256), (32768, 256), (3000, 36)):
+        for L in range(1, 49):
+            for K in range(1, 49):
+                lib_mfma = runtime.rows_on_matrix_cores(B, H, L, K)
+                if lib_mfma != rows_rule.matrix_cores_serve(B, H, L, K):
+                    mismatches.append((B, H, L, K, lib_mfma))
+    assert not mismatches, mismatches[:20]
+
+
+def test_rows_kernel_query_ids_and_errors(lib, monkeypatch):
+    """The query names a kernel of its path, honours the forced choices,
+    reports -1 for empty calls and returns the launch's error codes."""
+    from pathtile_amd import _lib, runtime
+
+    monkeypatch.delenv("PATHTILE_ROWS_ALGO", raising=False)
+    fwd_ids = {_lib.PT_KERNEL_FWD, _lib.PT_KERNEL_FWD_STREAM, _lib.PT_KERNEL_FWD_CG,
+               _lib.PT_KERNEL_FWD_CG16}
+    dx_ids = {_lib.PT_KERNEL_DX, _lib.PT_KERNEL_DX_STREAM, _lib.PT_KERNEL_DX_CG,
+              _lib.PT_KERNEL_DX_CG16}
+    assert runtime.rows_kernel_id(16384, 128, 48, 48) in fwd_ids
+    assert runtime.rows_kernel_id(16384, 128, 48, 48, dx=True) in dx_ids
+    assert runtime.rows_kernel_id(16384, 128, 48, 48, algo="valu") == _lib.PT_KERNEL_FWD
+    assert runtime.rows_kernel_id(257, 8, 48, 4, algo="mfma") == _lib.PT_KERNEL_FWD_CG
+    # the matrix cores need H % 8 == 0 and 16-byte aligned tensors
+    assert runtime.rows_kernel_id(257, 12, 48, 48, algo="mfma") == _lib.PT_KERNEL_FWD
+    assert runtime.rows_kernel_id(16384, 128, 48, 48, aligned16=False) == _lib.PT_KERNEL_FWD
+    assert runtime.rows_kernel_id(0, 128, 48, 48) == -1
+    assert runtime.rows_kernel_name(0, 128, 48, 48) == "none"
+    monkeypatch.setenv("PATHTILE_ROWS_ALGO", "valu")
+    assert runtime.rows_kernel_name(16384, 128, 48, 48) == "dwconv_rows_kernel<FWD>"
+    for bad in ((16, 8, 49, 4), (16, 8, 48, 49), (16, 8, 0, 4)):
+        with pytest.raises(ValueError):
+            runtime.rows_kernel_id(*bad)
+    with pytest.raises(ValueError):
+        runtime.rows_kernel_id(16, 8, 48, 4, waves_per_block=3)
+    out = ctypes.c_int(0)
+    assert lib.pt_rows_kernel_id(16, 8, 48, 4, 4, 0, 1, 0, None) == _lib.PT_ERR_NULL
+    assert lib.pt_rows_kernel_id(16, 8, 48, 4, 4, 7, 1, 0, ctypes.byref(out)) == _lib.PT_ERR_CONFIG

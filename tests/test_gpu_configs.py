@@ -30,7 +30,7 @@ import pytest
 import torch
 
 import oracle
-from pathtile_amd import rows_rule
+from pathtile_amd import runtime as _runtime
 
 pytestmark = pytest.mark.gpu
 
@@ -49,8 +49,8 @@ def rt():
 
 def _valu_serves(B, H, L, K):
     """The VALU kernel serves a 16-byte aligned call wherever the library's
-    rule does not pick the matrix cores (pathtile_amd.rows_rule)."""
-    return not rows_rule.matrix_cores_serve(B, H, L, K)
+    dispatch does not pick the matrix cores (pt_rows_kernel_id)."""
+    return not _runtime.rows_on_matrix_cores(B, H, L, K)
 
 
 def _full_size_case(rt, B, H, L, K, seed, monkeypatch):

@@ -1,12 +1,14 @@
 """The library's FWD/dX kernel choice on the GPU, on both sides of each
-threshold of the rule (rows_mfma_min_k in csrc/dwconv1d_abi.hip, restated in
-pathtile_amd/rows_rule.py): where the restated rule says the VALU kernels
-serve, sampled rows must be the reference's fmaf chain bit for bit; where it
-says the matrix cores serve, they must differ from that chain somewhere (the
-matrix cores sum in their own order) and stay within 1e-5 of FP64. A
-disagreement between the library and its restatement fails one of the two.
-The shapes cover the size classes the rule separates: calls of fewer than
-2^17 rows, tensors of at most 256 MiB and above, and H above 128 at L = 48."""
+threshold of the rule (rows_algo / rows_mfma_min_k in csrc/dwconv1d_abi.hip,
+restated in pathtile_amd/rows_rule.py): the library's own answer
+(pt_rows_kernel_id) must equal the restatement; where they say the VALU
+kernels serve, sampled rows must be the reference's fmaf chain bit for bit;
+where they say the matrix cores serve, they must differ from that chain
+somewhere (the matrix cores sum in their own order) and stay within 1e-5 of
+FP64. The shapes cover every row length with a threshold of its own and the
+size classes the rule separates: calls of fewer than 2^17 rows, tensors of at
+most 256 MiB and above, H above 128 at L = 48, rows of L % 4 != 0 from 2^18
+rows (B x H) and below, and rows shorter than 16."""
 
 from __future__ import annotations
 
@@ -15,7 +17,7 @@ import pytest
 import torch
 
 import oracle
-from pathtile_amd import rows_rule
+from pathtile_amd import rows_rule, runtime
 
 pytestmark = pytest.mark.gpu
 
@@ -33,6 +35,14 @@ CASES = [
     (8192, 128, 48, 8), (8192, 128, 48, 9),        # L48, <= 256 MiB, H <= 128: K = 9
     (4096, 256, 48, 16), (4096, 256, 48, 17),      # L48, H > 128: K = 17
     (16384, 128, 48, 16), (16384, 128, 48, 17),    # L48 above 256 MiB: K = 17
+    (16384, 128, 20, 8), (16384, 128, 20, 9),      # L20 from K = 9
+    (16384, 128, 28, 8), (16384, 128, 28, 9),      # L28 from K = 9
+    (16384, 128, 32, 8), (16384, 128, 32, 9),      # L32 from K = 9
+    (16384, 128, 36, 16), (16384, 128, 36, 17),    # L36 from K = 17
+    (16384, 128, 44, 8), (16384, 128, 44, 9),      # L44 from K = 9
+    (4095, 64, 37, 6), (4096, 64, 37, 6),          # L % 4 != 0: from 2^18 rows
+    (1000, 96, 37, 8), (1000, 96, 37, 9),          # below: 5 (48 / 37)^2 FMAs per output
+    (16384, 64, 12, 12),                           # L < 16, L % 4 == 0: VALU
 ]
 
 
@@ -49,6 +59,8 @@ def rt():
 def test_kernel_choice_matches_the_restated_rule(rt, case):
     B, H, L, K = case
     mfma = rows_rule.matrix_cores_serve(B, H, L, K)
+    assert runtime.rows_on_matrix_cores(B, H, L, K) == mfma
+    assert runtime.rows_on_matrix_cores(B, H, L, K, dx=True) == mfma
     print(f"[case] rule B={B} H={H} L={L} K={K} matrix_cores={mfma}", flush=True)
     g = torch.Generator().manual_seed(1000 + B + H + L + K)
     x = torch.randn(B, H, L, generator=g)

@@ -24,6 +24,7 @@ import torch
 
 import oracle
 from pathtile_amd import rows_rule
+from pathtile_amd import runtime as _runtime
 
 pytestmark = pytest.mark.gpu
 
@@ -105,12 +106,12 @@ SHAPES = [
 def _mfma_serves(B, H, L, K, algo):
     """Whether the channel-group matrix-core FWD/DX kernel serves a 16-byte
     aligned call: the layout must allow it (H % 8 == 0, any L) and, unless
-    forced, the library's rule must pick it (pathtile_amd.rows_rule)."""
+    forced, the library's dispatch must pick it (pt_rows_kernel_id)."""
     if algo in ("valu", "tile", "stream") or H % 8:
         return False
     if algo == "mfma":
         return True
-    return rows_rule.matrix_cores_serve(B, H, L, K)
+    return _runtime.rows_on_matrix_cores(B, H, L, K)
 
 
 @pytest.mark.parametrize("algo", ["auto", "valu", "tile", "stream", "mfma"])
@@ -702,6 +703,8 @@ def test_runtime_rows_algo_overrides_the_environment(env, monkeypatch):
         monkeypatch.setenv("PATHTILE_ROWS_ALGO", env)
     r_valu = runtime.HipWarpRuntime(rows_algo="valu")
     B, H, L, K = 64, 16, 48, 48
+    # the default rule (the environment aside; pinned to the library's
+    # dispatch in tests/test_abi_cpu.py)
     assert rows_rule.matrix_cores_serve(B, H, L, K)
     x, w, dy = _inputs(B, H, L, K, seed=31)
     xd, wd, dyd = _dev(x, w, dy)

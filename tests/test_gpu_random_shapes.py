@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import oracle
-from pathtile_amd import rows_rule
+from pathtile_amd import runtime as _runtime
 
 pytestmark = pytest.mark.gpu
 
@@ -73,7 +73,7 @@ def test_random_shape(rt, case):
     y, dx = y.cpu().numpy(), dx.cpu().numpy()
     assert oracle.normalized_max_abs(y, oracle.fwd_f64(x, w)) < FWD_TOL
     assert oracle.normalized_max_abs(dx, oracle.dx_f64(dy, w)) < FWD_TOL
-    if mis or not rows_rule.matrix_cores_serve(B, H, L, K):
+    if mis or not _runtime.rows_on_matrix_cores(B, H, L, K):
         assert np.array_equal(y, oracle.fwd_f32_refchain(x, w))
         assert np.array_equal(dx, oracle.dx_f32_refchain(dy, w))
 
