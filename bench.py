@@ -623,20 +623,17 @@ def extras(rt, args, dev, stream, x, w, dy, y, gk) -> dict:
         }, **prot)
         del xb, dyb, yb, dxb, y32, sets
         nb = 2 * B * H * L * 2 + H * K * 4
+        def rows3(tt):
+            return {ph: [round(v["ms"], 5), round(v["std_ms"], 5),
+                         round(100 * nb / (v["ms"] / 1e3) / 1e9 / PEAK_HBM_GBPS, 2)]
+                    for ph, v in tt.items()}
         out["bf16_io"] = {
-            "paths": {ph: {"ms": round(v["ms"], 5), "std_ms": round(v["std_ms"], 5),
-                           "gbps": round(nb / (v["ms"] / 1e3) / 1e9, 1),
-                           "pct_peak": round(100 * nb / (v["ms"] / 1e3) / 1e9 / PEAK_HBM_GBPS, 2)}
-                      for ph, v in t.items()},
+            "paths": rows3(t),
             "fwd_dx_dk_ms": round(t["fwd"]["ms"] + t["bwd_input"]["ms"] + t["bwd_weight"]["ms"], 5),
-            "rotated_buffer_sets": {
-                "sets": nsets,
-                "paths": {ph: {"ms": round(v["ms"], 5), "std_ms": round(v["std_ms"], 5),
-                               "pct_peak": round(100 * nb / (v["ms"] / 1e3) / 1e9 / PEAK_HBM_GBPS, 2)}
-                          for ph, v in t_cold.items()},
-            },
+            "paths_rotated": rows3(t_cold),
+            "rotated_sets": nsets,
             "gate_vs_fp32_path": float(f"{bf16_gate:.3e}"),
-            "note": "x, dY, y, dX bf16; taps, dK fp32; bytes 2BHL*2 + HK*4 per path",
+            "note": "[ms, std, % of 8 TB/s]; x, dY, y, dX bf16, taps and dK fp32; bytes 2BHL*2 + HK*4",
         }
 
     # Channels-last dK through the Flash-DWC bridge ABI (flash_dk_fp32).
@@ -723,16 +720,15 @@ def long_rows_leg(rt, args, dev, stream) -> dict:
                   "bwd_weight": "BF16_MFMA_FLOP_DK"}
 
     def paths(t, split):
+        # [ms, std ms, useful TFLOP/s, % of 8 TB/s, fraction of the BF16
+        # matrix peak the split kernels issue]
         out = {}
         for ph, v in t.items():
             s = v["ms"] / 1e3
-            row = {"ms": round(v["ms"], 5), "std_ms": round(v["std_ms"], 5),
-                   "tflops_useful": round(useful / s / 1e12, 2),
-                   "hbm_pct_peak": round(100 * nbytes / s / 1e9 / PEAK_HBM_GBPS, 2)}
+            row = [round(v["ms"], 5), round(v["std_ms"], 5), round(useful / s / 1e12, 2),
+                   round(100 * nbytes / s / 1e9 / PEAK_HBM_GBPS, 2)]
             if split and issued:
-                f = issued[issued_key[ph]]
-                row["tflops_bf16_issued"] = round(f / s / 1e12, 1)
-                row["frac_bf16_mfma_peak"] = round(f / s / 1e12 / PEAK_BF16_MFMA_TFLOPS, 4)
+                row.append(round(issued[issued_key[ph]] / s / 1e12 / PEAK_BF16_MFMA_TFLOPS, 4))
             out[ph] = row
         return out
 
@@ -759,13 +755,11 @@ def long_rows_leg(rt, args, dev, stream) -> dict:
         "config": {"B": LB, "H": LH, "L": LL, "K": LK},
         "paths": paths(t_split, True),
         "fwd_dx_dk_ms": round(sum(v["ms"] for v in t_split.values()), 5),
-        "kernels": {"fwd": "dwconv_rows_long_s3_kernel<192, 192, false, true>",
-                    "bwd_input": "dwconv_rows_long_s3_kernel<192, 192, true, true>",
-                    "bwd_weight": "dwconv_dk_long_s3_kernel<192, true>"},
         "fp32_mfma_kernels_ms": {k: round(v["ms"], 5) for k, v in t_fp32.items()},
         "check_fwd_first_256_samples": {k: float(f"{v:.3e}") for k, v in gate.items()},
-        "note": "BF16 matrix cores on 3-way split FP32 operands; issued BF16 flops from "
-                "profiles/pmc_mfma_long_l192_k192.md; fp32_mfma_kernels_ms: PATHTILE_LONG_ALGO=fp32",
+        "note": "[ms, std, useful TFLOP/s, % of 8 TB/s, issued BF16 / 2.5 PFLOP/s "
+                "(profiles/pmc_mfma_long_l192_k192.md)]; BF16 matrix cores on 3-way split "
+                "FP32 operands; fp32_mfma_kernels_ms: PATHTILE_LONG_ALGO=fp32",
     }
 
 
@@ -943,6 +937,18 @@ def main(argv=None) -> int:
         log("cpu baseline ...")
         line["cpu_baseline"] = cpu_baseline(x_cpu, w_cpu, dy_cpu, args.cpu_runs)
     rt.close()
+    # The key blocks last: a reader that keeps only the end of the output
+    # still sees P's per-path numbers, the rotated control and the checks.
+    last = ("protocol", "baseline_configs", "paths_rotated", "paths", "check_of_timed_outputs",
+            "cpu_baseline")
+    line = {k: v for k, v in line.items() if k not in last} | \
+        {k: line[k] for k in last if k in line}
+    summary = [f"{args.workload} {path_line(paths)}"]
+    for name, leg in line.get("baseline_configs", {}).items():
+        summary.append(name + " " + ", ".join(
+            f"{PATH_TAGS.get(k, k)} {v[0]:.4f} ms ({v[2]:.1f}%)" for k, v in leg["paths"].items()
+            if k in ("fwd", "bwd_input", "bwd_weight")))
+    log("summary: " + " | ".join(summary))
     print(json.dumps(line), flush=True)
     return 0
 

@@ -189,13 +189,16 @@ int pt_dwconv1d_dk_det_f32(const float* dy, const float* x, float* dk,
  * loops, harnesses that forbid hipMalloc). Same kernels, partial order and
  * result bits as pt_dwconv1d_dk_det_f32 with the same threads_per_block;
  * the partials go to a static device array of PT_DK_SCRATCH_BYTES (8 MiB)
- * that each device holds until the process ends. A call whose partials
- * (H * K * 4 bytes per batch range; at most the size
- * pt_dwconv1d_dk_det_workspace_bytes reports) exceed it returns
- * PT_ERR_SCRATCH. Every call on a device shares that
- * device's array: calls that overlap on one device (two streams, two host
- * threads) race and must be ordered by the caller. Each call overwrites
- * every partial it reads, so nothing needs clearing between calls.
+ * that each device holds until the process ends. A call for which
+ * pt_dwconv1d_dk_det_workspace_bytes reports more than that returns
+ * PT_ERR_SCRATCH; the limit follows from the shape and threads_per_block
+ * alone and is checked before any device query. Every call on a device
+ * shares that device's array: calls that overlap on one device (two
+ * streams, two host threads) race and must be ordered by the caller. Each
+ * call overwrites every partial it reads, so nothing needs clearing
+ * between calls. The first call on a device looks up the array's address
+ * and the kernels' occupancy (HIP queries that are not stream work): make
+ * one call on each device before capturing calls into a HIP graph.
  */
 int pt_dwconv1d_dk_det_f32_noalloc(const float* dy, const float* x, float* dk,
                                    int B, int H, int L, int K,

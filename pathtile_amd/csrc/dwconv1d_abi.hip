@@ -1259,12 +1259,17 @@ int pt_dwconv1d_dk_det_f32_noalloc(const float* dy, const float* x, float* dk,
   if (B == 0) return pt::zero_fill(dk, H * K, stream);
   if (!dy || !x) return PT_ERR_NULL;
   if (!pt::aligned(dy, 4) || !pt::aligned(x, 4)) return PT_ERR_ALIGN;
+  // The limit is the shape-only partial count (the size
+  // pt_dwconv1d_dk_det_workspace_bytes reports), decided before any device
+  // query; the launch's own count is at most that (the device cap only
+  // lowers it), so the partials always fit.
+  const pt::DkGeom g0 = pt::dk_geometry(B, H, L, K, threads_per_block, true);
+  if ((size_t)H * (size_t)K * (size_t)g0.nbt * sizeof(float) > (size_t)PT_DK_SCRATCH_BYTES)
+    return PT_ERR_SCRATCH;
   const pt::DkGeom g =
       pt::dk_geometry(B, H, L, K, threads_per_block,
                       pt::aligned(dy, 16) && pt::aligned(x, 16), 4, true);
   if (g.nblocks >= (1LL << 31)) return PT_ERR_SHAPE;
-  const size_t need = (size_t)H * (size_t)K * (size_t)g.nbt * sizeof(float);
-  if (need > (size_t)PT_DK_SCRATCH_BYTES) return PT_ERR_SCRATCH;
   float* partials = nullptr;
   st = pt::scratch_address(&partials);
   if (st != PT_OK) return st;

@@ -22,6 +22,7 @@ from __future__ import annotations
 import ctypes
 import math
 import threading
+from collections import OrderedDict
 from dataclasses import dataclass
 from typing import Any, Callable
 
@@ -71,6 +72,8 @@ DEFAULT_BWDK_BLOCK = int(_POLICY.get("dk_threads_per_block", 128))
 
 ALLOWED_WAVES = (1, 2, 4, 8, 16)
 MAX_BWDK_BLOCK = 768
+# Deterministic-dK workspaces a runtime keeps, one per (device, stream).
+WORKSPACE_STREAMS = 4
 
 
 # =============================================================================
@@ -182,6 +185,10 @@ def estimate_gpu_occupancy(
         "limiting_resources_est": ",".join(limiting),
         "gpu_profile": profile.key,
     }
+
+
+# The reference's backward-compatible name (kernels/warp_tiled_ampere.py:260).
+estimate_ampere_occupancy = estimate_gpu_occupancy
 
 
 def minimum_algorithmic_bytes(B: int, H: int, L: int, K: int) -> int:
@@ -396,12 +403,23 @@ class HipWarpRuntime:
         self.rows_algo = rows_algo
         self._rows_algo_id = ROWS_ALGOS[rows_algo]
         self.technique = "WaveRow-mi355x"
-        self.profile = MI355X
+        # The device current at construction, as the reference records it
+        # (:662-664); launches still follow each call's tensors. The profile
+        # is detected from it (gfx950 only) where a GPU is present.
+        if torch.cuda.is_available():
+            self.device_id: int | None = torch.cuda.current_device()
+            self.device: torch.device | None = torch.device("cuda", self.device_id)
+            self.profile = detect_gpu_profile(self.device_id)
+        else:
+            self.device_id = None
+            self.device = None
+            self.profile = MI355X
         self._lib = _lib.load()
         self._closed = False
         self._ws_lock = threading.Lock()
-        # (device index, stream handle) -> (stream, workspace)
-        self._workspaces: dict[tuple[int, int], tuple[Any, torch.Tensor]] = {}
+        # (device index, stream handle) -> (stream, workspace), least
+        # recently used first
+        self._workspaces: OrderedDict[tuple[int, int], tuple[Any, torch.Tensor]] = OrderedDict()
 
     # ------------------------------------------------------------------ checks
     @staticmethod
@@ -534,8 +552,12 @@ class HipWarpRuntime:
         device, and each stream keeps its own buffer, so launches on two
         streams never share partials. The buffer is allocated from torch's
         caching allocator while that stream is current, so when it is
-        replaced by a larger one, its memory returns to that stream's pool
-        and is reused only by work ordered after the launches that read it."""
+        replaced by a larger one, or dropped, its memory returns to that
+        stream's pool and is reused only by work ordered after the launches
+        that read it. At most WORKSPACE_STREAMS (device, stream) buffers are
+        kept, the least recently used dropped first, so callers that make
+        short-lived streams do not pile up workspaces; an entry holds its
+        stream, so no live entry's handle can be recycled by a new stream."""
         stream = torch.cuda.current_stream(device)
         key = (device.index if device.index is not None else torch.cuda.current_device(),
                int(stream.cuda_stream))
@@ -545,8 +567,10 @@ class HipWarpRuntime:
                 with torch.cuda.stream(stream):
                     ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
                 self._workspaces[key] = (stream, ws)
-                return ws
-            return entry[1]
+            self._workspaces.move_to_end(key)
+            while len(self._workspaces) > WORKSPACE_STREAMS:
+                self._workspaces.popitem(last=False)
+            return self._workspaces[key][1]
 
     def launch_bwd_weight_deterministic(
         self,
@@ -558,7 +582,10 @@ class HipWarpRuntime:
     ) -> None:
         """Two-pass dK: per-batch-tile partials, then a fixed-order reduction
         that overwrites gk (no zero-init). Bitwise reproducible for a fixed
-        shape and bwdk_block (kernels/warp_tiled_noatomic_optimized.py:1473)."""
+        shape, bwdk_block and input alignment (16-byte aligned or not) on a
+        given device: the range count that partitions the sums may be capped
+        by the device's CU count and the kernel's occupancy
+        (kernels/warp_tiled_noatomic_optimized.py:1473)."""
         self._check_open()
         K = int(K)
         B, H, L = self._check_bwd_weight(gy, x, gk, K)
@@ -998,7 +1025,7 @@ __all__ = [
     "DEFAULT_BWDK_BTILE", "DEFAULT_BWDK_KPACK", "DEFAULT_BWDK_BLOCK",
     "GPUProfile", "GPU_PROFILES", "MI355X", "detect_gpu_profile",
     "ceil_div", "round_up", "max_abs_diff", "normalized_max_abs",
-    "estimate_gpu_occupancy", "minimum_algorithmic_bytes",
+    "estimate_gpu_occupancy", "estimate_ampere_occupancy", "minimum_algorithmic_bytes",
     "algorithmic_bandwidth_gbps", "useful_flops",
     "KernelEventCollector", "KERNEL_EVENTS", "summarize_kernel_times",
     "HipWarpRuntime", "AmpereWarpRuntime",

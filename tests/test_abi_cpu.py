@@ -389,9 +389,10 @@ def test_xcd_remap_is_a_bijection():
 def test_noalloc_dk_validation_and_scratch_limit_before_launch(lib):
     """pt_dwconv1d_dk_det_f32_noalloc checks shape, config, NULL, alignment
     and then its static scratch (PT_DK_SCRATCH_BYTES of partials) before any
-    launch: a shape whose partials exceed it even at one sample range
-    (H * K * 4 bytes > 8 MiB) is refused with PT_ERR_SCRATCH, for 16-byte
-    aligned (channel-group) and 4-byte aligned (per-channel) inputs alike."""
+    device query or launch: a shape whose workspace size (the shape-only
+    partial count pt_dwconv1d_dk_det_workspace_bytes reports) exceeds it is
+    refused with PT_ERR_SCRATCH, for 16-byte aligned (channel-group) and
+    4-byte aligned (per-channel) inputs alike."""
     from pathtile_amd import _lib
 
     buf = (ctypes.c_ubyte * 4096)()
@@ -412,6 +413,15 @@ def test_noalloc_dk_validation_and_scratch_limit_before_launch(lib):
     assert need.value > _lib.PT_DK_SCRATCH_BYTES
     assert fn(pa, pb, pc, B, H, L, K, 128, S) == _lib.PT_ERR_SCRATCH
     assert fn(mis[0], mis[1], pc, B, H, L, K, 128, S) == _lib.PT_ERR_SCRATCH
+    # The limit is the size the workspace query reports, whatever one range
+    # needs: 8 ranges of 8192 * 48 taps (1.5 MiB each, 12 MiB in all) are
+    # refused; 8 ranges of 4096 * 48 (6 MiB) pass the check (and then need a
+    # device, which this host lacks).
+    for H2, refused in ((8192, True), (4096, False)):
+        assert lib.pt_dwconv1d_dk_det_workspace_bytes(64, H2, 8, 48, 128, ctypes.byref(need)) == 0
+        assert (need.value > _lib.PT_DK_SCRATCH_BYTES) == refused
+        st = fn(pa, pb, pc, 64, H2, 8, 48, 128, S)
+        assert (st == _lib.PT_ERR_SCRATCH) == refused, st
     assert "static scratch" in _lib.status_string(_lib.PT_ERR_SCRATCH)
     with pytest.raises(ValueError, match="static scratch"):
         _lib.check(_lib.PT_ERR_SCRATCH, "pt_dwconv1d_dk_det_f32_noalloc")

@@ -26,8 +26,26 @@ def test_reference_names_exist():
                  "DEFAULT_B", "DEFAULT_H", "DEFAULT_L", "DEFAULT_K",
                  "DEFAULT_WARPS_PER_BLOCK", "DEFAULT_BWDK_BTILE", "DEFAULT_BWDK_KPACK",
                  "DEFAULT_BWDK_BLOCK", "minimum_algorithmic_bytes", "normalized_max_abs",
-                 "configure_torch"):
+                 "configure_torch", "validate_correctness", "benchmark_kernels",
+                 "print_device_report", "estimate_ampere_occupancy",
+                 "estimate_gpu_occupancy", "summarize_kernel_times"):
         assert hasattr(wta, name), name
+        assert name in wta.__all__, name
+    # the reference's alias (kernels/warp_tiled_ampere.py:260)
+    assert wta.estimate_ampere_occupancy is wta.estimate_gpu_occupancy
+    # the harness helpers take the reference's parameters, in its order
+    import inspect
+
+    assert list(inspect.signature(wta.validate_correctness).parameters) == [
+        "output_dir", "cases", "seed"]
+    assert list(inspect.signature(wta.benchmark_kernels).parameters) == [
+        "runtime", "output_dir", "B", "H", "L", "K", "warmup", "runs", "seed"]
+    assert list(inspect.signature(wta.print_device_report).parameters) == ["runtime"]
+    # the runtime records its device (None without a GPU)
+    r = wta.HipWarpRuntime()
+    assert hasattr(r, "device_id") and hasattr(r, "device")
+    if not torch.cuda.is_available():
+        assert r.device_id is None and r.device is None
 
 
 def test_legacy_constants():

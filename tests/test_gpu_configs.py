@@ -20,7 +20,8 @@ own validation shapes, and on every tuner candidate (marked ``gpu``).
   validates before it times (benchmark/benchmark_pathtile_candidate_sweep.py:
   153-243).
 * The deterministic dK launched on two streams at once: each stream keeps
-  its own workspace, so both results equal the single-stream bits.
+  its own workspace, so both results equal the single-stream bits; on many
+  short-lived streams the runtime keeps a bounded number of workspaces.
 """
 
 from __future__ import annotations
@@ -267,4 +268,32 @@ def test_deterministic_dk_on_two_streams():
         assert torch.equal(o, g)
     keys = {k[1] for k in r._workspaces}
     assert {int(s.cuda_stream) for s in streams} <= keys
+    r.close()
+
+
+def test_deterministic_dk_workspaces_are_bounded():
+    """A caller that launches on many short-lived streams keeps at most
+    WORKSPACE_STREAMS workspaces alive (least recently used dropped), and
+    every launch keeps the single-stream bits."""
+    from pathtile_amd import runtime
+
+    r = runtime.HipWarpRuntime()
+    B, H, L, K = 4096, 64, 48, 24
+    print(f"[case] many streams B={B} H={H} L={L} K={K}", flush=True)
+    x, w, dy = oracle.make_inputs(B, H, L, K, seed=95)
+    xd, dyd = x.cuda(), dy.cuda()
+    g = torch.empty(H, K, device="cuda")
+    r.launch_bwd_weight_deterministic(dyd, xd, g, K)
+    torch.cuda.synchronize()
+    main = torch.cuda.current_stream()
+    for i in range(3 * runtime.WORKSPACE_STREAMS):
+        s = torch.cuda.Stream()
+        s.wait_stream(main)
+        o = torch.full_like(g, float("nan"))
+        with torch.cuda.stream(s):
+            r.launch_bwd_weight_deterministic(dyd, xd, o, K)
+        s.synchronize()
+        assert torch.equal(o, g), i
+        assert len(r._workspaces) <= runtime.WORKSPACE_STREAMS
+    assert len(r._workspaces) == runtime.WORKSPACE_STREAMS
     r.close()

@@ -366,7 +366,7 @@ def _misaligned(t):
     return v
 
 
-@pytest.mark.parametrize("shape", [
+STAGING_SHAPES = [
     (1001, 64, 48, 3),    # ragged last 4-sample step, K = 3 (coalesced atomics)
     (5, 32, 40, 24),      # fewer steps than interleaved ranges, L < bucket
     (2048, 128, 20, 9),   # L in the 32 bucket, odd K
@@ -380,23 +380,32 @@ def _misaligned(t):
     (70, 32, 2, 5),       # L = 2, K > L: taps without overlap
     (33, 16, 3, 48),      # L = 3
     (129, 64, 7, 7),
-])
-@pytest.mark.parametrize("threads", [64, 128, 256, 512])
+]
+# (shape, threads) where H is a multiple of the channel group (one channel
+# per wave for rows of 33-48 columns, two below): the cases the channel-group
+# kernel serves.
+STAGING_CASES = [(s, t) for s in STAGING_SHAPES for t in (64, 128, 256, 512)
+                 if s[1] % ((1 if s[2] > 32 else 2) * (t // 64)) == 0]
+
+
+@pytest.mark.parametrize("shape,threads", STAGING_CASES,
+                         ids=lambda v: "B{}H{}L{}K{}".format(*v) if isinstance(v, tuple) else str(v))
 def test_dk_channel_group_staging_widths(shape, threads):
     """Where H is a multiple of the channel group (one channel per wave for
     rows of 33-48 columns, two below; at most 8 waves) the channel-group
     kernel serves any L: 16-byte chunk staging for 16-byte aligned tensors
     whose group segments and samples are whole chunks, dword staging
-    otherwise (odd L, or the same values in misaligned storage). The
-    geometry is the same either way, so the deterministic results of the
-    two stagings are bitwise equal; both agree with FP64 and repeat bit for
-    bit with the workspace the API sizes."""
+    otherwise (odd L, or the same values in misaligned storage). These
+    shapes take fewer workgroups than one resident round, so the range count
+    (and with it the partition of the deterministic sums) comes from the
+    shape alone and the deterministic results of the two stagings are
+    bitwise equal; both agree with FP64 and repeat bit for bit with the
+    workspace the API sizes. (Where one round caps the range count, the two
+    staging kernels' occupancies can cap it differently:
+    test_dk_capped_grid_repeats_per_alignment.)"""
     from pathtile_amd import runtime
 
     B, H, L, K = shape
-    cpw = 1 if L > 32 else 2
-    if H % (cpw * (threads // 64)):
-        pytest.skip("H not a multiple of the channel group")
     x, w, dy = _inputs(B, H, L, K, seed=3000 + B + L + K)
     xd, dyd = _dev(x, dy)
     xm, dym = _misaligned(x), _misaligned(dy)
@@ -416,6 +425,30 @@ def test_dk_channel_group_staging_widths(shape, threads):
             if hi <= lo:
                 assert np.all(ga[:, j] == 0.0) and np.all(g1[:, j] == 0.0)
     assert np.array_equal(dets[0], dets[1])
+    r.close()
+
+
+def test_dk_capped_grid_repeats_per_alignment():
+    """B16384 H96 L48 K48: the range rule asks for 48 ranges of 48 channel
+    groups (2304 workgroups), more than one resident round, so the launch
+    caps the range count by the kernel's occupancy, which may differ between
+    the 16-byte and the dword staging kernels. Each alignment must still
+    repeat its own bits and stay within 1e-4 of FP64."""
+    from pathtile_amd import runtime
+
+    B, H, L, K = 16384, 96, 48, 48
+    x, w, dy = _inputs(B, H, L, K, seed=3131)
+    ref = oracle.dk_f64(dy, x, K)
+    r = runtime.HipWarpRuntime(bwdk_block=128)
+    for a, b in ((dy.to("cuda:0"), x.to("cuda:0")), (_misaligned(dy), _misaligned(x))):
+        g1 = _dk_det(r, a, b, K).cpu().numpy()
+        g2 = _dk_det(r, a, b, K).cpu().numpy()
+        ga = _dk_atomic(r, a, b, K).cpu().numpy()
+        assert np.array_equal(g1, g2)
+        assert oracle.normalized_max_abs(g1, ref) < DK_TOL
+        assert oracle.normalized_max_abs(ga, ref) < DK_TOL
+        del a, b
+        torch.cuda.empty_cache()
     r.close()
 
 

@@ -6,9 +6,12 @@ The two entry points run the same kernels in the same order, so their
 results must agree bit for bit. The workspace version gets a NaN-filled
 workspace: any partial that the kernels read without writing first would
 show up. Two no-allocation calls in a row, the second on a smaller input,
-check that nothing of the first call's scratch leaks into the second. (The
-refusal of shapes beyond the static scratch happens before any HIP call and
-is tested on the CPU, tests/test_abi_cpu.py.)
+check that nothing of the first call's scratch leaks into the second. After
+one eager call, a call allocates nothing (torch's allocation count and the
+device's free memory unchanged) and runs under HIP graph capture: every
+replay of the captured call gives the eager bits. (The refusal of shapes
+beyond the static scratch depends on the shape alone, comes before any
+device query, and is tested on the CPU, tests/test_abi_cpu.py.)
 """
 
 from __future__ import annotations
@@ -79,3 +82,45 @@ def test_noalloc_matches_workspace_entry_point(first, second, threads):
         assert np.array_equal(a, b)
         if B * H <= 2_000_000:
             assert oracle.normalized_max_abs(a, oracle.dk_f64(dy, x, K)) < 1e-4
+
+
+def test_noalloc_allocates_nothing_and_replays_under_graph_capture():
+    from pathtile_amd import _lib
+
+    lib = _lib.load()
+    B, H, L, K, threads = 4096, 128, 48, 48, 128
+    print(f"[case] noalloc graph B={B} H={H} L={L} K={K} threads={threads}", flush=True)
+    x, w, dy = oracle.make_inputs(B, H, L, K, seed=404)
+    xd, dyd = x.cuda(), dy.cuda()
+    gk = torch.full((H, K), float("nan"), device="cuda")
+
+    def call():
+        _lib.check(lib.pt_dwconv1d_dk_det_f32_noalloc(_vp(dyd), _vp(xd), _vp(gk), B, H, L, K,
+                                                      threads, _stream()), "det noalloc")
+
+    call()  # the warm-up call: scratch address and occupancy lookups
+    torch.cuda.synchronize()
+    eager = gk.clone()
+    assert np.array_equal(eager.cpu().numpy(), _det_workspace(lib, dyd, xd, K, threads).cpu().numpy())
+    torch.cuda.synchronize()
+    alloc0 = torch.cuda.memory_allocated()
+    free0, _ = torch.cuda.mem_get_info()
+    gk.fill_(float("nan"))
+    call()
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated() == alloc0
+    assert torch.cuda.mem_get_info()[0] == free0
+    assert torch.equal(gk, eager)
+
+    graph = torch.cuda.CUDAGraph()
+    gk.fill_(float("nan"))
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        call()
+    for i in range(4):
+        gk.fill_(float("nan"))          # eager work between the replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gk, eager), i
+    del graph
