@@ -1,6 +1,6 @@
 """Summaries of rocprofv3 results (rocpd SQLite ``*_results.db``) as Markdown.
 
-Six reports, each written for one workload:
+Seven reports, each written for one workload:
 
 ``trace``   kernel-trace statistics: calls and average/min/max duration per
             kernel, plus the launch geometry and resources of the largest
@@ -24,6 +24,10 @@ Six reports, each written for one workload:
 ``mix``     VALU instruction mix from the ``SQ_INSTS_VALU_*`` class counters:
             each class's share of ``SQ_INSTS_VALU`` and the FP32 fraction
             (FMA + add + multiply in FP32).
+``stall``   achieved occupancy (waves per CU and SIMD), the share of wave
+            cycles spent waiting, MemUnitStalled, DRAM-credit stalls of the
+            L2 channels and the UTCL1 translation miss rate, from counters
+            collected over several passes.
 ``lds``     LDS instructions per wave, LDS-busy fraction per CU, bank-conflict
             share of the LDS cycles and the share of wave cycles waiting for
             LDS, from ``SQ_INSTS_LDS`` / ``SQ_LDS_IDX_ACTIVE`` /
@@ -45,6 +49,7 @@ Usage::
         --useful-fma SUBSTR=N --emit SUBSTR=KEY
     python -m pathtile_amd.profiling mix     DB --command CMD --out FILE
     python -m pathtile_amd.profiling lds     DB --command CMD --out FILE
+    python -m pathtile_amd.profiling stall   [LABEL=]DB ... --command CMD --out FILE
 """
 
 from __future__ import annotations
@@ -343,6 +348,78 @@ def lds_report(db: str, command: str, match: str = "pt::") -> str:
     return "\n".join(out) + "\n"
 
 
+STALL_COUNTERS = ("MeanOccupancyPerCU", "SQ_WAVE_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY",
+                  "MemUnitStalled", "GRBM_GUI_ACTIVE", "TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum",
+                  "TCC_EA0_WRREQ_DRAM_CREDIT_STALL_sum", "TCP_UTCL1_TRANSLATION_MISS_sum",
+                  "TCP_UTCL1_TRANSLATION_HIT_sum")
+NUM_TCC = 128  # 16 L2 channels per XCD
+
+
+def stall_report(dbs: list[str], command: str, match: str = "pt::",
+                 labels: list[str] | None = None) -> str:
+    """Achieved occupancy and where the waves wait, per kernel (and per
+    database, `labels` naming each): mean resident waves per CU
+    (MeanOccupancyPerCU) and per SIMD; the share of wave cycles spent
+    waiting on anything (SQ_WAIT_ANY / SQ_WAVE_CYCLES) and on an issued
+    instruction (SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES); MemUnitStalled (% of
+    the time the texture units' data path is stalled); the share of L2
+    channel cycles with a read or write request held for lack of DRAM
+    credits ((TCC_EA0_*_DRAM_CREDIT_STALL summed over the 128 channels) /
+    (128 x GRBM_GUI_ACTIVE / 8)); and the UTCL1 (first-level address
+    translation) miss rate. Every counter is read from whichever database
+    holds it: collect them in passes that fit the counter blocks."""
+    labels = labels or [""] * len(dbs)
+    per = {}
+    for db, label in zip(dbs, labels):
+        for c in STALL_COUNTERS:
+            try:
+                rows = counter_rows(db, c)
+            except sqlite3.Error:
+                continue
+            rows = _largest_dispatches([r for r in rows if match in r["name"]], "grid", "value")
+            for r in rows:
+                per.setdefault((label, r["name"]), {}).setdefault(c, []).append(r["value"])
+    out = ["Command:", "", "```", command, "```", "",
+           "Occupancy = MeanOccupancyPerCU (waves per CU; per SIMD = / 4). Wait = "
+           "SQ_WAIT_ANY / SQ_WAVE_CYCLES; wait-inst = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES. "
+           "MemUnitStalled: % of time the TA data path stalls. DRAM credit stall = "
+           "TCC_EA0_{RD,WR}REQ_DRAM_CREDIT_STALL summed / (128 L2 channels x GRBM_GUI_ACTIVE / "
+           "8 XCDs). UTCL1 miss = misses / (hits + misses). Dispatches with each kernel's "
+           "largest grid, none below a quarter of its median counter value.", "",
+           "| run | kernel | dispatches | waves/CU | waves/SIMD | wait | wait-inst | "
+           "MemUnitStalled % | DRAM credit stall rd | wr | UTCL1 miss |",
+           "|---|---|---|---|---|---|---|---|---|---|---|"]
+
+    def fmt(v, spec):
+        return "-" if v is None else format(v, spec)
+
+    for (label, name), cs in per.items():
+        m = {c: statistics.mean(v) for c, v in cs.items()}
+        n = max(len(v) for v in cs.values())
+        occ = m.get("MeanOccupancyPerCU")
+        wait = (m["SQ_WAIT_ANY"] / m["SQ_WAVE_CYCLES"]
+                if "SQ_WAIT_ANY" in m and m.get("SQ_WAVE_CYCLES") else None)
+        wait_i = (m["SQ_WAIT_INST_ANY"] / m["SQ_WAVE_CYCLES"]
+                  if "SQ_WAIT_INST_ANY" in m and m.get("SQ_WAVE_CYCLES") else None)
+        gui = m.get("GRBM_GUI_ACTIVE")
+        rd = wr = None
+        if gui:
+            denom = NUM_TCC * gui / NUM_XCD
+            if "TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum" in m:
+                rd = m["TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum"] / denom
+            if "TCC_EA0_WRREQ_DRAM_CREDIT_STALL_sum" in m:
+                wr = m["TCC_EA0_WRREQ_DRAM_CREDIT_STALL_sum"] / denom
+        miss = None
+        if "TCP_UTCL1_TRANSLATION_MISS_sum" in m and "TCP_UTCL1_TRANSLATION_HIT_sum" in m:
+            tot = m["TCP_UTCL1_TRANSLATION_MISS_sum"] + m["TCP_UTCL1_TRANSLATION_HIT_sum"]
+            miss = m["TCP_UTCL1_TRANSLATION_MISS_sum"] / tot if tot else None
+        out.append(f"| {label} | `{short_name(name)}` | {n} | {fmt(occ, '.2f')} | "
+                   f"{fmt(None if occ is None else occ / 4, '.2f')} | {fmt(wait, '.3f')} | "
+                   f"{fmt(wait_i, '.3f')} | {fmt(m.get('MemUnitStalled'), '.1f')} | "
+                   f"{fmt(rd, '.3f')} | {fmt(wr, '.3f')} | {fmt(miss, '.4f')} |")
+    return "\n".join(out) + "\n"
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(prog="python -m pathtile_amd.profiling")
     sub = p.add_subparsers(dest="cmd", required=True)
@@ -387,6 +464,12 @@ def main(argv=None) -> int:
     d.add_argument("--command", required=True)
     d.add_argument("--title", default="LDS load")
     d.add_argument("--out", required=True)
+    st = sub.add_parser("stall")
+    st.add_argument("dbs", nargs="+", help="databases of the counter passes; LABEL=DB "
+                    "to name a run (several DBs of one run share its label)")
+    st.add_argument("--command", required=True)
+    st.add_argument("--title", default="Occupancy and stalls")
+    st.add_argument("--out", required=True)
     a = p.parse_args(argv)
 
     def pairs(items, conv):
@@ -408,6 +491,10 @@ def main(argv=None) -> int:
         text = f"# {a.title}\n\n" + mix_report(a.db, a.command)
     elif a.cmd == "lds":
         text = f"# {a.title}\n\n" + lds_report(a.db, a.command)
+    elif a.cmd == "stall":
+        labels = [d.rpartition("=")[0] if "=" in d else "" for d in a.dbs]
+        dbs = [d.rpartition("=")[2] for d in a.dbs]
+        text = f"# {a.title}\n\n" + stall_report(dbs, a.command, labels=labels)
     else:
         text = f"# {a.title}\n\n" + mfma_report(a.db, a.command, pairs(a.useful_fma, int),
                                                 pairs(a.emit, str))

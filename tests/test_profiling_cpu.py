@@ -100,3 +100,30 @@ def test_mix_report(tmp_path):
     text = profiling.mix_report(_db(tmp_path / "m.db", rows), "cmd")
     r = _row(text, "pt::dwconv_rows_cg_kernel<48, false, 2, 16>")
     assert r[1:] == ["2", "1000", "0.550", "0.400", "0.100", "0.050", "0.200", "0.010", "0.120"]
+
+
+def test_stall_report_merges_passes(tmp_path):
+    """Occupancy, wait shares, MemUnitStalled, DRAM-credit stall shares and
+    the UTCL1 miss rate, from two counter passes of one run (labelled) and
+    one counter of another run."""
+    gui = 8 * 1000.0  # 1000 cycles per XCD
+    pass_a = {"MeanOccupancyPerCU": 6.0, "SQ_WAVE_CYCLES": 1000.0, "SQ_WAIT_ANY": 700.0,
+              "SQ_WAIT_INST_ANY": 200.0, "MemUnitStalled": 12.5}
+    pass_b = {"GRBM_GUI_ACTIVE": gui,
+              "TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum": 128 * 1000 * 0.25,
+              "TCC_EA0_WRREQ_DRAM_CREDIT_STALL_sum": 128 * 1000 * 0.5,
+              "TCP_UTCL1_TRANSLATION_MISS_sum": 10.0, "TCP_UTCL1_TRANSLATION_HIT_sum": 990.0}
+    rows_a, rows_b = [], []
+    for d in range(2):
+        rows_a += [(K_MAIN, d, 4096, c, v) for c, v in pass_a.items()]
+        rows_b += [(K_MAIN, d, 4096, c, v) for c, v in pass_b.items()]
+    rows_a += [(K_MAIN, 9, 64, c, 1.0) for c in pass_a]  # gate dispatch: dropped
+    other = [(K_MAIN, 0, 4096, "MeanOccupancyPerCU", 3.0)]
+    text = profiling.stall_report(
+        [_db(tmp_path / "a.db", rows_a), _db(tmp_path / "b.db", rows_b),
+         _db(tmp_path / "c.db", other)], "cmd", labels=["slow", "slow", "fast"])
+    lines = [l for l in text.splitlines() if "dwconv_rows_cg_kernel" in l]
+    cells = {l.split("|")[1].strip(): [c.strip() for c in l.strip("|").split("|")] for l in lines}
+    assert cells["slow"][2:] == ["2", "6.00", "1.50", "0.700", "0.200", "12.5", "0.250",
+                                 "0.500", "0.0100"]
+    assert cells["fast"][2:] == ["1", "3.00", "0.75", "-", "-", "-", "-", "-", "-"]
