@@ -303,9 +303,13 @@ def workload_leg(rt, name: str, args, dev, stream, keep: bool = False) -> dict:
     # Checks of the timed launches' outputs: y and dx hold the last timed
     # launch's results; dK is launched once more on the same tensors (the
     # timed atomic launches accumulate into gk).
+    # Sampled batch rows: the first and the last sample (the ragged tail
+    # steps) and distinct others.
     g = torch.Generator().manual_seed(args.seed + 1)
-    idx = torch.randperm(B, generator=g)[: min(B, 256)]
-    idx[0], idx[-1] = 0, B - 1  # first and last sample: the ragged tail steps
+    n_rows = min(B, 256)
+    inner = (torch.randperm(B - 2, generator=g)[: max(0, n_rows - 2)] + 1 if B > 2
+             else torch.empty(0, dtype=torch.long))
+    idx = torch.cat([torch.tensor([0]), inner, torch.tensor([B - 1] if B > 1 else [])]).long()
     idx = idx.to(dev)
     gate = {
         "fwd": nerr(y[idx], fp64_fwd(x[idx], w)),

@@ -300,6 +300,27 @@ static long long bm_ranges(int B, int H, int L) {
   return nr < 1 ? 1 : nr;
 }
 
+// Waves per workgroup of the channel-group DK: the caller's, raised at small
+// K so that a workgroup's tap sums (cpw x waves channels x K taps) fill at
+// least one 128-byte line, up to 8 waves and where H allows. Each workgroup
+// adds its sums into dk with atomics, and every sample range adds into the
+// same few lines: at B16384 H64 L16 K3 (dk is six lines, 128 ranges) two-wave
+// workgroups took 25.2 us and eight-wave ones 23.0 (the deterministic
+// variant, without atomics, 24.5-25.0 at every size); at B16384 H64 L24 K3
+// 39.4 against 37.7, at B32768 H128 L40 K3 228.8 against 220.9, while at
+// K = 8 the sizes tie (B16384 H64 L16 K8: 22.8-23.0 us). A wave's partial
+// sums do not depend on its workgroup's size, so neither do the
+// deterministic variant's bits.
+static int dk_cg_waves(int H, int K, int cpw, int wpb) {
+  const int want = (32 + cpw * K - 1) / (cpw * K);
+  if (wpb >= want) return wpb;
+  for (int w = want < 8 ? want : 8; w <= 8; ++w)
+    if (H % (cpw * w) == 0) return w;
+  for (int w = 8; w > wpb; --w)
+    if (H % (cpw * w) == 0) return w;
+  return wpb;
+}
+
 // device_cap: size the channel-group DK's ranges for the current device (a
 // launch); without it the geometry depends on the shape alone and its
 // range count bounds every launch's (the deterministic workspace size).
@@ -315,8 +336,9 @@ static DkGeom dk_geometry(int B, int H, int L, int K, int threads, bool vec16,
   g.epc = 4;
   g.cpw = dk_cpw(L);
   if (g.cg) {
+    g.wpb = dk_cg_waves(H, K, g.cpw, g.wpb);
     dk_cg_staging(g, H, L, vec16);
-    const long long ngroups = (long long)H / (g.cpw * wpb);
+    const long long ngroups = (long long)H / (g.cpw * g.wpb);
     long long nr = cg_ranges(B, H, L);
     // The stride rule was measured where its workgroups fill the resident
     // slots exactly (H a power of two). Where they overflow them, the few
@@ -327,8 +349,8 @@ static DkGeom dk_geometry(int B, int H, int L, int K, int threads, bool vec16,
       const int mi = mfma_index(L);
       const DkCgFn fn = dk_cg_fn(g.nt, g.epc, g.cpw, L);
       const long long resident =
-          (long long)blocks_per_cu((const void*)fn, threads,
-                                   cg_lds_bytes(16 * (mi + 1), (int)wpb, L, g.cpw)) *
+          (long long)blocks_per_cu((const void*)fn, g.wpb * kWave,
+                                   cg_lds_bytes(16 * (mi + 1), g.wpb, L, g.cpw)) *
           num_cus();
       if (ngroups * nr > resident) nr = resident / ngroups;
       if (nr < 1) nr = 1;
@@ -828,7 +850,7 @@ static int dk_path(bool det, const float* gy, const float* x, float* dst,
     DkCgFn fn = dk_cg_fn(g.nt, g.epc, g.cpw, L);
     const size_t lds = cg_lds_bytes(16 * (mfma_index(L) + 1), g.wpb, L, g.cpw);
     void* args[] = {&gy, &x, &dst, &B, &H, &L, &K, &nbt, &nblocks, &d};
-    return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream,
+    return launch((const void*)fn, nblocks, (uint32_t)(g.wpb * kWave), lds, stream,
                   args);
   }
   if (g.algo == kDkMfma) {

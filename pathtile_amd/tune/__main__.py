@@ -59,11 +59,15 @@ def _read_csv(path: Path) -> list[dict]:
 
 
 def _git_rev() -> str:
+    """The checkout's HEAD; where the tree was copied without its .git (a
+    GPU box), the PATHTILE_GIT_REV the caller passes along."""
+    import os
+
     try:
         return subprocess.run(["git", "rev-parse", "HEAD"], cwd=PKG, capture_output=True,
                               text=True, check=True).stdout.strip()
     except Exception:
-        return "unknown"
+        return os.environ.get("PATHTILE_GIT_REV", "unknown")
 
 
 def _run_phase(name, cases, args, out: Path, log) -> list[dict]:

@@ -156,14 +156,21 @@ def buffer_sets(x, gy) -> list[tuple]:
 
 
 def measure_candidate(runtime, kind: str, sets: list[tuple], k, warmup: int,
-                      runs: int) -> dict[str, list[float]]:
+                      runs: int, outputs: dict | None = None) -> dict[str, list[float]]:
     """Warm-up, then `runs` event-timed launches per path, cycling through the
-    buffer sets (benchmark/benchmark_pathtile_candidate_sweep.py:246-317)."""
+    buffer sets (benchmark/benchmark_pathtile_candidate_sweep.py:246-317).
+    With `outputs`, the FWD/dX outputs start as NaN and the last timed
+    launches' results are returned in it ("fwd", "bwd_input": one buffer
+    set's y and dX; "bwd_weight": dK of the last timed launch)."""
     K = int(k.shape[1])
     coll = rt.KernelEventCollector()
     coll.enabled = True
     n = len(sets)
     if kind == FWD_DX_KIND:
+        if outputs is not None:
+            for _, _, y, gx in sets:
+                y.fill_(float("nan"))
+                gx.fill_(float("nan"))
         for i in range(warmup):
             x, gy, y, gx = sets[i % n]
             runtime.launch_fwd(x, k, y)
@@ -175,6 +182,9 @@ def measure_candidate(runtime, kind: str, sets: list[tuple], k, warmup: int,
         for i in range(runs):
             x, gy, y, gx = sets[i % n]
             runtime.launch_bwd_input(gy, k, gx, coll)
+        if outputs is not None:
+            last = sets[(runs - 1) % n]
+            outputs["fwd"], outputs["bwd_input"] = last[2], last[3]
     else:
         gk = torch.zeros_like(k)
         for i in range(warmup):
@@ -186,10 +196,65 @@ def measure_candidate(runtime, kind: str, sets: list[tuple], k, warmup: int,
             x, gy, _, _ = sets[i % n]
             gk.zero_()
             runtime.launch_bwd_weight(gy, x, gk, K, coll)
+        if outputs is not None:
+            outputs["bwd_weight"] = gk
     out: dict[str, list[float]] = {}
     for r in coll.rows(synchronize=True):
         out.setdefault(r["phase"], []).append(r["runtime_ms"])
     return out
+
+
+# Batch rows of the timed FWD/dX outputs compared against FP64 (the first
+# and last sample among them: the ragged tail steps).
+TIMED_CHECK_ROWS = 64
+
+
+class TimedCheck:
+    """FP64 references of one shape's full-size inputs on the GPU, and the
+    check of a candidate's timed outputs against them: FWD and dX on sampled
+    batch rows (all channels), dK over the whole batch, each within the
+    build's bars (1e-5, 1e-5, 1e-4 max-abs-scaled). This gates the timing on
+    correctness at the size that is timed, as the reference's sweep gates
+    each schedule (benchmark/benchmark_pathtile_candidate_sweep.py:
+    153-243), not only at the validation size."""
+
+    def __init__(self, case: ShapeCase, seed: int, x, k, gy):
+        self.case = case
+        B, K = case.B, case.K
+        g = torch.Generator().manual_seed(seed + 1)
+        n = min(B, TIMED_CHECK_ROWS)
+        inner = torch.randperm(B - 2, generator=g)[:max(0, n - 2)] + 1 if B > 2 else \
+            torch.empty(0, dtype=torch.long)
+        idx = torch.cat([torch.tensor([0]), inner, torch.tensor([B - 1] if B > 1 else [])]).long()
+        self.idx = idx.to(x.device)
+        kd = k.double()
+        self.y = _torch_same(x[self.idx].double(), kd)
+        # dX[b,h,s] = sum_j w[h,j] dY[b,h,s-j+p]: a correlation with the
+        # flipped taps, padded (K-1-p, p)
+        p = K // 2
+        self.gx = F.conv1d(F.pad(gy[self.idx].double(), (K - 1 - p, p)),
+                           kd.flip(-1).unsqueeze(1), groups=case.H)
+        L = case.L
+        xp = F.pad(x.double(), (p, K - 1 - p))
+        gyd = gy.double()
+        self.gk = torch.stack([(gyd * xp[..., j:j + L]).sum(dim=(0, 2)) for j in range(K)], dim=1)
+        del xp, gyd
+
+    @staticmethod
+    def _err(a, ref) -> float:
+        return float((a.double() - ref).abs().max() / ref.abs().max().clamp_min(1e-12))
+
+    def rows(self, kind: str, value: int, outputs: dict) -> list[dict]:
+        got = {}
+        if "fwd" in outputs:
+            got["fwd"] = (self._err(outputs["fwd"][self.idx], self.y), 1e-5)
+            got["bwd_input"] = (self._err(outputs["bwd_input"][self.idx], self.gx), 1e-5)
+        if "bwd_weight" in outputs:
+            got["bwd_weight"] = (self._err(outputs["bwd_weight"], self.gk), 1e-4)
+        return [{**self.case.as_dict(), "candidate_kind": kind, "candidate_value": value,
+                 "validation_B": self.case.B, "phase": ph, "normalized_max_abs": err,
+                 "allclose": bool(err <= bar), "source": "timed launches"}
+                for ph, (err, bar) in got.items()]
 
 
 def candidate_specs(trial_id: int) -> list[tuple[str, int]]:
@@ -220,9 +285,13 @@ def run_trial(cases: list[ShapeCase], trial_id: int, warmup: int, runs: int,
         for kind, value in specs:
             validation += validate_candidate(runtimes[(kind, value)], case, seed, kind, value)
         x, k, gy = make_inputs(case, seed)
+        check = TimedCheck(case, seed, x, k, gy)
         sets = buffer_sets(x, gy)
         for kind, value in specs:
-            times = measure_candidate(runtimes[(kind, value)], kind, sets, k, warmup, runs)
+            outputs: dict = {}
+            times = measure_candidate(runtimes[(kind, value)], kind, sets, k, warmup, runs,
+                                      outputs)
+            validation += check.rows(kind, value, outputs)
             for phase, vals in times.items():
                 summary.append({**case.as_dict(), "trial_id": trial_id, "candidate_kind": kind,
                                 "candidate_value": value, "phase": phase,
@@ -233,7 +302,7 @@ def run_trial(cases: list[ShapeCase], trial_id: int, warmup: int, runs: int,
                 control.append({**case.as_dict(), "trial_id": trial_id, "candidate_kind": kind,
                                 "candidate_value": value, "phase": phase,
                                 "buffer_sets": len(sets), **stats(vals)})
-        del x, k, gy, sets
+        del x, k, gy, sets, check
         torch.cuda.empty_cache()
         log(f"[tune] trial {trial_id} {case.config_id} done ({time.time() - t0:.1f}s)")
     bad = [v for v in validation if not v["allclose"]]

@@ -109,6 +109,14 @@ def test_odd_k_config_full_size(rt, monkeypatch):
     _full_size_case(rt, 16384, 128, 48, 47, 78, monkeypatch)
 
 
+def test_short_rows_above_the_mall_full_size(rt, monkeypatch):
+    """The tuner's holdout_b32768_h256_l24_k32 at its full size (805 MB per
+    tensor): rows of fewer than 33 columns on tensors above 256 MiB, where
+    FWD/dX take non-temporal loads and 16-channel workgroups are not used,
+    and dK ranges follow the 3 MiB stride rule."""
+    _full_size_case(rt, 32768, 256, 24, 32, 80, monkeypatch)
+
+
 def test_odd_row_length_above_the_mall_full_size(rt, monkeypatch):
     """L % 4 != 0 on tensors above 256 MiB (B16384 H128 L37 K48, 310 MB
     each): FWD/dX on the matrix-core kernel's element-wise form with

@@ -282,3 +282,40 @@ def test_noise_floor_from_the_duplicate_control():
     # a: 4.0 against 3.9 (the faster of each pair); b: 4.0 against 4.0
     assert nf["mean_regret_pct"] == pytest.approx((4.0 / 3.9 - 1) * 50)
     assert nf["max_regret_pct"] == pytest.approx((4.0 / 3.9 - 1) * 100)
+
+
+def test_timed_check_references_and_verdicts():
+    """The sweep's check of the timed outputs (sweep.TimedCheck): its FP64
+    references equal the oracle's (FWD and dX on the sampled rows, which
+    include the first and last sample; dK over the whole batch), correct
+    outputs pass the build's bars, and NaN (an unwritten tile) or a
+    perturbed output fail them."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from pathtile_amd.tune import sweep
+    from pathtile_amd.tune.shapes import ShapeCase
+
+    B, H, L, K = 70, 6, 13, 5
+    case = ShapeCase("t", B, H, L, K, "t")
+    x, w, dy = oracle.make_inputs(B, H, L, K, 3)
+    tc = sweep.TimedCheck(case, 1, x, w, dy)
+    idx = tc.idx.numpy()
+    assert idx[0] == 0 and idx[-1] == B - 1 and len(set(idx)) == min(B, sweep.TIMED_CHECK_ROWS)
+    assert np.abs(tc.y.numpy() - oracle.fwd_f64(x[idx], w)).max() < 1e-12
+    assert np.abs(tc.gx.numpy() - oracle.dx_f64(dy[idx], w)).max() < 1e-12
+    assert np.abs(tc.gk.numpy() - oracle.dk_f64(dy, x, K)).max() < 1e-9
+    good = {"fwd": torch.from_numpy(oracle.fwd_f64(x, w)).float(),
+            "bwd_input": torch.from_numpy(oracle.dx_f64(dy, w)).float(),
+            "bwd_weight": torch.from_numpy(oracle.dk_f64(dy, x, K)).float()}
+    rows = tc.rows("waves_per_block", 4, {k: good[k] for k in ("fwd", "bwd_input")})
+    rows += tc.rows("dk_threads_per_block", 128, {"bwd_weight": good["bwd_weight"]})
+    assert [r["phase"] for r in rows] == ["fwd", "bwd_input", "bwd_weight"]
+    assert all(r["allclose"] and r["validation_B"] == B for r in rows)
+    bad_y = good["fwd"].clone()
+    bad_y[B - 1, 0, 0] = float("nan")   # the last sample: a tile the launch missed
+    bad_k = good["bwd_weight"] * (1 + 1e-3)
+    rows = tc.rows("waves_per_block", 4, {"fwd": bad_y, "bwd_input": good["bwd_input"]})
+    rows += tc.rows("dk_threads_per_block", 128, {"bwd_weight": bad_k})
+    assert [r["allclose"] for r in rows] == [False, True, False]
