@@ -1030,6 +1030,15 @@ static bool long_dk_split(int L, int K) {
   return e < 0 ? (K >= 40 || L == 64 || L == 96) : e == 1;
 }
 
+// Split DK kernel of a row bucket: operands loaded in place (every wave
+// loads its own column tile of both tensors straight into registers and
+// publishes only the x parts) from LMAX = 128 up, the FP32 stage in LDS
+// below. Measured on MI355X at B16384 H128 (us, in place against staged):
+// L192 K192 790 / 858, L192 K96 640 / 703, L128 K64 382 / 452; L96 K48
+// 337 / 301, L64 K64 215 / 181, L64 K16 213 / 169 (short rows give a
+// wave's 64-byte row pieces too little work to hide their latency).
+static bool long_dk_in_place(int li) { return long_lmax(li) >= 128; }
+
 static int rows_long_path(bool dx, const float* in, const float* w, float* out,
                           int B, int H, int L, int K, void* stream) {
   int st = check_long_shape(B, H, L, K);
@@ -1484,10 +1493,13 @@ int pt_dwconv1d_dk_long_f32(const float* dy, const float* x, float* dk,
   void* args[] = {&dy, &x, &partials, &B, &H, &L, &K, &nranges, &det};
   const bool vec = L % 4 == 0 && pt::aligned(dy, 16) && pt::aligned(x, 16);
   const bool split = pt::long_dk_split(L, K);
-  st = pt::launch((const void*)(split ? pt::kDkLongS3Table : pt::kDkLongTable)[vec ? 1 : 0][li],
-                  (uint32_t)nb, (uint32_t)((lmax / 16) * pt::kWave),
-                  split ? pt::dk_long_s3_lds_bytes(lmax) : pt::dk_long_lds_bytes(lmax),
-                  stream, args);
+  if (split && pt::long_dk_in_place(li))
+    st = pt::launch((const void*)pt::kDkLongS3RTable[li], (uint32_t)nb, (uint32_t)((lmax / 16) * pt::kWave),
+                    pt::dk_long_s3r_lds_bytes(lmax), stream, args);
+  else
+    st = pt::launch((const void*)(split ? pt::kDkLongS3Table : pt::kDkLongTable)[vec ? 1 : 0][li],
+                    (uint32_t)nb, (uint32_t)((lmax / 16) * pt::kWave),
+                    split ? pt::dk_long_s3_lds_bytes(lmax) : pt::dk_long_lds_bytes(lmax), stream, args);
   if (st != PT_OK) return st;
   int ncoef = H * K;
   int nbt = nranges;

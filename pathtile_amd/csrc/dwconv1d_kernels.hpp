@@ -148,6 +148,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float* base) {
                                            kNumRecords, kRsrcWord3);
 }
 
+// A buffer of nrec bytes from base: loads at offsets past it return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_n(const float* base, int nrec) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, nrec, kRsrcWord3);
+}
+
 template <int CPOL = kCpolNone>
 __device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r,
                                             uint32_t voff, uint32_t soff) {
@@ -2377,18 +2382,28 @@ __global__ __launch_bounds__(kLongRowsWaves * kWave) void dwconv_rows_long_kerne
 // ---------------------------------------------------------------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// Three-way BF16 split of eight FP32 values (round to nearest even).
+// Three-way BF16 split of eight FP32 values (round to nearest even). Values
+// go in pairs: one v_cvt_pk_bf16_f32 rounds two, and widening a BF16 back to
+// FP32 is a shift or a mask, so a pair costs 11 VALU instructions.
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ void split3_bf16x8(const float (&v)[8], bf16x8& hi,
                                               bf16x8& mid, bf16x8& lo) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const __bf16 h = (__bf16)v[i];
-    const float r1 = v[i] - (float)h;
-    const __bf16 m = (__bf16)r1;
-    const float r2 = r1 - (float)m;
-    hi[i] = h;
-    mid[i] = m;
-    lo[i] = (__bf16)r2;
+  for (int i = 0; i < 8; i += 2) {
+    const f32x2v x = {v[i], v[i + 1]};
+    const bf16x2v h = __builtin_convertvector(x, bf16x2v);
+    const f32x2v r1 = x - __builtin_convertvector(h, f32x2v);
+    const bf16x2v m = __builtin_convertvector(r1, bf16x2v);
+    const f32x2v r2 = r1 - __builtin_convertvector(m, f32x2v);
+    const bf16x2v l = __builtin_convertvector(r2, bf16x2v);
+    hi[i] = h[0];
+    hi[i + 1] = h[1];
+    mid[i] = m[0];
+    mid[i + 1] = m[1];
+    lo[i] = l[0];
+    lo[i + 1] = l[1];
   }
 }
 
@@ -2761,6 +2776,7 @@ __global__ __launch_bounds__((LMAX / 16) * kWave) void dwconv_dk_long_s3_kernel(
   // waves per epilogue round: D rows go through the stages and publication
   constexpr int kRound = (4 * SZ + PUB * 4) / (16 * DS);
   static_assert(32 * LMAX == NE * EW * NTH, "whole rows per thread slice");
+  static_assert(16 % (32 / NE) == 0, "each load's rows lie in one half of the step");
   static_assert(kRound >= 1, "staging area holds one wave's D rows");
   extern __shared__ float lds[];
   bf16x8* const pub = reinterpret_cast<bf16x8*>(lds + 4 * SZ);  // [3][NT][64]
@@ -2788,14 +2804,17 @@ __global__ __launch_bounds__((LMAX / 16) * kWave) void dwconv_dk_long_s3_kernel(
   float stg[2][NE];  // dwords
   auto load_step = [&](int s) {
     const int bs = (r + s * nranges) * 32;
-    const size_t r0 = ((size_t)bs * (size_t)H + (size_t)h) * (size_t)L;
-    const __amdgpu_buffer_rsrc_t rg = make_rsrc(gy + r0);
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + r0);
     const int klim = min(32, B - bs);
+    // Load i covers rows [32 i / NE, 32 (i + 1) / NE), all in one half of
+    // the step: offsets run from the half's base, so they span 16 rows.
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
+      const int half = (i * (32 / NE)) / 16;
+      const size_t r0 = ((size_t)(bs + 16 * half) * (size_t)H + (size_t)h) * (size_t)L;
+      const __amdgpu_buffer_rsrc_t rg = make_rsrc(gy + r0);
+      const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + r0);
       const uint32_t o = (erow[i] < klim && ecol[i] < L)
-                             ? (uint32_t)erow[i] * row_bytes + 4u * (uint32_t)ecol[i]
+                             ? (uint32_t)(erow[i] - 16 * half) * row_bytes + 4u * (uint32_t)ecol[i]
                              : kOob;
       if constexpr (VEC) {
         stv[0][i] = buf_load_chunk<kCpolNT>(rg, o);
@@ -2806,6 +2825,7 @@ __global__ __launch_bounds__((LMAX / 16) * kWave) void dwconv_dk_long_s3_kernel(
       }
     }
   };
+
   // Rows are 8-byte aligned (RS even): 16-byte chunks go in as two halves.
   auto store_stage = [&](int buf) {
 #pragma unroll
@@ -2924,5 +2944,178 @@ __global__ __launch_bounds__((LMAX / 16) * kWave) void dwconv_dk_long_s3_kernel(
       atomicAdd(dst + (size_t)h * K + j, v);
   }
 }
+
+
+// ---------------------------------------------------------------------------
+// Long rows: DK on the BF16 matrix cores with operands loaded in place.
+// The contraction of the kernel above, without the FP32 staging: in step s
+// (32 samples) lane (g, c) of wave a loads dy and x at column 16 a + c of
+// samples 4 i + g, i = 0 .. 7, straight from HBM with dword loads (each
+// instruction reads four 64-byte row pieces), which is the operand layout of
+// v_mfma_f32_16x16x32_bf16 with the K index 8 g + i standing for sample
+// 4 i + g (the same permutation on both operands, so D = dyᵀx is unchanged).
+// The wave splits its values once: the dy parts stay in registers as its A
+// operands, the x parts go to a double-buffered publication in LDS as the B
+// operands of every wave whose tile row meets column tile a. One barrier per
+// step: a publication buffer is written again two steps later, after every
+// wave has passed the barrier that follows its reads. Loads run two steps
+// ahead in registers, with the default cache policy (each 128-byte line is
+// read by two waves; non-temporal loads measured 10% slower here). Buffer
+// bases sit at sample 0 and 16 of the step, so a byte offset spans at most 16
+// rows, and each buffer ends at the tensor's last byte, so samples past the
+// batch read zero with no per-load mask. Against the staged kernel the split
+// goes from every wave's gather of a stage to its own registers, LDS holds
+// only the publication (74 KB at LMAX = 192 against 148 KB), and a step has
+// one barrier instead of two.
+// Measured and not kept (MI355X, L = K = 192): two tiles' accumulation
+// chains interleaved (-1.5% time, +18 VGPRs, slower at K = 96); the next
+// tile's parts read before this tile's MFMAs (+3%, 164 VGPRs); producer and
+// consumer waves (4 producers split x for 12 consumers: +10%).
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr size_t dk_long_s3r_lds_bytes(int lmax) {
+  // publication [2][3 parts][LMAX / 16][64] bf16x8; the epilogue reuses it
+  return (size_t)2 * 3 * (lmax / 16) * 64 * 8 * sizeof(__bf16);
+}
+
+template <int LMAX>
+__global__ __launch_bounds__((LMAX / 16) * kWave) void dwconv_dk_long_s3r_kernel(
+    const float* __restrict__ gy, const float* __restrict__ x,
+    float* __restrict__ dst, int B, int H, int L, int K, int nranges, int det) {
+  constexpr int NT = LMAX / 16;
+  constexpr int NTH = NT * kWave;
+  constexpr int PUB = 3 * NT * 64;          // bf16x8 per publication buffer
+  constexpr int AREA = 2 * PUB * 4;         // floats of the whole area
+  constexpr int DS = LMAX + 1;              // epilogue D-row stride
+  constexpr int PART = NT * kLongMaxK;      // epilogue tap sums (floats)
+  constexpr int kRound = (AREA - PART) / (16 * DS);  // waves per epilogue round
+  static_assert(kRound >= 1, "the area holds one wave's D rows and the tap sums");
+  extern __shared__ float lds[];
+  bf16x8* const pub = reinterpret_cast<bf16x8*>(lds);  // [2][3][NT][64]
+  float* const part = lds + AREA - PART;               // [NT][kLongMaxK]
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int a = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // tile row
+  const int h = (int)(blockIdx.x % (uint32_t)H);
+  const int r = (int)(blockIdx.x / (uint32_t)H);
+  const int tsteps = (B + 31) / 32;
+  const int nsteps = r < tsteps ? (tsteps - 1 - r) / nranges + 1 : 0;
+  const int p = K >> 1;
+  const uint32_t row_bytes = (uint32_t)H * (uint32_t)L * 4u;
+  const int g = lane >> 4, col = lane & 15;
+  const int c = 16 * a + col;  // this lane's column
+  // Byte offset of sample 4 i + g (i < 4) from the base of its half-step,
+  // out of bounds past the row. Samples past the batch are out of bounds
+  // through the buffer's size: it ends at the tensor's last byte.
+  uint32_t voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    voff[i] = c < L ? (uint32_t)(4 * i + g) * row_bytes + 4u * (uint32_t)c : kOob;
+  const long long total = (long long)B * H * L;
+
+  float vy[2][8], vx[2][8];
+  auto load_step = [&](int s, float (&ty)[8], float (&tx)[8]) {
+    const int bs = (r + s * nranges) * 32;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const long long r0 = ((long long)(bs + 16 * half) * H + h) * L;
+      const long long rem = total - r0;
+      const int nrec = rem <= 0 ? 0 : (int)min(4 * rem, (long long)kNumRecords);
+      const __amdgpu_buffer_rsrc_t rg = make_rsrc_n(gy + r0, nrec);
+      const __amdgpu_buffer_rsrc_t rx = make_rsrc_n(x + r0, nrec);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ty[4 * half + i] = buf_load1<kCpolNone>(rg, voff[i], 0);
+        tx[4 * half + i] = buf_load1<kCpolNone>(rx, voff[i], 0);
+      }
+    }
+  };
+  bf16x8 ah, am, al;  // this wave's A operands (dy parts) of the current step
+  auto publish = [&](int buf, const float (&ty)[8], const float (&tx)[8]) {
+    split3_bf16x8(ty, ah, am, al);
+    bf16x8 xh, xm, xl;
+    split3_bf16x8(tx, xh, xm, xl);
+    pub[((3 * buf + 0) * NT + a) * 64 + lane] = xh;
+    pub[((3 * buf + 1) * NT + a) * 64 + lane] = xm;
+    pub[((3 * buf + 2) * NT + a) * 64 + lane] = xl;
+  };
+  auto in_band = [&](int bb) {
+    const int lo = 16 * (bb - a) - 15;
+    return lo + 30 >= -p && lo <= K - 1 - p && 16 * bb < L && 16 * a < L;
+  };
+  f32x4 acc[NT];
+#pragma unroll
+  for (int bb = 0; bb < NT; ++bb) acc[bb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto mfma_step = [&](int buf) {
+    const bf16x8* const q = pub + 3 * buf * NT * 64 + lane;
+#pragma unroll
+    for (int bb = 0; bb < NT; ++bb) {
+      if (in_band(bb)) {
+        const bf16x8 bh = q[(0 * NT + bb) * 64], bm = q[(1 * NT + bb) * 64], bl = q[(2 * NT + bb) * 64];
+        acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc[bb], 0, 0, 0);
+        acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bm, acc[bb], 0, 0, 0);
+        acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bh, acc[bb], 0, 0, 0);
+        acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bm, acc[bb], 0, 0, 0);
+        acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc[bb], 0, 0, 0);
+        acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc[bb], 0, 0, 0);
+      }
+    }
+  };
+
+  // Steps run in pairs and every step issues the same loads (an odd count
+  // gets one more step, and loads past the last step are all out of bounds:
+  // zeros, no memory access, and zero products leave the sums unchanged),
+  // so on every path the wait before a step's use is for the loads issued
+  // before the next step's, not for those too.
+  if (nsteps > 0) {
+    load_step(0, vy[0], vx[0]);
+    load_step(1, vy[1], vx[1]);
+    for (int s0 = 0; s0 < nsteps; s0 += 2) {
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        publish(d, vy[d], vx[d]);
+        load_step(s0 + d + 2, vy[d], vx[d]);
+        __syncthreads();  // every wave's x parts of step s0 + d published
+        mfma_step(d);
+      }
+    }
+  }
+  __syncthreads();  // the last step's publication is read before reuse
+
+  // Epilogue rounds: waves [q, q + kRound) put their D rows in the area
+  // (slot a - q), then sum their diagonals in order of t.
+  for (int q = 0; q < NT; q += kRound) {
+    const bool mine = a >= q && a < q + kRound;
+    float* const blk = lds + (mine ? a - q : 0) * 16 * DS;
+    if (mine) {
+#pragma unroll
+      for (int bb = 0; bb < NT; ++bb)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) blk[(4 * g + rr) * DS + 16 * bb + col] = acc[bb][rr];
+    }
+    __syncthreads();
+    if (mine) {
+      for (int jb = 0; jb < K; jb += kWave) {
+        const int j = jb + lane;
+        float v = 0.0f;
+        for (int tr = 0; tr < 16; ++tr) {
+          const int t = 16 * a + tr;
+          const int sc = t + j - p;
+          if (j < K && t < L && sc >= 0 && sc < L) v += blk[tr * DS + sc];
+        }
+        if (j < K) part[a * kLongMaxK + j] = v;
+      }
+    }
+    __syncthreads();
+  }
+  for (int j = threadIdx.x; j < K; j += NTH) {
+    float v = 0.0f;
+    for (int aa = 0; aa < NT; ++aa) v += part[aa * kLongMaxK + j];
+    if (det)
+      dst[((size_t)h * K + j) * (size_t)nranges + r] = v;
+    else
+      atomicAdd(dst + (size_t)h * K + j, v);
+  }
+}
+
 
 }  // namespace pt

@@ -83,6 +83,7 @@ extern const RowsLongFn kRowsLongS3TableVec[2][kNumLongLB][kNumLongS3KB];
 extern const size_t kRowsLongS3Lds[2][kNumLongLB][kNumLongS3KB];
 extern const DkLongFn kDkLongTable[2][kNumLongLB];
 extern const DkLongFn kDkLongS3Table[2][kNumLongLB];
+extern const DkLongFn kDkLongS3RTable[kNumLongLB];
 extern const DkBf16Fn kDkBf16mmaTable[3];
 extern const DkBf16Fn kDkBf16mmaTableNT[3];
 

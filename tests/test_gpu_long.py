@@ -252,6 +252,34 @@ def test_long_rows_reference_benchmark_shape(rt):
     assert abs(lhs - rhs) <= 1e-5 * float((gk.double().cpu().abs() * v.abs()).sum())
 
 
+@pytest.mark.parametrize("shape", [(32, 160000, 192, 48), (32, 340000, 96, 48)],
+                         ids=lambda s: "B{}H{}L{}K{}".format(*s))
+def test_long_dk_step_spans_more_than_2gib(rt, shape, monkeypatch):
+    """A 32-sample step of the split DK whose rows span more than 2 GiB
+    (from sample 17 of a step on at these shapes, a row starts 2^31 bytes or
+    more past sample 0's): with one buffer base per step those samples would
+    read as zero. Both split kernels (in place from row bucket 128, staged
+    below) against FP64 sums on the GPU, per channel block."""
+    monkeypatch.setenv("PATHTILE_LONG_ALGO", "split")
+    B, H, L, K = shape
+    print(f"[case] long split DK past 2 GiB B={B} H={H} L={L} K={K}", flush=True)
+    assert 16 * H * L * 4 < 2 ** 31 <= 31 * H * L * 4
+    gen = torch.Generator(device="cuda").manual_seed(77)
+    x = torch.randn(B, H, L, device="cuda", generator=gen)
+    dy = torch.randn(B, H, L, device="cuda", generator=gen)
+    gk = torch.full((H, K), float("nan"), device="cuda")
+    rt.launch_bwd_weight_long(dy, x, gk, K)
+    p = K // 2
+    ref = torch.empty(H, K, dtype=torch.float64, device="cuda")
+    for h0 in range(0, H, 16384):
+        xs = torch.nn.functional.pad(x[:, h0:h0 + 16384].double(), (p, K - 1 - p))
+        ds = dy[:, h0:h0 + 16384].double()
+        for j in range(K):
+            ref[h0:h0 + 16384, j] = (ds * xs[:, :, j:j + L]).sum(dim=(0, 2))
+    err = (gk.double() - ref).abs().max() / ref.abs().max()
+    assert float(err) < DK_TOL
+
+
 def test_long_rows_misaligned_tensors_take_the_dword_path(rt):
     """L % 4 == 0 but a 4-byte aligned (not 16-byte) view: the dword-move
     kernel serves it, with the same results as the aligned call."""
