@@ -657,7 +657,8 @@ def extras(rt, args, dev, stream, x, w, dy, y, gk) -> dict:
         out["channels_last_dk"] = {
             "ms": round(t["dk"]["ms"], 5), "std_ms": round(t["dk"]["std_ms"], 5),
             "gbps": round(gb, 1), "pct_peak": round(100 * gb / PEAK_HBM_GBPS, 2),
-            "kernel": f"dwconv_dk_cl_kernel<{16 * ((L + 15) // 16)}>",
+            "kernel": ("dwconv_dk_cl_kernel<48, 4, 2>" if L > 32
+                       else f"dwconv_dk_cl_kernel<{16 * ((L + 15) // 16)}>"),
             "gate_vs_row_major": float(f"{cl_gate:.3e}"),
             "note": "flash_dk_fp32, x/dY [B,1,L,H], GZ=1"}
         del xc, dyc, dwc

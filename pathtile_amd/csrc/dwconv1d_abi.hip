@@ -967,16 +967,17 @@ static int bf16_dk_launch(bool det, const void* gy, const void* x, float* dst,
   return launch((const void*)fn, nblocks, (uint32_t)threads, lds, stream, args);
 }
 
-// Channels-last DK: 32-channel workgroups of 16 waves, one resident pass of
-// them over the GPU (the sample ranges are the resident workgroups per
+// Channels-last DK: 32-channel workgroups (16 waves of two channels, or 8
+// of four at 48 columns), one resident pass of them over the GPU (the sample ranges are the resident workgroups per
 // channel group, rounded down so no workgroup waits for a second round),
 // at most one range per 4-sample step.
 static int dk_cl_launch(const float* x, const float* dy, float* dw, int B,
                         int H, int L, int K, void* stream) {
   const DkClFn fn = kDkClTable[mfma_index(L)];
-  const size_t lds = dk_cl_lds_bytes(16 * (mfma_index(L) + 1), L);
+  const int nw = dk_cl_waves(16 * (mfma_index(L) + 1));
+  const size_t lds = dk_cl_lds_bytes(16 * (mfma_index(L) + 1), L, nw);
   if (lds > (size_t)max_lds_per_block()) return PT_ERR_CONFIG;
-  const int threads = kClWaves * kWave;
+  const int threads = nw * kWave;
   const long long ngroups = (long long)H / kClChannels;
   const long long tsteps = ((long long)B + kCgStep - 1) / kCgStep;
   const long long slots = (long long)num_cus() * blocks_per_cu((const void*)fn, threads, lds);

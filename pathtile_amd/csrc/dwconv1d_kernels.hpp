@@ -1968,9 +1968,8 @@ __global__ __launch_bounds__(512) void dwconv_dk_bf16mma_kernel(
 // zeroes dw first).
 //
 // The channel-group contraction above with the staging transposed: a
-// workgroup owns kClChannels = 32 consecutive channels (16 waves of two),
-// so each (sample, t) row it loads is one whole 128-byte line of 32
-// channels. Rows land in LDS as [sample][t][kClChannels + 1]: a lane that
+// workgroup owns kClChannels = 32 consecutive channels (CPW per wave), so
+// each (sample, t) row it loads is one whole 128-byte line of 32 channels. Rows land in LDS as [sample][t][kClChannels + 1]: a lane that
 // gathers column t of channel c reads address t * 33 + c, so the 16 columns
 // of a tile hit 16 distinct banks, and the sample stride is padded to
 // 16 (mod 32) floats so the four 16-lane groups of a wave (four samples)
@@ -1979,6 +1978,17 @@ __global__ __launch_bounds__(512) void dwconv_dk_bf16mma_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kClChannels = 32;
 constexpr int kClWaves = kClChannels / kCgChannelsPerWave;  // 16
+// At 48 columns a wave takes four channels (8 waves, 226-250 VGPRs at two
+// waves per SIMD), which leaves registers for two steps of loads: measured
+// on MI355X 141.5 against 148.8 us at B16384 H128 K48 and 605 against 624
+// us at B32768 H256 K4; at 16 and 32 columns it was 10-15% slower, so two
+// channels per wave stay there.
+constexpr int kClWideChannels = 4;
+
+// Waves of the channels-last DK workgroup of row bucket lmax.
+__host__ __device__ constexpr int dk_cl_waves(int lmax) {
+  return lmax > 32 ? kClChannels / kClWideChannels : kClWaves;
+}
 
 // Floats between the samples of a channels-last stage: L rows of
 // kClChannels + 1, rounded up to 16 (mod 32).
@@ -1986,26 +1996,26 @@ __host__ __device__ constexpr int cl_sample_stride(int L) {
   return L * (kClChannels + 1) + ((16 - (L * (kClChannels + 1)) % 32) % 32 + 32) % 32;
 }
 
-__host__ __device__ constexpr size_t dk_cl_lds_bytes(int lmax, int L) {
+__host__ __device__ constexpr size_t dk_cl_lds_bytes(int lmax, int L, int waves = kClWaves) {
   const size_t stages = (size_t)2 * 2 * kCgStep * (size_t)cl_sample_stride(L) * sizeof(float);
-  const size_t dtile = ((size_t)kClWaves * (16 * (lmax / 16)) * (16 * (lmax / 16) + 1) +
+  const size_t dtile = ((size_t)waves * (16 * (lmax / 16)) * (16 * (lmax / 16) + 1) +
                         (size_t)kClChannels * kMaxK) *
                        sizeof(float);
   return stages > dtile ? stages : dtile;
 }
 
-template <int LMAX>
-__global__ __launch_bounds__(kClWaves * kWave) void dwconv_dk_cl_kernel(
+template <int LMAX, int CPW = kCgChannelsPerWave, int DEPTH = 1>
+__global__ __launch_bounds__(kClChannels / CPW * kWave) void dwconv_dk_cl_kernel(
     const float* __restrict__ x, const float* __restrict__ gy,
     float* __restrict__ dw, int B, int H, int L, int K, int nranges,
     uint32_t nblocks) {
   using G = CgGeo<LMAX>;
   constexpr int NT = G::nt;
-  constexpr int CPW = kCgChannelsPerWave;
+  constexpr int NW = kClChannels / CPW;
   constexpr int HC = kClChannels;
   constexpr int RW = HC + 1;           // LDS floats per (sample, t) row
   constexpr int CPR = HC / 4;          // 16-byte chunks per row
-  constexpr int NTH = kClWaves * kWave;
+  constexpr int NTH = NW * kWave;
   constexpr int kNpt = (kCgStep * LMAX * CPR + NTH - 1) / NTH;
   extern __shared__ float lds[];
 
@@ -2039,8 +2049,8 @@ __global__ __launch_bounds__(kClWaves * kWave) void dwconv_dk_cl_kernel(
     elds[i] = (uint32_t)(k * sks + t * RW + 4 * q);
   }
 
-  u32x4 stg[2][kNpt];
-  auto load_step = [&](int s) {
+  u32x4 stg[DEPTH][2][kNpt];
+  auto load_step = [&](int s, u32x4 (&st)[2][kNpt]) {
     const int bs = (r + s * nranges) * kCgStep;
     const size_t r0 = (size_t)bs * (size_t)L * (size_t)H;
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(gy + r0);
@@ -2049,19 +2059,19 @@ __global__ __launch_bounds__(kClWaves * kWave) void dwconv_dk_cl_kernel(
 #pragma unroll
     for (int i = 0; i < kNpt; ++i) {
       const uint32_t o = ek[i] < klim ? eoff[i] : kOob;
-      stg[0][i] = buf_load_chunk<kCpolNT>(rg, o);
-      stg[1][i] = buf_load_chunk<kCpolNT>(rx, o);
+      st[0][i] = buf_load_chunk<kCpolNT>(rg, o);
+      st[1][i] = buf_load_chunk<kCpolNT>(rx, o);
     }
   };
-  auto store_stage = [&](int buf) {
+  auto store_stage = [&](int buf, const u32x4 (&st)[2][kNpt]) {
     float* base = lds + buf * 2 * sz;
 #pragma unroll
     for (int i = 0; i < kNpt; ++i) {
       if (ek[i] < kCgStep) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          base[elds[i] + v] = __uint_as_float(stg[0][i][v]);
-          base[sz + elds[i] + v] = __uint_as_float(stg[1][i][v]);
+          base[elds[i] + v] = __uint_as_float(st[0][i][v]);
+          base[sz + elds[i] + v] = __uint_as_float(st[1][i][v]);
         }
       }
     }
@@ -2107,13 +2117,13 @@ __global__ __launch_bounds__(kClWaves * kWave) void dwconv_dk_cl_kernel(
     }
   };
 
-  if (nsteps > 0) {
+  if (nsteps > 0 && DEPTH == 1) {
     // Local step s is loaded into stg, stored to LDS stage s % 2 while step
     // s - 1 is consumed from the other stage, and consumed after the next
     // barrier; the loop is unrolled by 2 so the stage index is static.
-    load_step(0);
-    store_stage(0);
-    if (1 < nsteps) load_step(1);
+    load_step(0, stg[0]);
+    store_stage(0, stg[0]);
+    if (1 < nsteps) load_step(1, stg[0]);
     __syncthreads();
     for (int s0 = 0; s0 < nsteps; s0 += 2) {
 #pragma unroll
@@ -2125,17 +2135,36 @@ __global__ __launch_bounds__(kClWaves * kWave) void dwconv_dk_cl_kernel(
           // and issue the loads of s + 2 before this step's matrix work
           // (1-2% faster than after it at every shape measured).
           if (s + 1 < nsteps) {
-            store_stage(d ^ 1);
-            if (s + 2 < nsteps) load_step(s + 2);
+            store_stage(d ^ 1, stg[0]);
+            if (s + 2 < nsteps) load_step(s + 2, stg[0]);
           }
           mfma_step(d);
           __syncthreads();
         }
       }
     }
+  } else if (nsteps > 0) {
+    // Two steps of loads in registers. Every step issues the same loads
+    // (past the last step all out of bounds: no memory traffic), so the wait
+    // before a stage store is for that step's loads only.
+    load_step(0, stg[0]);
+    load_step(1, stg[DEPTH - 1]);
+    store_stage(0, stg[0]);
+    load_step(2, stg[0]);
+    __syncthreads();
+    for (int s0 = 0; s0 < nsteps; s0 += 2) {
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const int s = s0 + d;
+        store_stage(d ^ 1, stg[(d + 1) % DEPTH]);
+        load_step(s + 3, stg[(d + 1) % DEPTH]);
+        if (s < nsteps) mfma_step(d);
+        __syncthreads();
+      }
+    }
   }
 
-  dk_cg_epilogue<LMAX, true>(acc, lds, dw, wave, kClWaves, g, r, HC, L, K, nranges, 0, H);
+  dk_cg_epilogue<LMAX, true, CPW>(acc, lds, dw, wave, NW, g, r, HC, L, K, nranges, 0, H);
 }
 
 // ---------------------------------------------------------------------------
