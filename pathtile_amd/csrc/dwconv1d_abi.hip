@@ -1038,7 +1038,7 @@ static bool long_dk_split(int L, int K) {
 // L192 K192 790 / 858, L192 K96 640 / 703, L128 K64 382 / 452; L96 K48
 // 337 / 301, L64 K64 215 / 181, L64 K16 213 / 169 (short rows give a
 // wave's 64-byte row pieces too little work to hide their latency).
-static bool long_dk_in_place(int li) { return long_lmax(li) >= 128; }
+static bool long_dk_in_place(int li) { return li >= kNumLongDkStagedLB; }
 
 static int rows_long_path(bool dx, const float* in, const float* w, float* out,
                           int B, int H, int L, int K, void* stream) {
@@ -1495,12 +1495,15 @@ int pt_dwconv1d_dk_long_f32(const float* dy, const float* x, float* dk,
   const bool vec = L % 4 == 0 && pt::aligned(dy, 16) && pt::aligned(x, 16);
   const bool split = pt::long_dk_split(L, K);
   if (split && pt::long_dk_in_place(li))
-    st = pt::launch((const void*)pt::kDkLongS3RTable[li], (uint32_t)nb, (uint32_t)((lmax / 16) * pt::kWave),
+    st = pt::launch((const void*)pt::kDkLongS3RTable[li - pt::kNumLongDkStagedLB], (uint32_t)nb,
+                    (uint32_t)((lmax / 16) * pt::kWave),
                     pt::dk_long_s3r_lds_bytes(lmax), stream, args);
+  else if (split)
+    st = pt::launch((const void*)pt::kDkLongS3Table[vec ? 1 : 0][li], (uint32_t)nb,
+                    (uint32_t)((lmax / 16) * pt::kWave), pt::dk_long_s3_lds_bytes(lmax), stream, args);
   else
-    st = pt::launch((const void*)(split ? pt::kDkLongS3Table : pt::kDkLongTable)[vec ? 1 : 0][li],
-                    (uint32_t)nb, (uint32_t)((lmax / 16) * pt::kWave),
-                    split ? pt::dk_long_s3_lds_bytes(lmax) : pt::dk_long_lds_bytes(lmax), stream, args);
+    st = pt::launch((const void*)pt::kDkLongTable[vec ? 1 : 0][li], (uint32_t)nb,
+                    (uint32_t)((lmax / 16) * pt::kWave), pt::dk_long_lds_bytes(lmax), stream, args);
   if (st != PT_OK) return st;
   int ncoef = H * K;
   int nbt = nranges;

@@ -82,8 +82,11 @@ extern const RowsLongFn kRowsLongS3Table[2][kNumLongLB][kNumLongS3KB];
 extern const RowsLongFn kRowsLongS3TableVec[2][kNumLongLB][kNumLongS3KB];
 extern const size_t kRowsLongS3Lds[2][kNumLongLB][kNumLongS3KB];
 extern const DkLongFn kDkLongTable[2][kNumLongLB];
-extern const DkLongFn kDkLongS3Table[2][kNumLongLB];
-extern const DkLongFn kDkLongS3RTable[kNumLongLB];
+// Split DK: staged for row buckets 64 and 96 ([16-byte staging][bucket]),
+// operands in place for 128, 160 and 192 ([bucket - 2]).
+constexpr int kNumLongDkStagedLB = 2;
+extern const DkLongFn kDkLongS3Table[2][kNumLongDkStagedLB];
+extern const DkLongFn kDkLongS3RTable[kNumLongLB - kNumLongDkStagedLB];
 extern const DkBf16Fn kDkBf16mmaTable[3];
 extern const DkBf16Fn kDkBf16mmaTableNT[3];
 

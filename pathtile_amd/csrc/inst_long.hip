@@ -26,14 +26,12 @@ const DkLongFn kDkLongTable[2][kNumLongLB] = {
     {&dwconv_dk_long_kernel<64, false>, &dwconv_dk_long_kernel<96, false>, &dwconv_dk_long_kernel<128, false>, &dwconv_dk_long_kernel<160, false>, &dwconv_dk_long_kernel<192, false>},
     {&dwconv_dk_long_kernel<64, true>, &dwconv_dk_long_kernel<96, true>, &dwconv_dk_long_kernel<128, true>, &dwconv_dk_long_kernel<160, true>, &dwconv_dk_long_kernel<192, true>},
 };
-// DK on the BF16 matrix cores with split operands: [16-byte staging][row bucket]
-const DkLongFn kDkLongS3Table[2][kNumLongLB] = {
-    {&dwconv_dk_long_s3_kernel<64, false>, &dwconv_dk_long_s3_kernel<96, false>, &dwconv_dk_long_s3_kernel<128, false>, &dwconv_dk_long_s3_kernel<160, false>, &dwconv_dk_long_s3_kernel<192, false>},
-    {&dwconv_dk_long_s3_kernel<64, true>, &dwconv_dk_long_s3_kernel<96, true>, &dwconv_dk_long_s3_kernel<128, true>, &dwconv_dk_long_s3_kernel<160, true>, &dwconv_dk_long_s3_kernel<192, true>},
+// Split DK, staged (row buckets 64 and 96): [16-byte staging][bucket]
+const DkLongFn kDkLongS3Table[2][kNumLongDkStagedLB] = {
+    {&dwconv_dk_long_s3_kernel<64, false>, &dwconv_dk_long_s3_kernel<96, false>},
+    {&dwconv_dk_long_s3_kernel<64, true>, &dwconv_dk_long_s3_kernel<96, true>},
 };
-// DK on the BF16 matrix cores, operands loaded in place: [row bucket]
-// (buckets 64 and 96 take the staged kernel; their entries are unused)
-const DkLongFn kDkLongS3RTable[kNumLongLB] = {
-    &dwconv_dk_long_s3r_kernel<64>, &dwconv_dk_long_s3r_kernel<96>, &dwconv_dk_long_s3r_kernel<128>,
-    &dwconv_dk_long_s3r_kernel<160>, &dwconv_dk_long_s3r_kernel<192>};
+// Split DK, operands loaded in place (row buckets 128, 160, 192)
+const DkLongFn kDkLongS3RTable[kNumLongLB - kNumLongDkStagedLB] = {
+    &dwconv_dk_long_s3r_kernel<128>, &dwconv_dk_long_s3r_kernel<160>, &dwconv_dk_long_s3r_kernel<192>};
 }  // namespace pt
