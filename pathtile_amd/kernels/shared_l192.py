@@ -1,36 +1,19 @@
-"""Drop-in for the reference's ``kernels/shared_l192.py`` API (long rows),
-on MI355X.
+"""Drop-in for the reference's long-row module ``kernels/shared_l192.py``
+(public surface as ``kernels/warp_tiled.py``, ``__all__`` at :1020-1031;
+benchmarked at B16384 H128 L192 K192, benchmark/benchmark_gmc_vs_shared_l192.py:14-17).
 
-The reference module is the shared-memory family's long-row variant, with
-the same public surface as ``kernels/warp_tiled.py`` (``__all__`` at
-kernels/shared_l192.py:1020-1031) and benchmarked at B16384 H128 L192 K192
-(benchmark/benchmark_gmc_vs_shared_l192.py:14-17). Here the same names run
-the hand-written gfx950 kernels of ``libpathtile_hip.so``:
+Rows and taps up to 48 take the specialised kernels; anything up to L = 192,
+K = 256 takes ``pt_dwconv1d_{fwd,dx,dk}_long_f32`` at FP32 accuracy, dK
+deterministic and written into ``gk`` (no zero-init, as the reference's
+one-thread-per-tap kernel writes it, :966-1001). Every launch is
+host-synchronous and appends its kernel time (ms) to ``FWD_TIMES`` /
+``BWD_IN_TIMES`` / ``BWD_K_TIMES`` (:741-780).
 
-* rows and taps up to 48: the specialised path (the FWD/dX kernels chosen
-  per shape, the deterministic two-pass dK);
-* anything up to L = 192, K = 256: the long-row matrix-core kernels
-  (``pt_dwconv1d_{fwd,dx,dk}_long_f32``), at FP32 accuracy (by default the
-  BF16 matrix cores on FP32 operands split three ways, six exact part
-  products summed in FP32; ``PATHTILE_LONG_ALGO=fp32`` selects the FP32
-  instructions), dK deterministic and written into ``gk`` as the
-  reference's dK kernel writes it (one thread per tap,
-  kernels/shared_l192.py:966-1001).
-
-Every launch is host-synchronous and its kernel time (ms, HIP events) is
-appended to ``FWD_TIMES`` / ``BWD_IN_TIMES`` / ``BWD_K_TIMES`` (:741-780).
-
-Differences from the reference, by design:
-
-* Importing this module needs no GPU (the reference raises at import
-  without CUDA, :15-18); CPU tensors raise
-  ``ValueError("x and kernel must be CUDA tensors")`` at the first call.
-* L is limited to 192 and K to 256 (``ValueError``); the reference's kernel
-  has no stated bound.
-* ``CudaContextGuard`` is a no-op and ``TorchCudaInterop.as_gpuarray``
-  validates and returns the tensor (no PyCUDA), as in the ``warp_tiled``
-  mirror. The launch constants and shared-memory helpers keep the
-  reference's values (BWD_K_B_TILE = 32 here, :118) as documented constants.
+Differences by design: importing needs no GPU (the reference raises at
+import without CUDA, :15-18; CPU tensors raise at the first call instead);
+L > 192 or K > 256 raise ``ValueError``; ``CudaContextGuard`` and
+``TorchCudaInterop`` are the no-PyCUDA shims of the ``warp_tiled`` mirror;
+the launch constants keep the reference's values (:109-118).
 """
 
 from __future__ import annotations
