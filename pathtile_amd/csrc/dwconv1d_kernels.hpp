@@ -148,11 +148,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float* base) {
                                            kNumRecords, kRsrcWord3);
 }
 
-// A buffer of nrec bytes from base: loads at offsets past it return zero.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_n(const float* base, int nrec) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, nrec, kRsrcWord3);
-}
-
 template <int CPOL = kCpolNone>
 __device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r,
                                             uint32_t voff, uint32_t soff) {
@@ -3048,7 +3043,7 @@ __global__ __launch_bounds__((LMAX / 16) * kWave) void dwconv_dk_long_s3r_kernel
     for (int half = 0; half < 2; ++half) {
       const long long r0 = ((long long)(bs + 16 * half) * H + h) * L;
       const long long rem = total - r0;
-      const int nrec = rem <= 0 ? 0 : (int)min(4 * rem, (long long)kNumRecords);
+      const uint32_t nrec = rem <= 0 ? 0u : (uint32_t)min(4 * rem, (long long)kNumRecords);
       const __amdgpu_buffer_rsrc_t rg = make_rsrc_n(gy + r0, nrec);
       const __amdgpu_buffer_rsrc_t rx = make_rsrc_n(x + r0, nrec);
 #pragma unroll
