@@ -295,3 +295,29 @@ def test_long_rows_misaligned_tensors_take_the_dword_path(rt):
     rt.launch_fwd_long(x.cuda(), w.cuda(), y2)
     assert torch.equal(y, y2)
     assert oracle.normalized_max_abs(y.cpu().numpy(), oracle.fwd_f64(x, w)) < FWD_TOL
+
+
+@pytest.mark.parametrize("shape", [(48, 4, 160, 48), (40, 3, 96, 48)], ids=lambda s: "B{}H{}L{}K{}".format(*s))
+def test_long_dk_misaligned_tensors_match_aligned(rt, shape, monkeypatch):
+    """Split DK on 4-byte aligned (not 16-byte) views: the in-place kernel
+    (bucket 160) loads dwords whatever the alignment, the staged one (bucket
+    96) takes its dword form; both give the aligned call's bits and stay
+    within 1e-4 of FP64."""
+    monkeypatch.setenv("PATHTILE_LONG_ALGO", "split")
+    B, H, L, K = shape
+    print(f"[case] long dK misaligned B={B} H={H} L={L} K={K}", flush=True)
+    x, _, dy = oracle.make_inputs(B, H, L, K, seed=21 + L)
+
+    def view(t):
+        buf = torch.empty(t.numel() + 1, device="cuda")
+        v = buf[1:].view(*t.shape)
+        v.copy_(t.cuda())
+        assert v.data_ptr() % 16 != 0
+        return v
+
+    g1 = torch.empty(H, K, device="cuda")
+    g2 = torch.empty(H, K, device="cuda")
+    rt.launch_bwd_weight_long(view(dy), view(x), g1, K)
+    rt.launch_bwd_weight_long(dy.cuda(), x.cuda(), g2, K)
+    assert torch.equal(g1, g2)
+    assert oracle.normalized_max_abs(g1.cpu().numpy(), oracle.dk_f64(dy, x, K)) < DK_TOL
